@@ -1,0 +1,480 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Fused softmax attention on gfx950 (head width 64), replacing the
+ * reference's gemm(Q K^T) -> softmax_rows -> gemm(P V) sequence
+ * (sam3_model.c:1000-1013) for windowed and global ViT blocks.
+ *
+ * Both kernels compute S^T = K Q^T and O^T = V^T P^T rather than S and O:
+ * in the 32 x 32 MFMA output layout a lane then holds one query (column
+ * l % 32) and 16 of its keys, so the row max / row sum need one exchange
+ * between lanes l and l ^ 32, the per-query rescale of O is a per-lane
+ * scalar, and P feeds the P V product straight from registers.
+ *
+ * Workgroup: 256 threads = 4 waves; each wave owns 32 queries, the
+ * workgroup 128 queries of one (window, head) unit (blockIdx.y). K and V
+ * blocks are staged through double-buffered LDS with the next block
+ * prefetched into registers while the current one is consumed. The
+ * online softmax keeps (m, l) per lane: m is the running max of the
+ * scaled scores, l the partial sum over the lane's keys; the halves are
+ * combined once at the end.
+ *
+ * MFMA 32x32 lane layouts (l = lane, h = l / 32):
+ *   A operand:  lane l holds A[l % 32][k-slice h]
+ *   B operand:  lane l holds B[k-slice h][l % 32]
+ *   D (16 f32): reg r of lane l is D[8 (r / 4) + 4 h + r % 4][l % 32]
+ */
+#include "k_common.h"
+
+/* ------------------------------------------------------------ fp32 path */
+
+/* fp32 operands in the reference row layout (Q/K/V/O opnds of
+ * sam3_model.c:1004-1011), v_mfma_f32_32x32x2_f32, 32-key blocks.
+ * RoPE and the scale are applied on the loads. The contraction index of
+ * Q K^T is ordered d = step + 32 h, so a lane's Q registers are one
+ * contiguous half row and RoPE pairs stay in one lane. */
+__global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
+{
+    __shared__ float Kt[2][64][33]; /* K^T block: [d][key] */
+    __shared__ float Vs[2][32][72]; /* V block:   [key][d] */
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
+              l32 = l & 31;
+    const int N = d.N;
+    const long b0 = blockIdx.y / d.nb1, b1 = blockIdx.y % d.nb1;
+    const float *Qb = (const float *)d.Q + d.qoff + b0 * d.sq0 + b1 * d.sq1;
+    const float *Kb = (const float *)d.K + d.koff + b0 * d.sk0 + b1 * d.sk1;
+    const float *Vb = (const float *)d.V + d.voff + b0 * d.sv0 + b1 * d.sv1;
+    const float2 *cs = (const float2 *)d.rope;
+    const int qi = blockIdx.x * 128 + w * 32 + l32;
+    const int nblk = (N + 31) / 32;
+    /* Loader role: key row kr of a block, 8 channels from dc. */
+    const int kr = t >> 3, dc = (t & 7) * 8;
+    float qreg[32], kpre[8], vpre[8];
+    f32x16 o0, o1;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    /* Q: lane holds channels 32 h .. 32 h + 31 of query qi, rotated and
+     * scaled. */
+    for (int i = 0; i < 32; i++)
+        qreg[i] = 0.0f;
+    if (qi < N) {
+        const float *qr = Qb + (long)qi * d.ldq + 32 * h;
+
+        for (int i = 0; i < 32; i++)
+            qreg[i] = qr[i];
+        if (cs) {
+            const float2 *rot = cs + (long)(qi % d.npos) * 32 + 16 * h;
+
+            for (int j = 0; j < 16; j++) {
+                const float a = qreg[2 * j], b = qreg[2 * j + 1];
+                const float2 r = rot[j];
+
+                qreg[2 * j] = fmaf(a, r.x, -(b * r.y));
+                qreg[2 * j + 1] = fmaf(a, r.y, b * r.x);
+            }
+        }
+    }
+    for (int r = 0; r < 16; r++) {
+        o0[r] = 0.0f;
+        o1[r] = 0.0f;
+    }
+
+    /* Global -> registers for block kb (RoPE on K), registers -> LDS. */
+    auto fetch = [&](int kb) {
+        const int key = kb * 32 + kr;
+
+        if (key < N) {
+            const float *kp = Kb + (long)key * d.ldk + dc;
+            const float *vp = Vb + (long)key * d.ldv + dc;
+
+            for (int e = 0; e < 8; e++) {
+                kpre[e] = kp[e];
+                vpre[e] = vp[e];
+            }
+            if (cs) {
+                const float2 *rot = cs + (long)(key % d.npos) * 32 + dc / 2;
+
+                for (int j = 0; j < 4; j++) {
+                    const float a = kpre[2 * j], b = kpre[2 * j + 1];
+                    const float2 r = rot[j];
+
+                    kpre[2 * j] = fmaf(a, r.x, -(b * r.y));
+                    kpre[2 * j + 1] = fmaf(a, r.y, b * r.x);
+                }
+            }
+        }
+        else
+            for (int e = 0; e < 8; e++) {
+                kpre[e] = 0.0f;
+                vpre[e] = 0.0f;
+            }
+    };
+    auto stage = [&](int buf) {
+        for (int e = 0; e < 8; e++) {
+            Kt[buf][dc + e][kr] = kpre[e];
+            Vs[buf][kr][dc + e] = vpre[e];
+        }
+    };
+
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int kb = 0; kb < nblk; kb++) {
+        const int buf = kb & 1;
+        f32x16 s;
+        float mx, m_new, corr, rs = 0.0f;
+
+        if (kb + 1 < nblk)
+            fetch(kb + 1);
+        for (int r = 0; r < 16; r++)
+            s[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < 32; st++)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[buf][st + 32 * h][l32],
+                                                     qreg[st], s, 0, 0, 0);
+        /* Scale, mask keys past N, online softmax. */
+        mx = -INFINITY;
+        for (int r = 0; r < 16; r++) {
+            const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+
+            s[r] = key < N ? s[r] * d.scale : -INFINITY;
+            mx = fmaxf(mx, s[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        m_new = fmaxf(m_run, mx);
+        corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E_F);
+        for (int r = 0; r < 16; r++) {
+            s[r] = __builtin_amdgcn_exp2f((s[r] - m_new) * LOG2E_F);
+            rs += s[r];
+        }
+        l_run = l_run * corr + rs;
+        m_run = m_new;
+        for (int r = 0; r < 16; r++) {
+            o0[r] *= corr;
+            o1[r] *= corr;
+        }
+        /* O^T += V^T P^T: step st contracts key 8 (st / 4) + 4 h + st % 4,
+         * the key of this lane's score register st. */
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int key = 8 * (st >> 2) + 4 * h + (st & 3);
+
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][l32], s[st],
+                                                      o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][32 + l32],
+                                                      s[st], o1, 0, 0, 0);
+        }
+        if (kb + 1 < nblk)
+            stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (qi < N) {
+        const float inv = 1.0f / l_run;
+        const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
+
+        for (int r = 0; r < 16; r++) {
+            const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+
+            if (d.odt == DT_F32) {
+                ((float *)d.O)[orow + dd] = o0[r] * inv;
+                ((float *)d.O)[orow + 32 + dd] = o1[r] * inv;
+            }
+            else {
+                ((uint16_t *)d.O)[orow + dd] = f2bf(o0[r] * inv);
+                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(o1[r] * inv);
+            }
+        }
+    }
+}
+
+extern "C" int launch_attn_f32(const attn_desc *d, void *stream)
+{
+    if (d->nb > 65535)
+        return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(k_attn_f32, dim3((d->N + 127) / 128, d->nb), dim3(256),
+                       0, (hipStream_t)stream, *d);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ packing */
+
+/* fp32 reference-layout Q/K/V -> packed bf16 of the fast path, 64 rows
+ * of one unit per workgroup: q16/k16 [unit][Np][64] with RoPE applied
+ * (q also scaled), vt16 [unit][64][Np] transposed through LDS; rows past
+ * N are zero. */
+__global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
+                                                  uint16_t *__restrict__ q16,
+                                                  uint16_t *__restrict__ k16,
+                                                  uint16_t *__restrict__ vt16,
+                                                  int Np)
+{
+    __shared__ uint16_t Vl[64][66];
+    const int t = threadIdx.x, row = t >> 2, ds = (t & 3) * 16;
+    const int unit = blockIdx.y, i = blockIdx.x * 64 + row;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+    const float2 *cs = (const float2 *)d.rope;
+    float q[16], k[16], v[16];
+
+    if (i < d.N) {
+        const float *qr = (const float *)d.Q + d.qoff + b0 * d.sq0 +
+                          b1 * d.sq1 + (long)i * d.ldq + ds;
+        const float *kr = (const float *)d.K + d.koff + b0 * d.sk0 +
+                          b1 * d.sk1 + (long)i * d.ldk + ds;
+        const float *vr = (const float *)d.V + d.voff + b0 * d.sv0 +
+                          b1 * d.sv1 + (long)i * d.ldv + ds;
+
+        for (int e = 0; e < 16; e++) {
+            q[e] = qr[e];
+            k[e] = kr[e];
+            v[e] = vr[e];
+        }
+        if (cs) {
+            const float2 *rot = cs + (long)(i % d.npos) * 32 + ds / 2;
+
+            for (int j = 0; j < 8; j++) {
+                const float2 r = rot[j];
+                float a = q[2 * j], b = q[2 * j + 1];
+
+                q[2 * j] = fmaf(a, r.x, -(b * r.y));
+                q[2 * j + 1] = fmaf(a, r.y, b * r.x);
+                a = k[2 * j];
+                b = k[2 * j + 1];
+                k[2 * j] = fmaf(a, r.x, -(b * r.y));
+                k[2 * j + 1] = fmaf(a, r.y, b * r.x);
+            }
+        }
+        for (int e = 0; e < 16; e++)
+            q[e] *= d.scale;
+    }
+    else
+        for (int e = 0; e < 16; e++) {
+            q[e] = 0.0f;
+            k[e] = 0.0f;
+            v[e] = 0.0f;
+        }
+    {
+        const long o = ((long)unit * Np + i) * 64 + ds;
+        u32x4 a, b;
+
+        for (int e = 0; e < 4; e++) {
+            a[e] = pack_bf16x2(q[2 * e], q[2 * e + 1]);
+            b[e] = pack_bf16x2(q[8 + 2 * e], q[8 + 2 * e + 1]);
+        }
+        *(u32x4 *)(q16 + o) = a;
+        *(u32x4 *)(q16 + o + 8) = b;
+        for (int e = 0; e < 4; e++) {
+            a[e] = pack_bf16x2(k[2 * e], k[2 * e + 1]);
+            b[e] = pack_bf16x2(k[8 + 2 * e], k[8 + 2 * e + 1]);
+        }
+        *(u32x4 *)(k16 + o) = a;
+        *(u32x4 *)(k16 + o + 8) = b;
+    }
+    for (int e = 0; e < 16; e++)
+        Vl[ds + e][row] = f2bf(v[e]);
+    __syncthreads();
+    {
+        /* Thread t writes channel t / 4, keys 16 (t % 4) .. +15. */
+        const int dd = t >> 2, k0 = (t & 3) * 16;
+        uint16_t *dst = vt16 + ((long)unit * 64 + dd) * Np + blockIdx.x * 64 + k0;
+
+        for (int e = 0; e < 16; e++)
+            dst[e] = Vl[dd][k0 + e];
+    }
+}
+
+extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
+                               void *vt16, void *stream)
+{
+    const int Np = (d->N + 63) / 64 * 64;
+
+    if (d->nb > 65535)
+        return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(k_qkv_pack, dim3(Np / 64, d->nb), dim3(256), 0,
+                       (hipStream_t)stream, *d, (uint16_t *)q16,
+                       (uint16_t *)k16, (uint16_t *)vt16, Np);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ bf16 path */
+
+/* Row of the K block feeding A-operand row i: bits 2 and 3 of i swapped.
+ * The S^T register r of lane half h then holds key
+ * 32 c + 16 (r / 8) + 8 h + r % 8, so registers 8a .. 8a + 7 are eight
+ * consecutive keys: the B operand of the P V product for keys
+ * 16 (2c + a) + 8 h .. +7 without any data movement. */
+__device__ __forceinline__ int kperm(int i)
+{
+    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+/* Lazy rescale threshold: the running max is only moved (and O, l
+ * rescaled) when a new score exceeds it by more than 8 ln 2, so P stays
+ * below 2^8; the final O / l is unchanged in exact arithmetic. */
+#define RESCALE_TH 5.545177444479562f
+
+/* Packed bf16 operands (k_qkv_pack layout), v_mfma_f32_32x32x16_bf16 with
+ * f32 accumulation, 64-key blocks. LDS: K block [key][d] and V^T block
+ * [d][key], rows of 72 bf16 (144 B). */
+__global__ __launch_bounds__(256) void k_attn_bf16(attn_desc d,
+                                                   const uint16_t *__restrict__ q16,
+                                                   const uint16_t *__restrict__ k16,
+                                                   const uint16_t *__restrict__ vt16)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][72];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][72];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
+              l32 = l & 31;
+    const int N = d.N, Np = (N + 63) / 64 * 64, nblk = Np / 64;
+    const long unit = blockIdx.y;
+    const uint16_t *Qu = q16 + unit * Np * 64;
+    const uint16_t *Ku = k16 + unit * Np * 64;
+    const uint16_t *Vu = vt16 + unit * 64 * Np;
+    const int qi = blockIdx.x * 128 + w * 32 + l32;
+    const int krow = kperm(l32);
+    bf16x8 qb[4];
+    u32x4 kpre[2], vpre[2];
+    f32x16 o0, o1;
+    float m_run = -INFINITY, l_run = 0.0f;
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+    for (int s = 0; s < 4; s++) {
+        if (qi < Np)
+            qb[s] = *(const bf16x8 *)(Qu + (long)qi * 64 + 16 * s + 8 * h);
+        else
+            for (int e = 0; e < 8; e++)
+                qb[s][e] = (__bf16)0.0f;
+    }
+    for (int r = 0; r < 16; r++) {
+        o0[r] = 0.0f;
+        o1[r] = 0.0f;
+    }
+
+    auto fetch = [&](int kb) {
+        for (int j = 0; j < 2; j++) {
+            const int c = t + 256 * j, row = c >> 3, ch = (c & 7) * 8;
+
+            kpre[j] = *(const u32x4 *)(Ku + ((long)kb * 64 + row) * 64 + ch);
+            vpre[j] = *(const u32x4 *)(Vu + (long)row * Np + kb * 64 + ch);
+        }
+    };
+    auto stage = [&](int buf) {
+        for (int j = 0; j < 2; j++) {
+            const int c = t + 256 * j, row = c >> 3, ch = (c & 7) * 8;
+
+            *(u32x4 *)&Ks[buf][row][ch] = kpre[j];
+            *(u32x4 *)&Vt[buf][row][ch] = vpre[j];
+        }
+    };
+
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int kb = 0; kb < nblk; kb++) {
+        const int buf = kb & 1;
+        f32x16 s0, s1;
+        float mx = -INFINITY, m_new, mc;
+        bf16x8 pb[4];
+
+        if (kb + 1 < nblk)
+            fetch(kb + 1);
+        for (int r = 0; r < 16; r++) {
+            s0[r] = 0.0f;
+            s1[r] = 0.0f;
+        }
+#pragma unroll
+        for (int ds = 0; ds < 4; ds++) {
+            const bf16x8 a0 = *(const bf16x8 *)&Ks[buf][krow][16 * ds + 8 * h];
+            const bf16x8 a1 = *(const bf16x8 *)&Ks[buf][32 + krow][16 * ds + 8 * h];
+
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qb[ds], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qb[ds], s1, 0, 0, 0);
+        }
+        if (kb * 64 + 64 > N) {
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
+
+                if (key >= N)
+                    s0[r] = -INFINITY;
+                if (key + 32 >= N)
+                    s1[r] = -INFINITY;
+            }
+        }
+        for (int r = 0; r < 16; r++)
+            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        m_new = fmaxf(m_run, mx);
+        if (__ballot(m_new - m_run > RESCALE_TH) != 0) {
+            const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E_F);
+
+            l_run *= corr;
+            for (int r = 0; r < 16; r++) {
+                o0[r] *= corr;
+                o1[r] *= corr;
+            }
+            m_run = m_new;
+        }
+        mc = m_run * LOG2E_F;
+        for (int r = 0; r < 16; r++) {
+            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], LOG2E_F, -mc));
+            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], LOG2E_F, -mc));
+        }
+        for (int a = 0; a < 2; a++)
+            for (int e = 0; e < 8; e++) {
+                pb[a][e] = (__bf16)s0[8 * a + e];
+                pb[2 + a][e] = (__bf16)s1[8 * a + e];
+            }
+        for (int j = 0; j < 4; j++)
+            for (int e = 0; e < 4; e++) {
+                bf16x2 p2;
+
+                p2.x = pb[j][2 * e];
+                p2.y = pb[j][2 * e + 1];
+                l_run = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, l_run, false);
+            }
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const bf16x8 v0 = *(const bf16x8 *)&Vt[buf][l32][16 * st + 8 * h];
+            const bf16x8 v1 = *(const bf16x8 *)&Vt[buf][32 + l32][16 * st + 8 * h];
+
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, pb[st], o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, pb[st], o1, 0, 0, 0);
+        }
+        if (kb + 1 < nblk)
+            stage(buf ^ 1);
+        __syncthreads();
+    }
+
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (qi < N) {
+        const float inv = 1.0f / l_run;
+        const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+        const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
+
+        for (int r = 0; r < 16; r++) {
+            const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+
+            if (d.odt == DT_F32) {
+                ((float *)d.O)[orow + dd] = o0[r] * inv;
+                ((float *)d.O)[orow + 32 + dd] = o1[r] * inv;
+            }
+            else {
+                ((uint16_t *)d.O)[orow + dd] = f2bf(o0[r] * inv);
+                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(o1[r] * inv);
+            }
+        }
+    }
+}
+
+extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
+                                const void *k16, const void *vt16,
+                                void *stream)
+{
+    if (d->nb > 65535)
+        return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(k_attn_bf16, dim3((d->N + 127) / 128, d->nb),
+                       dim3(256), 0, (hipStream_t)stream, *d,
+                       (const uint16_t *)q16, (const uint16_t *)k16,
+                       (const uint16_t *)vt16);
+    return hipGetLastError();
+}

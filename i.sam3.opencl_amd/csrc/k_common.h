@@ -1,0 +1,91 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Device-side helpers shared by the gfx950 kernels: vector types of the
+ * MFMA builtins, bf16 / half conversions and wave64 reductions.
+ */
+#ifndef K_COMMON_H
+#define K_COMMON_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sam3_launch.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define LOG2E_F 1.4426950408889634f
+
+/* Activations of the GEMM / LayerNorm epilogues (sam3_kernels.cl:24-26). */
+#define ACT_NONE_K 0
+#define ACT_GELU_K 1
+#define ACT_RELU_K 2
+
+__device__ __forceinline__ float act_k(float v, int act)
+{
+    if (act == ACT_GELU_K)
+        return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+    if (act == ACT_RELU_K)
+        return fmaxf(v, 0.0f);
+    return v;
+}
+
+/* fp32 -> bf16 / half, round to nearest even (v_cvt_pk_bf16_f32,
+ * v_cvt_f16_f32 on gfx950). */
+__device__ __forceinline__ uint16_t f2bf(float x)
+{
+    __bf16 h = (__bf16)x;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float bf2f(uint16_t v)
+{
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+}
+
+__device__ __forceinline__ float h2f(uint16_t v)
+{
+    return (float)__builtin_bit_cast(_Float16, v);
+}
+
+/* Pack two floats into one dword of two bf16, lo in bits 0-15. */
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi)
+{
+    bf16x2 p;
+
+    p.x = (__bf16)lo;
+    p.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, p);
+}
+
+/* Element load of any storage type as float. */
+template <typename T> __device__ __forceinline__ float ld_f(const T *p);
+template <> __device__ __forceinline__ float ld_f<float>(const float *p)
+{
+    return *p;
+}
+template <> __device__ __forceinline__ float ld_f<uint16_t>(const uint16_t *p)
+{
+    return bf2f(*p);
+}
+
+/* Wave64 butterfly reductions (ds_swizzle / DPP chosen by the compiler). */
+__device__ __forceinline__ float wave_sum(float v)
+{
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+    for (int o = 32; o > 0; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+#endif /* K_COMMON_H */

@@ -1,0 +1,291 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Row and element kernels of the attention path on gfx950: LayerNorm
+ * (optionally fused with the window partition and a bf16 store),
+ * softmax_rows, rope_apply, window partition / unpartition, add_bcast
+ * and storage conversions. All are HBM-bound; they use one workgroup
+ * per row or one thread per element with 64-bit index arithmetic.
+ */
+#include "k_common.h"
+
+/* ------------------------------------------------------------ LayerNorm */
+
+/* Block-wide sum of 256 threads: wave64 butterflies, then 4 partials. */
+__device__ __forceinline__ float block_sum256(float v, float *red)
+{
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+
+    v = wave_sum(v);
+    __syncthreads();
+    if (l == 0)
+        red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+/* One 256-thread workgroup per output row. The row is held in registers
+ * (up to 8 values per thread, C <= 2048) between the mean, variance and
+ * normalisation passes; wider rows are re-read. With ws > 0 output row r
+ * is window-partition position r of an H x H grid (sam3_kernels.cl:
+ * 712-724) and takes its token from there, or zeros in the padding. */
+template <typename TY>
+__global__ __launch_bounds__(256) void k_layernorm(
+    const float *__restrict__ X, TY *__restrict__ Y, const float *__restrict__ g,
+    const float *__restrict__ bt, int C, float eps, int act, int H, int ws,
+    int nwx)
+{
+    __shared__ float red[4];
+    const long r = blockIdx.x;
+    long src = r;
+    float v[8];
+    float s = 0.0f, mean, var, rs;
+    const int t = threadIdx.x;
+    int i, c;
+
+    if (ws > 0) {
+        const int w = (int)(r / ((long)ws * ws)), p = (int)(r % ((long)ws * ws));
+        const int y = (w / nwx) * ws + p / ws, x = (w % nwx) * ws + p % ws;
+
+        if (y >= H || x >= H) {
+            for (c = t; c < C; c += 256)
+                Y[r * C + c] = (TY)0.0f;
+            return;
+        }
+        src = (long)y * H + x;
+    }
+    const float *xr = X + src * C;
+    for (i = 0; i < 8; i++) {
+        c = t + 256 * i;
+        v[i] = c < C ? xr[c] : 0.0f;
+        s += v[i];
+    }
+    for (c = t + 2048; c < C; c += 256)
+        s += xr[c];
+    mean = block_sum256(s, red) / (float)C;
+    s = 0.0f;
+    for (i = 0; i < 8; i++) {
+        c = t + 256 * i;
+        if (c < C) {
+            const float d = v[i] - mean;
+
+            s = fmaf(d, d, s);
+        }
+    }
+    for (c = t + 2048; c < C; c += 256) {
+        const float d = xr[c] - mean;
+
+        s = fmaf(d, d, s);
+    }
+    var = block_sum256(s, red) / (float)C;
+    rs = 1.0f / sqrtf(var + eps);
+    for (c = t; c < C; c += 256) {
+        const float xv = c < 2048 ? v[c >> 8] : xr[c];
+        const float y = fmaf((xv - mean) * rs, g[c], bt[c]);
+
+        Y[r * C + c] = (TY)act_k(y, act);
+    }
+}
+
+extern "C" int launch_layernorm(const float *X, void *Y, int ydt,
+                                const float *g, const float *b, long rows,
+                                int C, float eps, int act, int H, int ws,
+                                int nwx, void *stream)
+{
+    const long out_rows = ws > 0 ? (long)nwx * nwx * ws * ws : rows;
+
+    if (out_rows == 0)
+        return hipSuccess;
+    if (ydt == DT_BF16)
+        hipLaunchKernelGGL(k_layernorm<__bf16>, dim3(out_rows), dim3(256), 0,
+                           (hipStream_t)stream, X, (__bf16 *)Y, g, b, C, eps,
+                           act, H, ws, nwx);
+    else
+        hipLaunchKernelGGL(k_layernorm<float>, dim3(out_rows), dim3(256), 0,
+                           (hipStream_t)stream, X, (float *)Y, g, b, C, eps,
+                           act, H, ws, nwx);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ softmax */
+
+/* In-place softmax of one row of L floats per 256-thread workgroup. */
+__global__ __launch_bounds__(256) void k_softmax_rows(float *__restrict__ S,
+                                                      int L)
+{
+    __shared__ float red[4];
+    float *s = S + (long)blockIdx.x * L;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    float m = -INFINITY, sum = 0.0f, inv;
+    int j;
+
+    for (j = t; j < L; j += 256)
+        m = fmaxf(m, s[j]);
+    m = wave_max(m);
+    __syncthreads();
+    if (l == 0)
+        red[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (j = t; j < L; j += 256) {
+        const float v = expf(s[j] - m);
+
+        s[j] = v;
+        sum += v;
+    }
+    inv = 1.0f / block_sum256(sum, red);
+    for (j = t; j < L; j += 256)
+        s[j] *= inv;
+}
+
+extern "C" int launch_softmax_rows(float *S, long rows, int L, void *stream)
+{
+    hipLaunchKernelGGL(k_softmax_rows, dim3(rows), dim3(256), 0,
+                       (hipStream_t)stream, S, L);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ RoPE */
+
+/* One thread per (row, q/k, pair): the rotation of rope_apply
+ * (sam3_kernels.cl:679-698) at position r % npos. */
+__global__ __launch_bounds__(256) void k_rope_apply(
+    float *__restrict__ qkv, long total, int E, int hd, int npos,
+    const float2 *__restrict__ cs)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    const int nf = hd / 2, half = E / 2;
+
+    if (gid >= total)
+        return;
+    const int pr = (int)(gid % half);
+    const long rest = gid / half;
+    const int qk = (int)(rest % 2);
+    const long r = rest / 2;
+    const int h = pr / nf, j = pr % nf;
+    float *x = qkv + r * 3 * E + (long)qk * E + (long)h * hd + 2 * j;
+    const float2 rot = cs[(r % npos) * nf + j];
+    const float a = x[0], b = x[1];
+
+    x[0] = fmaf(a, rot.x, -(b * rot.y));
+    x[1] = fmaf(a, rot.y, b * rot.x);
+}
+
+extern "C" int launch_rope_apply(float *qkv, long rows, int E, int hd,
+                                 int npos, const float *cs, void *stream)
+{
+    const long total = rows * E;
+
+    if (total == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(k_rope_apply, dim3((total + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, qkv, total, E, hd, npos,
+                       (const float2 *)cs);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ windows */
+
+__global__ __launch_bounds__(256) void k_window_partition(
+    const float *__restrict__ X, float *__restrict__ out, long total, int H,
+    int W, int C, int ws, int nwx)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= total)
+        return;
+    const long r = gid / C;
+    const int c = (int)(gid % C);
+    const int w = (int)(r / ((long)ws * ws)), i = (int)(r % ((long)ws * ws));
+    const int y = (w / nwx) * ws + i / ws, x = (w % nwx) * ws + i % ws;
+
+    out[gid] = (y < H && x < W) ? X[((long)y * W + x) * C + c] : 0.0f;
+}
+
+extern "C" int launch_window_partition(const float *X, float *out, int H,
+                                       int W, int C, int ws, int nwx,
+                                       void *stream)
+{
+    const long total = (long)nwx * nwx * ws * ws * C;
+
+    hipLaunchKernelGGL(k_window_partition, dim3((total + 255) / 256),
+                       dim3(256), 0, (hipStream_t)stream, X, out, total, H, W,
+                       C, ws, nwx);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void k_window_unpartition_add(
+    float *__restrict__ X, const float *__restrict__ Wd, long total, int W,
+    int C, int ws, int nwx)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= total)
+        return;
+    const long t = gid / C;
+    const int c = (int)(gid % C);
+    const int y = (int)(t / W), x = (int)(t % W);
+    const long w = (long)(y / ws) * nwx + x / ws;
+    const long i = (long)(y % ws) * ws + x % ws;
+
+    X[gid] += Wd[(w * ws * ws + i) * C + c];
+}
+
+extern "C" int launch_window_unpartition_add(float *X, const float *Wd, int H,
+                                             int W, int C, int ws, int nwx,
+                                             void *stream)
+{
+    const long total = (long)H * W * C;
+
+    hipLaunchKernelGGL(k_window_unpartition_add, dim3((total + 255) / 256),
+                       dim3(256), 0, (hipStream_t)stream, X, Wd, total, W, C,
+                       ws, nwx);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ add_bcast */
+
+__global__ __launch_bounds__(256) void k_add_bcast(float *out,
+                                                   const float *a,
+                                                   const float *b, long n,
+                                                   long bmod)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (i < n)
+        out[i] = a[i] + b[i % bmod];
+}
+
+extern "C" int launch_add_bcast(float *out, const float *a, const float *b,
+                                long n, long bmod, void *stream)
+{
+    hipLaunchKernelGGL(k_add_bcast, dim3((n + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, out, a, b, n, bmod);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ convert */
+
+__global__ __launch_bounds__(256) void k_convert(const float *__restrict__ s,
+                                                 uint16_t *__restrict__ d,
+                                                 int dt, long n)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (i >= n)
+        return;
+    if (dt == DT_BF16)
+        d[i] = f2bf(s[i]);
+    else
+        d[i] = __builtin_bit_cast(uint16_t, (_Float16)s[i]);
+}
+
+extern "C" int launch_convert(const float *src, void *dst, int dst_dt,
+                              size_t count, void *stream)
+{
+    if (count == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(k_convert, dim3((count + 255) / 256), dim3(256), 0,
+                       (hipStream_t)stream, src, (uint16_t *)dst, dst_dt,
+                       (long)count);
+    return hipGetLastError();
+}

@@ -1,0 +1,325 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Batched GEMM of the reference's contract on gfx950 MFMA:
+ *   C = act(alpha * A * op(B) + bias) + R     (sam3_kernels.cl:57-69)
+ * batch b = blockIdx.z split as (b / nb1, b % nb1) with per-operand
+ * strides, element offsets, transb for B stored N x K (the Linear weight
+ * layout) or K x N, R possibly aliasing C.
+ *
+ * One 256-thread workgroup (4 waves, 2 x 2) computes a 128 x 128 tile of
+ * C; each wave owns 64 x 64 as 2 x 2 blocks of 32 x 32 MFMA
+ * accumulators (64 f32 per lane).
+ *  - MODE_F32:  v_mfma_f32_32x32x2_f32; K tiles of 16 staged in LDS as
+ *    [k][m] / [k][n] floats (row stride 132: conflict-free lane reads).
+ *  - MODE_BF16: v_mfma_f32_32x32x16_bf16 with f32 accumulation; K tiles
+ *    of 64 staged as [m][k] / [n][k] bf16 rows of 72 elements (144 B:
+ *    16-lane groups of 16-byte reads hit distinct banks).
+ * Operands may be float, half (B only) or bf16; they are converted while
+ * being staged. Loads are 16-byte vectors when the host has checked the
+ * alignment of every row start, else guarded scalar loads. Rows and
+ * columns outside the matrices read as zero and are not stored.
+ *
+ * MFMA 32x32 lane layouts (64 lanes, l = lane, h = l / 32):
+ *   A operand:  lane l holds A[l % 32][k-slice of half h]
+ *   B operand:  lane l holds B[k-slice of half h][l % 32]
+ *   D (16 f32): reg r of lane l is D[8 (r / 4) + 4 h + r % 4][l % 32]
+ */
+#include "k_common.h"
+
+/* Up to 8 consecutive elements of type dt at base[idx], as float; the
+ * first `valid` are read, the rest are zero. vec: the 8 elements are
+ * 16-byte aligned (float: two 16-byte loads). */
+__device__ __forceinline__ void load8(const void *base, int dt, long idx,
+                                      int valid, bool vec, float f[8])
+{
+    if (vec && valid >= 8) {
+        if (dt == DT_F32) {
+            const f32x4 *p = (const f32x4 *)((const float *)base + idx);
+            const f32x4 x = p[0], y = p[1];
+
+            f[0] = x[0]; f[1] = x[1]; f[2] = x[2]; f[3] = x[3];
+            f[4] = y[0]; f[5] = y[1]; f[6] = y[2]; f[7] = y[3];
+        }
+        else {
+            const u32x4 v = *(const u32x4 *)((const uint16_t *)base + idx);
+
+            for (int e = 0; e < 4; e++) {
+                const uint16_t lo = (uint16_t)(v[e] & 0xffffu);
+                const uint16_t hi = (uint16_t)(v[e] >> 16);
+
+                f[2 * e] = dt == DT_BF16 ? bf2f(lo) : h2f(lo);
+                f[2 * e + 1] = dt == DT_BF16 ? bf2f(hi) : h2f(hi);
+            }
+        }
+        return;
+    }
+    for (int e = 0; e < 8; e++) {
+        float v = 0.0f;
+
+        if (e < valid) {
+            if (dt == DT_F32)
+                v = ((const float *)base)[idx + e];
+            else if (dt == DT_BF16)
+                v = bf2f(((const uint16_t *)base)[idx + e]);
+            else
+                v = h2f(((const uint16_t *)base)[idx + e]);
+        }
+        f[e] = v;
+    }
+}
+
+__device__ __forceinline__ int clamp8(long n)
+{
+    return n <= 0 ? 0 : n >= 8 ? 8 : (int)n;
+}
+
+/* Epilogue of one 32 x 32 accumulator block at tile rows mb, cols nb0:
+ * alpha, bias, activation, residual, store (store_one,
+ * sam3_kernels.cl:306-319). */
+__device__ __forceinline__ void store_block(const gemm_desc &d, void *C,
+                                           const void *R, f32x16 acc, int mb,
+                                           int ncol)
+{
+    const int l = threadIdx.x & 63, h = l >> 5;
+
+    if (ncol >= d.N)
+        return;
+    for (int r = 0; r < 16; r++) {
+        const int m = mb + 8 * (r >> 2) + 4 * h + (r & 3);
+        float v;
+        long idx;
+
+        if (m >= d.M)
+            continue;
+        idx = (long)m * d.ldc + ncol;
+        v = d.alpha * acc[r];
+        if (d.bias)
+            v += d.bias[ncol];
+        v = act_k(v, d.act);
+        if (d.cdt == DT_F32) {
+            if (R)
+                v += ((const float *)R)[idx];
+            ((float *)C)[idx] = v;
+        }
+        else {
+            if (R)
+                v += bf2f(((const uint16_t *)R)[idx]);
+            ((uint16_t *)C)[idx] = f2bf(v);
+        }
+    }
+}
+
+/* Operand base of batch b (bytes depend on the element type). */
+__device__ __forceinline__ long batch_off(long off, long s0, long s1, long b0,
+                                          long b1)
+{
+    return off + b0 * s0 + b1 * s1;
+}
+
+template <bool TRANSB>
+__global__ __launch_bounds__(256) void k_gemm_f32(gemm_desc d, int avec,
+                                                  int bvec)
+{
+    __shared__ float As[16][132];
+    __shared__ float Bs[16][132];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
+              l32 = l & 31;
+    const int wm = w >> 1, wn = w & 1;
+    const int n0 = blockIdx.x * 128, m0 = blockIdx.y * 128;
+    const long b0 = blockIdx.z / d.nb1, b1 = blockIdx.z % d.nb1;
+    const long abase = batch_off(d.aoff, d.sa0, d.sa1, b0, b1);
+    const long bbase = batch_off(d.boff, d.sb0, d.sb1, b0, b1);
+    const long cbase = batch_off(d.coff, d.sc0, d.sc1, b0, b1);
+    const long rbase = batch_off(d.roff, d.sc0, d.sc1, b0, b1);
+    f32x16 acc[2][2];
+
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++)
+            for (int r = 0; r < 16; r++)
+                acc[i][j][r] = 0.0f;
+
+    for (int k0 = 0; k0 < d.K; k0 += 16) {
+        float f[8];
+
+        {
+            const int row = t >> 1, kk = (t & 1) * 8;
+            const int gm = m0 + row, gk = k0 + kk;
+
+            load8(d.A, d.adt, abase + (long)gm * d.lda + gk, gm < d.M ? clamp8(d.K - gk) : 0,
+                  avec, f);
+            for (int e = 0; e < 8; e++)
+                As[kk + e][row] = f[e];
+        }
+        if (TRANSB) {
+            const int row = t >> 1, kk = (t & 1) * 8;
+            const int gn = n0 + row, gk = k0 + kk;
+
+            load8(d.B, d.bdt, bbase + (long)gn * d.ldb + gk,
+                  gn < d.N ? clamp8(d.K - gk) : 0, bvec, f);
+            for (int e = 0; e < 8; e++)
+                Bs[kk + e][row] = f[e];
+        }
+        else {
+            const int kr = t >> 4, ns = (t & 15) * 8;
+            const int gk = k0 + kr, gn = n0 + ns;
+
+            load8(d.B, d.bdt, bbase + (long)gk * d.ldb + gn,
+                  gk < d.K ? clamp8(d.N - gn) : 0, bvec, f);
+            for (int e = 0; e < 8; e++)
+                Bs[kr][ns + e] = f[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const float a0 = As[2 * s + h][wm * 64 + l32];
+            const float a1 = As[2 * s + h][wm * 64 + 32 + l32];
+            const float c0 = Bs[2 * s + h][wn * 64 + l32];
+            const float c1 = Bs[2 * s + h][wn * 64 + 32 + l32];
+
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, c0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, c1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, c0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, c1, acc[1][1], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    {
+        char *C = (char *)d.C + cbase * (d.cdt == DT_F32 ? 4 : 2);
+        const char *R = d.R ? (const char *)d.R + rbase * (d.cdt == DT_F32 ? 4 : 2)
+                            : NULL;
+
+        for (int i = 0; i < 2; i++)
+            for (int j = 0; j < 2; j++)
+                store_block(d, C, R, acc[i][j], m0 + wm * 64 + i * 32,
+                            n0 + wn * 64 + j * 32 + l32);
+    }
+}
+
+template <bool TRANSB>
+__global__ __launch_bounds__(256) void k_gemm_bf16(gemm_desc d, int avec,
+                                                   int bvec)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t As[128][72];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[128][72];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
+              l32 = l & 31;
+    const int wm = w >> 1, wn = w & 1;
+    const int n0 = blockIdx.x * 128, m0 = blockIdx.y * 128;
+    const long b0 = blockIdx.z / d.nb1, b1 = blockIdx.z % d.nb1;
+    const long abase = batch_off(d.aoff, d.sa0, d.sa1, b0, b1);
+    const long bbase = batch_off(d.boff, d.sb0, d.sb1, b0, b1);
+    const long cbase = batch_off(d.coff, d.sc0, d.sc1, b0, b1);
+    const long rbase = batch_off(d.roff, d.sc0, d.sc1, b0, b1);
+    f32x16 acc[2][2];
+
+    for (int i = 0; i < 2; i++)
+        for (int j = 0; j < 2; j++)
+            for (int r = 0; r < 16; r++)
+                acc[i][j][r] = 0.0f;
+
+    for (int k0 = 0; k0 < d.K; k0 += 64) {
+        float f[8];
+
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = t + 256 * j, row = c >> 3, kk = (c & 7) * 8;
+            const int gm = m0 + row, gk = k0 + kk;
+            u32x4 v;
+
+            load8(d.A, d.adt, abase + (long)gm * d.lda + gk,
+                  gm < d.M ? clamp8(d.K - gk) : 0, avec, f);
+            for (int e = 0; e < 4; e++)
+                v[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+            *(u32x4 *)&As[row][kk] = v;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int c = t + 256 * j;
+
+            if (TRANSB) {
+                const int row = c >> 3, kk = (c & 7) * 8;
+                const int gn = n0 + row, gk = k0 + kk;
+                u32x4 v;
+
+                load8(d.B, d.bdt, bbase + (long)gn * d.ldb + gk,
+                      gn < d.N ? clamp8(d.K - gk) : 0, bvec, f);
+                for (int e = 0; e < 4; e++)
+                    v[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+                *(u32x4 *)&Bs[row][kk] = v;
+            }
+            else {
+                const int kr = c >> 4, ns = (c & 15) * 8;
+                const int gk = k0 + kr, gn = n0 + ns;
+
+                load8(d.B, d.bdt, bbase + (long)gk * d.ldb + gn,
+                      gk < d.K ? clamp8(d.N - gn) : 0, bvec, f);
+                for (int e = 0; e < 8; e++)
+                    Bs[ns + e][kr] = f2bf(f[e]);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const bf16x8 a0 = *(const bf16x8 *)&As[wm * 64 + l32][16 * s + 8 * h];
+            const bf16x8 a1 = *(const bf16x8 *)&As[wm * 64 + 32 + l32][16 * s + 8 * h];
+            const bf16x8 c0 = *(const bf16x8 *)&Bs[wn * 64 + l32][16 * s + 8 * h];
+            const bf16x8 c1 = *(const bf16x8 *)&Bs[wn * 64 + 32 + l32][16 * s + 8 * h];
+
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, c0, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, c1, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, c0, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, c1, acc[1][1], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+    {
+        char *C = (char *)d.C + cbase * (d.cdt == DT_F32 ? 4 : 2);
+        const char *R = d.R ? (const char *)d.R + rbase * (d.cdt == DT_F32 ? 4 : 2)
+                            : NULL;
+
+        for (int i = 0; i < 2; i++)
+            for (int j = 0; j < 2; j++)
+                store_block(d, C, R, acc[i][j], m0 + wm * 64 + i * 32,
+                            n0 + wn * 64 + j * 32 + l32);
+    }
+}
+
+/* 16-byte alignment of every 8-element load: offset, batch strides and
+ * leading dimension are multiples of the elements per 16 bytes (the
+ * buffers themselves come from hipMalloc, 256-byte aligned). */
+static int vec_ok(int dt, long off, long s0, long s1, int ld)
+{
+    const long q = dt == DT_F32 ? 4 : 8;
+
+    return off % q == 0 && s0 % q == 0 && s1 % q == 0 && ld % q == 0;
+}
+
+extern "C" int launch_gemm(const gemm_desc *d, void *stream)
+{
+    const dim3 grid((d->N + 127) / 128, (d->M + 127) / 128, d->nb);
+    const int avec = vec_ok(d->adt, d->aoff, d->sa0, d->sa1, d->lda);
+    const int bvec = vec_ok(d->bdt, d->boff, d->sb0, d->sb1, d->ldb);
+    hipStream_t s = (hipStream_t)stream;
+
+    if (d->nb > 65535 || grid.y > 65535)
+        return hipErrorInvalidConfiguration;
+    if (d->mode == MODE_BF16) {
+        if (d->transb)
+            hipLaunchKernelGGL(k_gemm_bf16<true>, grid, dim3(256), 0, s, *d,
+                               avec, bvec);
+        else
+            hipLaunchKernelGGL(k_gemm_bf16<false>, grid, dim3(256), 0, s, *d,
+                               avec, bvec);
+    }
+    else {
+        if (d->transb)
+            hipLaunchKernelGGL(k_gemm_f32<true>, grid, dim3(256), 0, s, *d,
+                               avec, bvec);
+        else
+            hipLaunchKernelGGL(k_gemm_f32<false>, grid, dim3(256), 0, s, *d,
+                               avec, bvec);
+    }
+    return hipGetLastError();
+}

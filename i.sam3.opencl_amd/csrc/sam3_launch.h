@@ -1,0 +1,130 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Internal interface between the C host layer (hip_backend.c,
+ * sam3_ops.c) and the HIP kernels (*.hip). Every launcher is extern "C",
+ * takes device pointers, sizes and a hipStream_t (as void *), queues its
+ * kernel(s) on that stream and returns the hipError_t of the launch
+ * (0 = hipSuccess). Shapes are validated by the callers.
+ */
+#ifndef SAM3_LAUNCH_H
+#define SAM3_LAUNCH_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types, the HIPB_* values of sam3_hip.h. */
+#define DT_F32 0
+#define DT_F16 1
+#define DT_BF16 2
+
+/* MFMA arithmetic of a GEMM or attention launch. */
+#define MODE_F32 0  /* v_mfma_f32_32x32x2_f32, fp32 operands */
+#define MODE_BF16 1 /* v_mfma_f32_32x32x16_bf16, f32 accumulation */
+
+/* Batched GEMM with the reference contract (sam3_kernels.cl:57-69). */
+struct gemm_desc {
+    int M, N, K;
+    const void *A;
+    long aoff;
+    int lda;
+    long sa0, sa1;
+    int adt;
+    const void *B;
+    long boff;
+    int ldb;
+    long sb0, sb1;
+    int bdt, transb;
+    void *C;
+    long coff;
+    int ldc;
+    long sc0, sc1;
+    int cdt;
+    int nb, nb1;
+    const float *bias;
+    const void *R; /* same type and layout as C */
+    long roff;
+    float alpha;
+    int act;
+    int mode;
+};
+int launch_gemm(const struct gemm_desc *d, void *stream);
+
+/* Row LayerNorm of rows x C floats into Y (float or bf16). With ws > 0
+ * the output rows are the window-partitioned order of an H x H grid
+ * (nwx windows per side, zero rows for padding): row count nwx^2 ws^2. */
+int launch_layernorm(const float *X, void *Y, int ydt, const float *g,
+                     const float *b, long rows, int C, float eps, int act,
+                     int H, int ws, int nwx, void *stream);
+
+int launch_softmax_rows(float *S, long rows, int L, void *stream);
+int launch_rope_apply(float *qkv, long rows, int E, int hd, int npos,
+                      const float *cs, void *stream);
+int launch_window_partition(const float *X, float *out, int H, int W, int C,
+                            int ws, int nwx, void *stream);
+int launch_window_unpartition_add(float *X, const float *Wd, int H, int W,
+                                  int C, int ws, int nwx, void *stream);
+int launch_add_bcast(float *out, const float *a, const float *b, long n,
+                     long bmod, void *stream);
+
+/* Fused attention over nb units of N tokens, head width 64. */
+struct attn_desc {
+    int N, nb, nb1;
+    const void *Q;
+    long qoff;
+    int ldq;
+    long sq0, sq1;
+    const void *K;
+    long koff;
+    int ldk;
+    long sk0, sk1;
+    const void *V;
+    long voff;
+    int ldv;
+    long sv0, sv1;
+    void *O;
+    long ooff;
+    int ldo;
+    long so0, so1;
+    int odt;
+    const float *rope; /* (cos, sin) x 32 per position, or NULL */
+    int npos;
+    float scale;
+};
+
+/* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads. */
+int launch_attn_f32(const struct attn_desc *d, void *stream);
+
+/* Packed bf16 staging of the fast path, Np = N rounded up to 64:
+ * q16/k16 [nb][Np][64] (RoPE applied, q scaled), vt16 [nb][64][Np],
+ * zero in the padding. */
+int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
+                    void *vt16, void *stream);
+
+/* bf16 MFMA attention on the packed operands; O addressed as in d. */
+int launch_attn_bf16(const struct attn_desc *d, const void *q16,
+                     const void *k16, const void *vt16, void *stream);
+
+/* Decoder attention (8 heads, head width c = dint / 8). */
+int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,
+                       const float *V, long sv, float *O, int P, int Nq,
+                       int Nk, int dint, float scale, void *stream);
+/* Split-K token->image attention for c == 16; scratch holds the
+ * partial results, mha_manykeys_scratch() bytes. */
+size_t mha_manykeys_scratch(int P, int Nq, int Nk);
+int launch_mha_manykeys(const float *Q, long sq, const float *K, long sk,
+                        const float *V, long sv, float *O, int P, int Nq,
+                        int Nk, int dint, float scale, void *scratch,
+                        void *stream);
+
+/* fp32 -> bf16 / half conversion of count elements (weight uploads). */
+int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
+                   void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3_LAUNCH_H */

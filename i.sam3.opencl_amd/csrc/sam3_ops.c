@@ -1,0 +1,674 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * sam3_ops.c - the operator layer of the attention path on HIP: the
+ * functions of sam3_ops.h (gemm, linear, layernorm, add_bcast, mat,
+ * bmat), the attention helpers of sam3_model.c (softmax_rows,
+ * rope_apply, window_partition, window_unpartition_add, mha), and the
+ * fused attention entry points attn_fused / vit_attention.
+ *
+ * Each operator validates its shapes and that every element it will
+ * touch lies inside its buffers before anything is queued (a bad
+ * operand is a fatal error naming the call, never a device fault), then
+ * queues its kernel(s) on the backend's stream inside the profiling
+ * bracket of the reference's run() (sam3_model.c:167-207).
+ */
+#include "hipb_internal.h"
+#include "sam3_launch.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ENC_EPS 1e-5f   /* ViT LayerNorm eps (sam3_model.c:30) */
+#define DEC_HEADS 8     /* decoder heads (sam3_model.c:36) */
+
+struct opnd mat(hipb_mem buf, long off, int ld)
+{
+    struct opnd o = {buf, off, ld, 0, 0};
+
+    return o;
+}
+
+struct opnd bmat(hipb_mem buf, long off, int ld, long s0, long s1)
+{
+    struct opnd o = {buf, off, ld, s0, s1};
+
+    return o;
+}
+
+/* True if rows x cols elements at (off, ld) for every batch b < nb,
+ * b = (b / nb1) * s0 + (b % nb1) * s1, lie inside o.buf; fatal
+ * otherwise. */
+static int opnd_ok(const char *op, const char *name, struct opnd o, long rows,
+                   long cols, int nb, int nb1)
+{
+    long last, b0max, b1max;
+
+    if (!o.buf) {
+        hipb_fatal("%s: operand %s has no buffer", op, name);
+        return 0;
+    }
+    if (rows <= 0 || cols <= 0)
+        return 1;
+    if (o.off < 0 || o.s0 < 0 || o.s1 < 0 || o.ld < 0 ||
+        (rows > 1 && o.ld < cols)) {
+        hipb_fatal("%s: operand %s has a negative offset or stride, or "
+                   "ld %d < %ld columns",
+                   op, name, o.ld, cols);
+        return 0;
+    }
+    b0max = (nb - 1) / nb1;
+    b1max = (nb < nb1 ? nb : nb1) - 1;
+    last = o.off + b0max * o.s0 + b1max * o.s1 + (rows - 1) * (long)o.ld +
+           cols - 1;
+    if ((size_t)last >= hipb_count(o.buf)) {
+        hipb_fatal("%s: operand %s reaches element %ld of buffer <%s> "
+                   "(%lu elements)",
+                   op, name, last, o.buf->what,
+                   (unsigned long)hipb_count(o.buf));
+        return 0;
+    }
+    return 1;
+}
+
+static int buf_ok(const char *op, const char *name, hipb_mem m, size_t count,
+                  int dtype)
+{
+    if (!m) {
+        hipb_fatal("%s: %s has no buffer", op, name);
+        return 0;
+    }
+    if (dtype >= 0 && m->dtype != dtype) {
+        hipb_fatal("%s: %s <%s> has element type %d, expected %d", op, name,
+                   m->what, m->dtype, dtype);
+        return 0;
+    }
+    if (hipb_count(m) < count) {
+        hipb_fatal("%s: %s <%s> holds %lu elements, %lu needed", op, name,
+                   m->what, (unsigned long)hipb_count(m),
+                   (unsigned long)count);
+        return 0;
+    }
+    return 1;
+}
+
+/* ------------------------------------------------------------ GEMM */
+
+void gemm(struct sam_model *m, int M, int N, int K, struct opnd A,
+          struct opnd B, int transb, struct opnd C, int nb, int nb1,
+          hipb_mem bias, hipb_mem R, long roff, float alpha, int act)
+{
+    struct hipb_backend *b = m->hip;
+    struct gemm_desc d;
+    struct opnd Ro;
+    const char *what;
+    int err;
+
+    if (M < 0 || N < 0 || K < 0 || nb < 1 || nb1 < 1 || act < ACT_NONE ||
+        act > ACT_RELU) {
+        hipb_fatal("gemm: invalid shape M=%d N=%d K=%d nb=%d nb1=%d act=%d",
+                   M, N, K, nb, nb1, act);
+        return;
+    }
+    if (M == 0 || N == 0)
+        return;
+    if (!opnd_ok("gemm", "A", A, M, K, nb, nb1) ||
+        !opnd_ok("gemm", "B", B, transb ? N : K, transb ? K : N, nb, nb1) ||
+        !opnd_ok("gemm", "C", C, M, N, nb, nb1))
+        return;
+    if (A.buf->dtype == HIPB_F16 || C.buf->dtype == HIPB_F16) {
+        hipb_fatal("gemm: half storage is for operand B only");
+        return;
+    }
+    if (bias && !buf_ok("gemm", "bias", bias, (size_t)N, HIPB_F32))
+        return;
+    if (R) {
+        Ro = C;
+        Ro.buf = R;
+        Ro.off = roff;
+        if (!opnd_ok("gemm", "R", Ro, M, N, nb, nb1))
+            return;
+        if (R->dtype != C.buf->dtype) {
+            hipb_fatal("gemm: residual R must have C's element type");
+            return;
+        }
+    }
+    memset(&d, 0, sizeof(d));
+    d.M = M;
+    d.N = N;
+    d.K = K;
+    d.A = A.buf->ptr;
+    d.aoff = A.off;
+    d.lda = A.ld;
+    d.sa0 = A.s0;
+    d.sa1 = A.s1;
+    d.adt = A.buf->dtype;
+    d.B = B.buf->ptr;
+    d.boff = B.off;
+    d.ldb = B.ld;
+    d.sb0 = B.s0;
+    d.sb1 = B.s1;
+    d.bdt = B.buf->dtype;
+    d.transb = transb != 0;
+    d.C = C.buf->ptr;
+    d.coff = C.off;
+    d.ldc = C.ld;
+    d.sc0 = C.s0;
+    d.sc1 = C.s1;
+    d.cdt = C.buf->dtype;
+    d.nb = nb;
+    d.nb1 = nb1;
+    d.bias = bias ? (const float *)bias->ptr : NULL;
+    d.R = R ? R->ptr : NULL;
+    d.roff = roff;
+    d.alpha = alpha;
+    d.act = act;
+    d.mode = (b->bf16 || d.adt == HIPB_BF16 || d.bdt == HIPB_BF16)
+                 ? MODE_BF16
+                 : MODE_F32;
+    what = d.mode == MODE_BF16 ? "gemm_bf16" : "gemm_f32";
+    hipb_run_begin(b);
+    err = launch_gemm(&d, b->stream);
+    hipb_run_end(b, err, what, 2.0 * M * N * K * (double)nb);
+}
+
+/* Y[rows, out] = act(X[rows, in] W^T + b) (+ Y when residual)
+ * (sam3_model.c:305-310). */
+void linear(struct sam_model *m, int rows, int in, int out, hipb_mem X,
+            long xoff, hipb_mem W, hipb_mem b, hipb_mem Y, long yoff, int act,
+            int residual)
+{
+    gemm(m, rows, out, in, mat(X, xoff, in), mat(W, 0, in), 1,
+         mat(Y, yoff, out), 1, 1, b, residual ? Y : NULL, yoff, 1.0f, act);
+}
+
+/* ------------------------------------------------------------ row ops */
+
+void layernorm(struct sam_model *m, long rows, int C, hipb_mem X, hipb_mem Y,
+               hipb_mem g, hipb_mem b, float eps, int act)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (rows < 0 || C < 1 || act < ACT_NONE || act > ACT_RELU) {
+        hipb_fatal("layernorm: invalid shape rows=%ld C=%d", rows, C);
+        return;
+    }
+    if (!buf_ok("layernorm", "X", X, (size_t)rows * C, HIPB_F32) ||
+        !buf_ok("layernorm", "Y", Y, (size_t)rows * C, -1) ||
+        !buf_ok("layernorm", "g", g, (size_t)C, HIPB_F32) ||
+        !buf_ok("layernorm", "b", b, (size_t)C, HIPB_F32))
+        return;
+    if (Y->dtype == HIPB_F16 || (Y->dtype == HIPB_BF16 && X == Y)) {
+        hipb_fatal("layernorm: Y must be float, or bf16 distinct from X");
+        return;
+    }
+    if (rows == 0)
+        return;
+    hipb_run_begin(be);
+    err = launch_layernorm(X->ptr, Y->ptr, Y->dtype, g->ptr, b->ptr, rows, C,
+                           eps, act, 0, 0, 0, be->stream);
+    hipb_run_end(be, err, "layernorm", 0.0);
+}
+
+void add_bcast(struct sam_model *m, hipb_mem out, hipb_mem a, hipb_mem b,
+               long n, long bmod)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (n < 0 || bmod < 1) {
+        hipb_fatal("add_bcast: invalid n=%ld bmod=%ld", n, bmod);
+        return;
+    }
+    if (!buf_ok("add_bcast", "out", out, (size_t)n, HIPB_F32) ||
+        !buf_ok("add_bcast", "a", a, (size_t)n, HIPB_F32) ||
+        !buf_ok("add_bcast", "b", b, (size_t)(bmod < n ? bmod : n),
+                HIPB_F32))
+        return;
+    if (n == 0)
+        return;
+    hipb_run_begin(be);
+    err = launch_add_bcast(out->ptr, a->ptr, b->ptr, n, bmod, be->stream);
+    hipb_run_end(be, err, "add_bcast", 0.0);
+}
+
+void softmax_rows(struct sam_model *m, hipb_mem S, long rows, int L)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (rows < 0 || L < 1) {
+        hipb_fatal("softmax_rows: invalid shape rows=%ld L=%d", rows, L);
+        return;
+    }
+    if (!buf_ok("softmax_rows", "S", S, (size_t)rows * L, HIPB_F32))
+        return;
+    if (rows == 0)
+        return;
+    hipb_run_begin(be);
+    err = launch_softmax_rows(S->ptr, rows, L, be->stream);
+    hipb_run_end(be, err, "softmax_rows", 0.0);
+}
+
+void rope_apply(struct sam_model *m, hipb_mem table, long rows, int npos)
+{
+    struct hipb_backend *be = m->hip;
+    const int E = m->embed, hd = m->hd;
+    int err;
+
+    if (rows < 0 || npos < 1 || hd < 2 || hd % 2 || E % hd) {
+        hipb_fatal("rope_apply: invalid shape rows=%ld npos=%d", rows, npos);
+        return;
+    }
+    if (!buf_ok("rope_apply", "qkv", m->qkv, (size_t)rows * 3 * E, HIPB_F32) ||
+        !buf_ok("rope_apply", "table", table, (size_t)npos * hd, HIPB_F32))
+        return;
+    if (rows == 0)
+        return;
+    hipb_run_begin(be);
+    err = launch_rope_apply(m->qkv->ptr, rows, E, hd, npos, table->ptr,
+                            be->stream);
+    hipb_run_end(be, err, "rope_apply", 0.0);
+}
+
+void window_partition(struct sam_model *m, hipb_mem X, hipb_mem out, int H,
+                      int C, int ws, int nwx)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (H < 1 || C < 1 || ws < 1 || nwx < 1 || (long)nwx * ws < H) {
+        hipb_fatal("window_partition: invalid geometry H=%d ws=%d nwx=%d", H,
+                   ws, nwx);
+        return;
+    }
+    if (!buf_ok("window_partition", "X", X, (size_t)H * H * C, HIPB_F32) ||
+        !buf_ok("window_partition", "out", out,
+                (size_t)nwx * nwx * ws * ws * C, HIPB_F32))
+        return;
+    hipb_run_begin(be);
+    err = launch_window_partition(X->ptr, out->ptr, H, H, C, ws, nwx,
+                                  be->stream);
+    hipb_run_end(be, err, "window_partition", 0.0);
+}
+
+void window_unpartition_add(struct sam_model *m, hipb_mem X, hipb_mem Wd,
+                            int H, int C, int ws, int nwx)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (H < 1 || C < 1 || ws < 1 || nwx < 1 || (long)nwx * ws < H) {
+        hipb_fatal("window_unpartition_add: invalid geometry H=%d ws=%d "
+                   "nwx=%d",
+                   H, ws, nwx);
+        return;
+    }
+    if (!buf_ok("window_unpartition_add", "X", X, (size_t)H * H * C,
+                HIPB_F32) ||
+        !buf_ok("window_unpartition_add", "Wd", Wd,
+                (size_t)nwx * nwx * ws * ws * C, HIPB_F32))
+        return;
+    hipb_run_begin(be);
+    err = launch_window_unpartition_add(X->ptr, Wd->ptr, H, H, C, ws, nwx,
+                                        be->stream);
+    hipb_run_end(be, err, "window_unpartition_add", 0.0);
+}
+
+/* ------------------------------------------------------------ decoder */
+
+/* Extent in elements of P prompts of `rows` rows of dint channels with
+ * per-prompt stride s (0 = shared). */
+static size_t dec_extent(int P, long s, int rows, int dint)
+{
+    return (size_t)((long)(P - 1) * s + (long)rows * dint);
+}
+
+void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
+         long sq, hipb_mem kp, long sk, hipb_mem vp, long sv, hipb_mem o)
+{
+    struct hipb_backend *be = m->hip;
+    const int c = dint / DEC_HEADS;
+    const float scale = 1.0f / sqrtf((float)c);
+    const int many = Nk > 64;
+    int err;
+
+    if (P < 1 || Nq < 1 || Nk < 1 || dint < DEC_HEADS || sq < 0 || sk < 0 ||
+        sv < 0) {
+        hipb_fatal("mha: invalid shape P=%d Nq=%d Nk=%d dint=%d", P, Nq, Nk,
+                   dint);
+        return;
+    }
+    /* The reference takes c == 16 for many keys and its float16 vector
+     * kernels need c of 16 or 32 (sam3_kernels.cl:527-569). */
+    if ((many && c != 16) || dint % DEC_HEADS || (c != 16 && c != 32)) {
+        hipb_fatal("mha: unsupported shape");
+        return;
+    }
+    if (!buf_ok("mha", "q", qp, dec_extent(P, sq, Nq, dint), HIPB_F32) ||
+        !buf_ok("mha", "k", kp, dec_extent(P, sk, Nk, dint), HIPB_F32) ||
+        !buf_ok("mha", "v", vp, dec_extent(P, sv, Nk, dint), HIPB_F32) ||
+        !buf_ok("mha", "o", o, (size_t)P * Nq * dint, HIPB_F32))
+        return;
+    hipb_run_begin(be);
+    if (many) {
+        void *scr = hipb_scratch(be, mha_manykeys_scratch(P, Nq, Nk));
+
+        if (!scr)
+            return;
+        err = launch_mha_manykeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
+                                  o->ptr, P, Nq, Nk, dint, scale, scr,
+                                  be->stream);
+        hipb_run_end(be, err, "attn_manykeys",
+                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+    }
+    else {
+        err = launch_mha_fewkeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
+                                 o->ptr, P, Nq, Nk, dint, scale, be->stream);
+        hipb_run_end(be, err, "attn_fewkeys",
+                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+    }
+}
+
+/* ------------------------------------------------------------ attention */
+
+/* Grow a model-owned bf16 staging buffer to count elements. */
+static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
+                       const char *what)
+{
+    if (*buf && hipb_count(*buf) >= count)
+        return 1;
+    if (*buf) {
+        hipb_finish(b);
+        hipb_release(buf);
+    }
+    *buf = hipb_alloc_typed(b, count, HIPB_BF16, what);
+    return *buf != NULL;
+}
+
+void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
+                struct opnd K, struct opnd V, struct opnd O, hipb_mem rope,
+                int npos, float scale)
+{
+    struct hipb_backend *b = m->hip;
+    const int hd = 64;
+    struct attn_desc d;
+    int err;
+
+    if (N < 0 || nb < 1 || nb1 < 1 || (rope && npos < 1)) {
+        hipb_fatal("attn_fused: invalid shape N=%d nb=%d nb1=%d npos=%d", N,
+                   nb, nb1, npos);
+        return;
+    }
+    if (m->hd != 0 && m->hd != hd) {
+        hipb_fatal("attn_fused: unsupported head width %d", m->hd);
+        return;
+    }
+    if (N == 0)
+        return;
+    if (!opnd_ok("attn_fused", "Q", Q, N, hd, nb, nb1) ||
+        !opnd_ok("attn_fused", "K", K, N, hd, nb, nb1) ||
+        !opnd_ok("attn_fused", "V", V, N, hd, nb, nb1) ||
+        !opnd_ok("attn_fused", "O", O, N, hd, nb, nb1))
+        return;
+    if (Q.buf->dtype != HIPB_F32 || K.buf->dtype != HIPB_F32 ||
+        V.buf->dtype != HIPB_F32 || O.buf->dtype == HIPB_F16) {
+        hipb_fatal("attn_fused: Q, K, V must be float; O float or bf16");
+        return;
+    }
+    if (rope && !buf_ok("attn_fused", "rope", rope, (size_t)npos * hd,
+                        HIPB_F32))
+        return;
+    d.N = N;
+    d.nb = nb;
+    d.nb1 = nb1;
+    d.Q = Q.buf->ptr;
+    d.qoff = Q.off;
+    d.ldq = Q.ld;
+    d.sq0 = Q.s0;
+    d.sq1 = Q.s1;
+    d.K = K.buf->ptr;
+    d.koff = K.off;
+    d.ldk = K.ld;
+    d.sk0 = K.s0;
+    d.sk1 = K.s1;
+    d.V = V.buf->ptr;
+    d.voff = V.off;
+    d.ldv = V.ld;
+    d.sv0 = V.s0;
+    d.sv1 = V.s1;
+    d.O = O.buf->ptr;
+    d.ooff = O.off;
+    d.ldo = O.ld;
+    d.so0 = O.s0;
+    d.so1 = O.s1;
+    d.odt = O.buf->dtype;
+    d.rope = rope ? (const float *)rope->ptr : NULL;
+    d.npos = rope ? npos : 1;
+    d.scale = scale;
+    if (b->bf16) {
+        const size_t np = ((size_t)N + 63) / 64 * 64;
+        const size_t cnt = (size_t)nb * np * hd;
+
+        if (!ensure_bf16(b, &m->q16, cnt, "packed q") ||
+            !ensure_bf16(b, &m->k16, cnt, "packed k") ||
+            !ensure_bf16(b, &m->vt16, cnt, "packed v^T"))
+            return;
+        hipb_run_begin(b);
+        err = launch_qkv_pack(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                              b->stream);
+        hipb_run_end(b, err, "qkv_pack", 0.0);
+        if (hipb_failed())
+            return;
+        hipb_run_begin(b);
+        err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                               b->stream);
+        hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * hd * nb);
+        return;
+    }
+    hipb_run_begin(b);
+    err = launch_attn_f32(&d, b->stream);
+    hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)N * hd * nb);
+}
+
+/* Attention geometry of a block (block_geom, sam3_model.c:777-791). */
+struct geom {
+    int s, nwx, nwin, N;
+};
+
+static struct geom block_geom(const struct sam_model *m,
+                              const struct vit_block *blk)
+{
+    struct geom g;
+
+    g.s = blk->window ? blk->window : m->grid;
+    g.nwx = (m->grid + g.s - 1) / g.s;
+    g.nwin = g.nwx * g.nwx;
+    g.N = g.s * g.s;
+    return g;
+}
+
+/* Heads whose score planes fit the score buffer (head_chunk,
+ * sam3_model.c:793-798). */
+static int head_chunk(const struct sam_model *m, const struct geom *g)
+{
+    long hc = m->score_cap / ((long)g->nwin * g->N * g->N);
+
+    return hc > m->heads ? m->heads : (int)hc;
+}
+
+void vit_attention(struct sam_model *m, const struct vit_block *blk,
+                   int unfused)
+{
+    struct hipb_backend *b = m->hip;
+    const struct geom g = block_geom(m, blk);
+    const int T = m->grid * m->grid, E = m->embed, hd = m->hd;
+    const long rows = (long)g.nwin * g.N;
+    const float scale = 1.0f / sqrtf((float)hd);
+    hipb_mem table = blk->window ? m->rope_win : m->rope_glob;
+    hipb_mem A = m->xn;
+    int h0;
+
+    if (!table) {
+        hipb_fatal("vit_attention: no RoPE table for this block");
+        return;
+    }
+    if (rows > (long)(hipb_count(m->qkv) / (3 * (size_t)E))) {
+        hipb_fatal("vit_attention: block needs %ld rows, work buffers hold "
+                   "fewer",
+                   rows);
+        return;
+    }
+    if (b->bf16 && !unfused) {
+        /* LayerNorm straight into bf16 in window-partitioned row order,
+         * QKV projection on bf16 MFMA, then the packed fast path. */
+        if (!ensure_bf16(b, &m->xn16, (size_t)rows * E, "normalized tokens "
+                                                        "(bf16)") ||
+            !buf_ok("vit_attention", "x", m->x, (size_t)T * E, HIPB_F32))
+            return;
+        hipb_run_begin(b);
+        {
+            int err = launch_layernorm(
+                m->x->ptr, m->xn16->ptr, HIPB_BF16, blk->n1w->ptr,
+                blk->n1b->ptr, T, E, ENC_EPS, ACT_NONE,
+                blk->window ? m->grid : 0, blk->window ? g.s : 0, g.nwx,
+                b->stream);
+            hipb_run_end(b, err, "layernorm", 0.0);
+        }
+        if (hipb_failed())
+            return;
+        linear(m, (int)rows, E, 3 * E, m->xn16, 0, blk->qkvw, blk->qkvb,
+               m->qkv, 0, ACT_NONE, 0);
+        if (hipb_failed())
+            return;
+        attn_fused(m, g.N, g.nwin * m->heads, m->heads,
+                   bmat(m->qkv, 0, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->qkv, E, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->qkv, 2L * E, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->attn, 0, E, (long)g.N * E, hd), table, g.N, scale);
+        return;
+    }
+
+    layernorm(m, T, E, m->x, m->xn, blk->n1w, blk->n1b, ENC_EPS, ACT_NONE);
+    if (blk->window) {
+        window_partition(m, m->xn, m->xw, m->grid, E, g.s, g.nwx);
+        A = m->xw;
+    }
+    linear(m, (int)rows, E, 3 * E, A, 0, blk->qkvw, blk->qkvb, m->qkv, 0,
+           ACT_NONE, 0);
+    if (hipb_failed())
+        return;
+    if (!unfused) {
+        /* RoPE and the scale are applied on the Q/K loads. */
+        attn_fused(m, g.N, g.nwin * m->heads, m->heads,
+                   bmat(m->qkv, 0, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->qkv, E, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->qkv, 2L * E, 3 * E, (long)g.N * 3 * E, hd),
+                   bmat(m->attn, 0, E, (long)g.N * E, hd), table, g.N, scale);
+        return;
+    }
+
+    /* The reference's sequence (sam3_model.c:998-1013). */
+    rope_apply(m, table, rows, g.N);
+    if (!m->scores) {
+        size_t need = 0;
+        int i;
+
+        for (i = 0; i < m->depth; i++) {
+            const struct geom gi = block_geom(m, &m->blocks[i]);
+            size_t n = (size_t)head_chunk(m, &gi) * gi.nwin * gi.N * gi.N;
+
+            if (n > need)
+                need = n;
+        }
+        if (need == 0)
+            need = (size_t)head_chunk(m, &g) * g.nwin * g.N * g.N;
+        m->scores = hipb_alloc(b, need * sizeof(float), "attention scores");
+        if (!m->scores)
+            return;
+    }
+    {
+        const int hc = head_chunk(m, &g);
+
+        for (h0 = 0; h0 < m->heads && !hipb_failed(); h0 += hc) {
+            int hcc = m->heads - h0 < hc ? m->heads - h0 : hc;
+            long plane = (long)g.N * g.N, tstride = (long)g.N * 3 * E;
+
+            gemm(m, g.N, g.N, hd,
+                 bmat(m->qkv, (long)h0 * hd, 3 * E, tstride, hd),
+                 bmat(m->qkv, E + (long)h0 * hd, 3 * E, tstride, hd), 1,
+                 bmat(m->scores, 0, g.N, hcc * plane, plane), g.nwin * hcc,
+                 hcc, NULL, NULL, 0, scale, ACT_NONE);
+            softmax_rows(m, m->scores, (long)g.nwin * hcc * g.N, g.N);
+            gemm(m, g.N, hd, g.N, bmat(m->scores, 0, g.N, hcc * plane, plane),
+                 bmat(m->qkv, 2L * E + (long)h0 * hd, 3 * E, tstride, hd), 0,
+                 bmat(m->attn, (long)h0 * hd, E, (long)g.N * E, hd),
+                 g.nwin * hcc, hcc, NULL, NULL, 0, 1.0f, ACT_NONE);
+        }
+    }
+}
+
+/* ------------------------------------------------------------ setup */
+
+void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
+                   int embed, int heads, int hd, struct vit_block *blocks,
+                   int depth)
+{
+    const size_t f = sizeof(float);
+    const long T = (long)grid * grid;
+    size_t cap;
+    long rows = T;
+    int i;
+
+    memset(m, 0, sizeof(*m));
+    m->hip = b;
+    m->grid = grid;
+    m->embed = embed;
+    m->heads = heads;
+    m->hd = hd;
+    m->blocks = blocks;
+    m->depth = depth;
+    if (grid < 1 || hd != 64 || embed != heads * hd) {
+        hipb_fatal("Unsupported attention head width %d", hd);
+        return;
+    }
+    cap = b->max_alloc < ((size_t)512 << 20) ? b->max_alloc
+                                             : ((size_t)512 << 20);
+    m->score_cap = (long)(cap / f);
+    for (i = 0; i < depth; i++) {
+        const struct geom g = block_geom(m, &blocks[i]);
+        const int hc = head_chunk(m, &g);
+
+        if (hc < 1) {
+            hipb_fatal("HIP device cannot hold the attention scores of one "
+                       "head (%lu MiB)",
+                       (unsigned long)((size_t)g.nwin * g.N * g.N * f >> 20));
+            return;
+        }
+        if ((long)g.nwin * g.N > rows)
+            rows = (long)g.nwin * g.N;
+    }
+    m->x = hipb_alloc(b, T * embed * f, "tokens");
+    m->xn = hipb_alloc(b, T * embed * f, "normalized tokens");
+    m->xw = hipb_alloc(b, rows * embed * f, "window partition");
+    m->qkv = hipb_alloc(b, rows * 3 * embed * f, "qkv");
+    m->attn = hipb_alloc(b, rows * embed * f, "attention output");
+}
+
+void sam_path_free(struct sam_model *m)
+{
+    if (m->hip)
+        hipb_finish(m->hip);
+    hipb_release(&m->x);
+    hipb_release(&m->xn);
+    hipb_release(&m->xw);
+    hipb_release(&m->qkv);
+    hipb_release(&m->scores);
+    hipb_release(&m->attn);
+    hipb_release(&m->xn16);
+    hipb_release(&m->q16);
+    hipb_release(&m->k16);
+    hipb_release(&m->vt16);
+}

@@ -1,0 +1,274 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * sam3_hip.h - MI355X (gfx950) backend and operator API for the SAM 3
+ * attention path of i.sam3.opencl.
+ *
+ * A drop-in for the reference's OpenCL path on the attention region:
+ * - the backend section replaces ocl_backend.h (ocl_backend.h:57-104):
+ *   cl_mem becomes hipb_mem, ocl_* becomes hipb_*, and the raw OpenCL
+ *   calls model code makes (clFinish, clEnqueueCopyBuffer) get
+ *   hipb_finish / hipb_copy;
+ * - the operator section keeps the names, argument meaning and error
+ *   behaviour of sam3_ops.h (sam3_ops.h:19-65) and of the static helpers
+ *   of sam3_model.c that the attention path calls (softmax_rows,
+ *   rope_apply, window_partition, window_unpartition_add, mha), and adds
+ *   attn_fused (the fused replacement of the per-head-chunk
+ *   gemm -> softmax_rows -> gemm loop, sam3_model.c:1000-1013) and
+ *   vit_attention (the attention region of vit_block,
+ *   sam3_model.c:981-1013).
+ *
+ * Every function is plain C with plain pointers and sizes. Errors follow
+ * the reference: any failure is fatal with a message naming the call
+ * (G_fatal_error in the reference). A binding that must survive errors
+ * selects HIPB_ERR_RECORD and reads hipb_last_error() after each call.
+ *
+ * One host thread drives one hipb_backend; all work goes to its one
+ * in-order stream (the reference's one in-order queue, ocl_backend.c
+ * clCreateCommandQueue). The API is not re-entrant, like the reference's
+ * (kernel objects there are shared and mutated by SETARG).
+ */
+#ifndef SAM3_HIP_H
+#define SAM3_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ */
+/* Backend (replaces ocl_backend.h)                                    */
+/* ------------------------------------------------------------------ */
+
+/* Element type of a device buffer. The reference only knows float
+ * buffers and half weight matrices (ocl_backend.c:520-587); bf16 is the
+ * storage of the precision=bf16 fast path. */
+#define HIPB_F32 0
+#define HIPB_F16 1
+#define HIPB_BF16 2
+
+/* Device profile (profile= option, ocl_backend.h:14-25). A HIP device is
+ * a discrete GPU with its own memory: "auto" and "dgpu" select it, the
+ * host-memory profiles do not exist here. */
+#define HIPB_ARCH_DGPU 2
+
+/* Error handling mode: fatal (print and exit, the reference's
+ * G_fatal_error) or record (keep the message, return to the caller). */
+#define HIPB_ERR_FATAL 0
+#define HIPB_ERR_RECORD 1
+
+/* A device buffer (replaces cl_mem). */
+typedef struct hipb_buf *hipb_mem;
+
+struct hipb_buf {
+    void *ptr;        /* device address */
+    size_t bytes;     /* allocation size */
+    int dtype;        /* HIPB_F32, HIPB_F16 or HIPB_BF16 */
+    const char *what; /* name given at allocation, for messages */
+};
+
+struct hipb_backend {
+    int device;            /* HIP device ordinal */
+    char device_name[256]; /* marketing name */
+    char arch_name[64];    /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    size_t max_alloc;      /* largest single allocation allowed */
+    size_t global_mem;     /* device memory in bytes */
+    int cu_count;          /* compute units */
+    int clock_khz;         /* peak engine clock */
+    int arch;              /* HIPB_ARCH_DGPU */
+    int fp16w;    /* precision=fp16: weight matrices stored as half */
+    int bf16;     /* precision=bf16: bf16 MFMA fast path */
+    int profile;  /* per-kernel timing (I_SAM3_OPENCL_PROFILE set) */
+    void *stream; /* hipStream_t, default priority, in order */
+    void *ev[2];  /* hipEvent_t pair of the region timer */
+    void *scratch;          /* backend-owned device scratch (split-K partials) */
+    size_t scratch_bytes;
+};
+
+/* Select a device and create its stream (ocl_init, ocl_backend.h:57-59).
+ * device_opt: NULL, "auto", "gpu" or a device ordinal "0".."N-1";
+ * platform_opt: NULL, "" or a substring of "HIP" / "AMD" (anything else
+ * matches no device); profile_opt: NULL, "auto" or "dgpu";
+ * precision_opt: NULL or "fp32" (exact path, f32 MFMA), "fp16" (weight
+ * matrices stored as half, float arithmetic, as the reference) or
+ * "bf16" (bf16 MFMA with f32 accumulation for attention and the GEMMs).
+ * Fatal if no device matches. I_SAM3_OPENCL_PROFILE in the environment
+ * switches on per-kernel timing, as in the reference. */
+void hipb_init(struct hipb_backend *b, const char *device_opt,
+               const char *platform_opt, const char *profile_opt,
+               const char *precision_opt);
+
+const char *hipb_arch_name(int arch);                 /* ocl_arch_name */
+void hipb_free(struct hipb_backend *b);                 /* ocl_free */
+const char *hipb_errstr(int err);                       /* ocl_errstr */
+void hipb_check(int err, const char *what);             /* ocl_check */
+
+/* Allocate n bytes of float storage, fatal on failure (ocl_alloc). */
+hipb_mem hipb_alloc(struct hipb_backend *b, size_t n, const char *what);
+/* Allocate count elements of the given HIPB_* type (no counterpart: the
+ * reference only has float buffers plus half weights). */
+hipb_mem hipb_alloc_typed(struct hipb_backend *b, size_t count, int dtype,
+                          const char *what);
+/* Allocate and fill from host memory (ocl_upload). */
+hipb_mem hipb_upload(struct hipb_backend *b, const void *src, size_t n,
+                     const char *what);
+/* Weight matrix used only as GEMM operand B: half with precision=fp16,
+ * bf16 with precision=bf16, else float (ocl_upload_weight). */
+hipb_mem hipb_upload_weight(struct hipb_backend *b, const float *src,
+                            size_t count, const char *what);
+int hipb_is_half(hipb_mem m);                           /* ocl_is_half */
+/* Blocking transfers at byte offsets (ocl_write / ocl_read). */
+void hipb_write(struct hipb_backend *b, hipb_mem dst, size_t off,
+                const void *src, size_t n);
+void hipb_read(struct hipb_backend *b, hipb_mem src, size_t off, void *dst,
+               size_t n);
+/* Release and set to NULL (ocl_release). */
+void hipb_release(hipb_mem *m);
+/* Wait for all queued work (clFinish(ocl->queue), sam3_model.c:1140). */
+void hipb_finish(struct hipb_backend *b);
+/* Device copy on the stream (clEnqueueCopyBuffer, sam3_model.c:1266). */
+void hipb_copy(struct hipb_backend *b, hipb_mem src, hipb_mem dst,
+               size_t src_off, size_t dst_off, size_t n);
+
+/* Error mode and the last recorded error (NULL if none). */
+void hipb_set_error_mode(int mode);
+const char *hipb_last_error(void);
+void hipb_clear_error(void);
+
+/* Per-kernel profile, the reference's run() table (sam3_model.c:149-207):
+ * with b->profile set every launch is timed with events on the stream
+ * and accumulated per kernel name with its algorithmic FLOPs. */
+int hipb_prof_count(void);
+int hipb_prof_entry(int i, const char **what, double *ms, double *wall_ms,
+                    double *flops, long *calls);
+void hipb_prof_reset(void);
+void hipb_prof_print(void);
+
+/* Region timer: events recorded on the backend's stream around the work
+ * queued between start and stop; stop waits and returns milliseconds. */
+void hipb_timer_start(struct hipb_backend *b);
+float hipb_timer_stop(struct hipb_backend *b);
+
+/* ------------------------------------------------------------------ */
+/* Operators (sam3_ops.h and the attention helpers of sam3_model.c)    */
+/* ------------------------------------------------------------------ */
+
+#define ACT_NONE 0
+#define ACT_GELU 1
+#define ACT_RELU 2
+
+/* One GEMM operand: buffer, element offset, leading dimension and the
+ * two batch strides (sam3_ops.h:19-24). */
+struct opnd {
+    hipb_mem buf;
+    long off;
+    int ld;
+    long s0, s1;
+};
+
+/* One ViT block (sam3_model.h:21-25). Weights uploaded with
+ * hipb_upload_weight (qkvw, projw, l1w, l2w) or hipb_upload. */
+struct vit_block {
+    hipb_mem n1w, n1b, qkvw, qkvb, projw, projb, n2w, n2b;
+    hipb_mem l1w, l1b, l2w, l2b;
+    int window; /* Window side, 0 for global attention. */
+};
+
+/* The part of struct sam_model (sam3_model.h:41-117) the attention path
+ * reads and writes. */
+struct sam_model {
+    struct hipb_backend *hip; /* the reference's m->ocl */
+    int embed, depth, heads, hd, mlp;
+    int grid; /* token grid side, SAM_GRID = 72 in the reference */
+    struct vit_block *blocks;
+    hipb_mem rope_win, rope_glob; /* (cos, sin) per position, hd/2 each */
+    long score_cap;               /* floats of the score buffer */
+    /* Encoder work buffers (sam3_model.c:847-854). */
+    hipb_mem x, xn, xw, qkv, scores, attn;
+    /* precision=bf16 staging: LN output and packed Q, K, V^T. */
+    hipb_mem xn16, q16, k16, vt16;
+};
+
+/* Set up m for the attention path on backend b and allocate its work
+ * buffers for the given blocks, sized like alloc_buffers
+ * (sam3_model.c:815-854): rows = max over blocks of nwin * N, score
+ * buffer = min(max_alloc, 512 MiB); fatal if one head's scores do not
+ * fit (sam3_model.c:833-837). No counterpart: the reference does this
+ * inside sam_load. */
+void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
+                   int embed, int heads, int hd, struct vit_block *blocks,
+                   int depth);
+void sam_path_free(struct sam_model *m);
+
+struct opnd mat(hipb_mem buf, long off, int ld);                 /* ops.h:48 */
+struct opnd bmat(hipb_mem buf, long off, int ld, long s0, long s1); /* ops.h:49 */
+
+/* Batched C = act(alpha * A * op(B) + bias) + R (sam3_ops.h:51-54,
+ * contract sam3_kernels.cl:57-69). A and C are float (C may be bf16 and
+ * A bf16 with precision=bf16); B may be half or bf16 weights. R may
+ * alias C. */
+void gemm(struct sam_model *m, int M, int N, int K, struct opnd A,
+          struct opnd B, int transb, struct opnd C, int nb, int nb1,
+          hipb_mem bias, hipb_mem R, long roff, float alpha, int act);
+
+/* Y[rows, out] = act(X[rows, in] W^T + b) (+ Y when residual)
+ * (sam3_ops.h:56-58). */
+void linear(struct sam_model *m, int rows, int in, int out, hipb_mem X,
+            long xoff, hipb_mem W, hipb_mem b, hipb_mem Y, long yoff, int act,
+            int residual);
+
+/* Row LayerNorm, Y may alias X (sam3_ops.h:60-61). */
+void layernorm(struct sam_model *m, long rows, int C, hipb_mem X, hipb_mem Y,
+               hipb_mem g, hipb_mem b, float eps, int act);
+
+/* out[i] = a[i] + b[i % bmod]; out may alias a (sam3_ops.h:63-65). */
+void add_bcast(struct sam_model *m, hipb_mem out, hipb_mem a, hipb_mem b,
+               long n, long bmod);
+
+/* In-place softmax of rows of L floats (sam3_model.c:332-341). */
+void softmax_rows(struct sam_model *m, hipb_mem S, long rows, int L);
+
+/* In-place RoPE of the q and k thirds of m->qkv rows at position
+ * r % npos (sam3_model.c:965-978). */
+void rope_apply(struct sam_model *m, hipb_mem table, long rows, int npos);
+
+/* H x H token grid -> ws x ws windows and back with residual add
+ * (sam3_model.c:360-392). */
+void window_partition(struct sam_model *m, hipb_mem X, hipb_mem out, int H,
+                      int C, int ws, int nwx);
+void window_unpartition_add(struct sam_model *m, hipb_mem X, hipb_mem Wd,
+                            int H, int C, int ws, int nwx);
+
+/* Decoder multi-head attention on projected tensors, 8 heads of width
+ * dint / 8, per-prompt element strides (0 = shared by all prompts)
+ * (sam3_model.c:413-451). Nk > 64 requires dint / 8 == 16, else fatal
+ * "mha: unsupported shape", as the reference. */
+void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
+         long sq, hipb_mem kp, long sk, hipb_mem vp, long sv, hipb_mem o);
+
+/* Fused softmax attention of nb independent (window, head) units of N
+ * tokens and head width 64: O = softmax(scale * rope(Q) rope(K)^T) V.
+ * Q, K, V and O use the operand addressing of gemm (batch b split as
+ * (b / nb1, b % nb1) with strides s0/s1, rows of ld elements), so the
+ * operands of the reference's QK^T and PV calls (sam3_model.c:1004-1011)
+ * apply unchanged. rope (NULL for none) rotates Q and K rows at position
+ * i % npos of the unit. With precision=bf16 the product runs on bf16
+ * MFMA with f32 accumulation; otherwise on f32 MFMA. Replaces the
+ * gemm -> softmax_rows -> gemm loop of sam3_model.c:1000-1013. */
+void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
+                struct opnd K, struct opnd V, struct opnd O, hipb_mem rope,
+                int npos, float scale);
+
+/* Attention region of one ViT block (sam3_model.c:981-1013): norm1,
+ * window partition, QKV projection, RoPE and attention of m->x into
+ * m->attn (rows = nwin * N, window-partitioned for windowed blocks).
+ * With unfused != 0 it replays the reference's operator sequence
+ * (gemm -> softmax_rows -> gemm per head chunk, through m->scores). */
+void vit_attention(struct sam_model *m, const struct vit_block *blk,
+                   int unfused);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3_HIP_H */

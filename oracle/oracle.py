@@ -1,0 +1,237 @@
+"""ctypes view of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke()
+as the checker, and by the cpu_baseline leg of bench.py. The product
+library never imports or calls it.
+
+Every wrapper takes and returns numpy float32 arrays in the reference's
+token-major layout; see sam3_oracle.h for the reference file:line each
+function restates.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+ACT_NONE, ACT_GELU, ACT_RELU = 0, 1, 2
+GEMM_SEQ, GEMM_CPU_T = 0, 1
+
+_lib = None
+
+_f = ctypes.c_float
+_i = ctypes.c_int
+_l = ctypes.c_long
+_p = ctypes.c_void_p
+
+
+def build():
+    """Compile liboracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        gemm_args = [_i, _i, _i, _p, _l, _i, _l, _l, _p, _l, _i, _l, _l, _i,
+                     _p, _l, _i, _l, _l, _i, _i, _p, _p, _l, _f, _i]
+        L.or_gemm.argtypes = [_i] + gemm_args
+        L.or_gemm_dispatch.argtypes = [_i] + gemm_args
+        L.or_softmax_rows.argtypes = [_p, _l, _i]
+        L.or_layernorm.argtypes = [_p, _p, _l, _i, _p, _p, _f, _i]
+        L.or_rope_apply.argtypes = [_p, _l, _i, _i, _i, _p]
+        L.or_window_partition.argtypes = [_p, _p, _i, _i, _i, _i, _i]
+        L.or_window_unpartition_add.argtypes = [_p, _p, _i, _i, _i, _i, _i]
+        L.or_add_bcast.argtypes = [_p, _p, _p, _l, _l]
+        att = [_p, _l, _p, _l, _p, _l, _p, _i, _i, _i, _i, _i, _f]
+        L.or_attn_fewkeys.argtypes = att
+        L.or_attn_manykeys.argtypes = att
+        L.or_mha.argtypes = [_i, _i, _i, _i, _p, _l, _p, _l, _p, _l, _p]
+        L.or_mha.restype = _i
+        L.or_vit_attention.argtypes = [_i, _p, _i, _i, _i, _i, _i, _p, _p, _p,
+                                       _p, _p, _l, _p, _p]
+        L.or_vit_attention.restype = _i
+        L.or_sdpa_f64.argtypes = [_i, _i, _i, _p, _i, _p, _i, _p, _i, _p, _i,
+                                  ctypes.c_double]
+        L.or_threads.restype = _i
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def threads():
+    return lib().or_threads()
+
+
+def gemm(kind, M, N, K, A, aoff, lda, sa0, sa1, B, boff, ldb, sb0, sb1,
+         transb, C, coff, ldc, sc0, sc1, nb, nb1, bias=None, R=None, roff=0,
+         alpha=1.0, act=ACT_NONE, dispatch_cpu=None):
+    """C (updated in place) = act(alpha A op(B) + bias) + R.
+
+    kind is GEMM_SEQ or GEMM_CPU_T; with dispatch_cpu set, the kernel is
+    chosen the way sam3_model.c:230-302 chooses it instead. R may be C.
+    """
+    args = (M, N, K, _ptr(A), aoff, lda, sa0, sa1, _ptr(B), boff, ldb, sb0,
+            sb1, transb, _ptr(C), coff, ldc, sc0, sc1, nb, nb1, _ptr(bias),
+            _ptr(R), roff, alpha, act)
+    if dispatch_cpu is None:
+        lib().or_gemm(kind, *args)
+    else:
+        lib().or_gemm_dispatch(int(dispatch_cpu), *args)
+    return C
+
+
+def linear(X, W, b=None, act=ACT_NONE, cpu=True, Y=None, residual=False):
+    """Y = act(X W^T + b) (+ Y), as linear() (sam3_model.c:305-310)."""
+    X = _f32(X)
+    W = _f32(W)
+    rows, nin = X.shape
+    nout = W.shape[0]
+    if Y is None:
+        Y = np.zeros((rows, nout), np.float32)
+    b = None if b is None else _f32(b)
+    gemm(0, rows, nout, nin, X, 0, nin, 0, 0, W, 0, nin, 0, 0, 1, Y, 0, nout,
+         0, 0, 1, 1, b, Y if residual else None, 0, 1.0, act, dispatch_cpu=cpu)
+    return Y
+
+
+def softmax_rows(S):
+    S = _f32(S).copy()
+    L = S.shape[-1]
+    lib().or_softmax_rows(_ptr(S), S.size // L, L)
+    return S
+
+
+def layernorm(X, g, b, eps=1e-5, act=ACT_NONE):
+    X = _f32(X)
+    C = X.shape[-1]
+    Y = np.empty_like(X)
+    g = _f32(g)
+    b = _f32(b)
+    lib().or_layernorm(_ptr(X), _ptr(Y), X.size // C, C, _ptr(g), _ptr(b),
+                       eps, act)
+    return Y
+
+
+def rope_apply(qkv, E, hd, npos, cs):
+    """In-place RoPE on a copy of qkv [rows, 3E]; cs is [npos, hd/2, 2]."""
+    qkv = _f32(qkv).copy()
+    cs = _f32(cs)
+    lib().or_rope_apply(_ptr(qkv), qkv.size // (3 * E), E, hd, npos, _ptr(cs))
+    return qkv
+
+
+def window_partition(X, H, W, C, ws):
+    nwx = (H + ws - 1) // ws
+    out = np.empty((nwx * nwx * ws * ws, C), np.float32)
+    X = _f32(X)
+    lib().or_window_partition(_ptr(X), _ptr(out), H, W, C, ws, nwx)
+    return out
+
+
+def window_unpartition_add(X, Wd, H, W, C, ws):
+    nwx = (H + ws - 1) // ws
+    X = _f32(X).copy()
+    Wd = _f32(Wd)
+    lib().or_window_unpartition_add(_ptr(X), _ptr(Wd), H, W, C, ws, nwx)
+    return X
+
+
+def add_bcast(a, b, bmod):
+    a = _f32(a)
+    out = np.empty_like(a)
+    b = _f32(b)
+    lib().or_add_bcast(_ptr(out), _ptr(a), _ptr(b), a.size, bmod)
+    return out
+
+
+def attn_fewkeys(Q, sq, K, sk, V, sv, P, Nq, Nk, dint, c, scale):
+    O = np.zeros((P * Nq, dint), np.float32)
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    lib().or_attn_fewkeys(_ptr(Q), sq, _ptr(K), sk, _ptr(V), sv, _ptr(O), P,
+                          Nq, Nk, dint, c, scale)
+    return O
+
+
+def attn_manykeys(Q, sq, K, sk, V, sv, P, Nq, Nk, dint, c, scale):
+    O = np.zeros((P * Nq, dint), np.float32)
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    lib().or_attn_manykeys(_ptr(Q), sq, _ptr(K), sk, _ptr(V), sv, _ptr(O), P,
+                           Nq, Nk, dint, c, scale)
+    return O
+
+
+def mha(P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv):
+    O = np.zeros((P * Nq, dint), np.float32)
+    qp, kp, vp = _f32(qp), _f32(kp), _f32(vp)
+    rc = lib().or_mha(P, Nq, Nk, dint, _ptr(qp), sq, _ptr(kp), sk, _ptr(vp),
+                      sv, _ptr(O))
+    if rc != 0:
+        raise ValueError("mha: unsupported shape")
+    return O
+
+
+def vit_attention(x, grid, E, heads, hd, ws, n1w, n1b, qkvw, qkvb, rope,
+                  score_cap=(512 << 20) // 4, cpu=True, want_qkv=False):
+    """Attention region of one ViT block; returns attn [rows, E] (and qkv)."""
+    s = ws if ws else grid
+    nwx = (grid + s - 1) // s
+    rows = nwx * nwx * s * s
+    attn = np.zeros((rows, E), np.float32)
+    qkv = np.zeros((rows, 3 * E), np.float32) if want_qkv else None
+    x, n1w, n1b = _f32(x), _f32(n1w), _f32(n1b)
+    qkvw, qkvb, rope = _f32(qkvw), _f32(qkvb), _f32(rope)
+    hc = lib().or_vit_attention(int(cpu), _ptr(x), grid, E, heads, hd, ws,
+                                _ptr(n1w), _ptr(n1b), _ptr(qkvw), _ptr(qkvb),
+                                _ptr(rope), score_cap, _ptr(attn), _ptr(qkv))
+    if hc < 1:
+        raise ValueError("score buffer cannot hold one head")
+    return (attn, qkv) if want_qkv else attn
+
+
+def sdpa_f64(Q, K, V, scale):
+    Q = np.ascontiguousarray(Q, np.float64)
+    K = np.ascontiguousarray(K, np.float64)
+    V = np.ascontiguousarray(V, np.float64)
+    Nq, d = Q.shape
+    Nk = K.shape[0]
+    dv = V.shape[1]
+    assert dv == d
+    O = np.zeros((Nq, d), np.float64)
+    lib().or_sdpa_f64(Nq, Nk, d, _ptr(Q), d, _ptr(K), d, _ptr(V), d, _ptr(O),
+                      d, scale)
+    return O
+
+
+def rope_table(side, hd=64, theta=10000.0):
+    """Synthetic axial 2D RoPE table [side*side, hd/2, 2] of (cos, sin).
+
+    Frequencies f_k = theta^(-4k/hd) for k < hd/4; pair k < hd/4 rotates
+    by x * f_k and pair hd/4 + k by y * f_k at position p = y * side + x.
+    The reference reads this table from its checkpoint; here it is an
+    input shared by both sides.
+    """
+    nf = hd // 2
+    q = nf // 2
+    f = theta ** (-4.0 * np.arange(q, dtype=np.float64) / hd)
+    pos = np.arange(side * side)
+    x = (pos % side).astype(np.float64)
+    y = (pos // side).astype(np.float64)
+    ang = np.concatenate([np.outer(x, f), np.outer(y, f)], axis=1)
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)

@@ -1,0 +1,117 @@
+/* CPU oracle for the SAM 3 attention path of i.sam3.opencl.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library restates, in plain C on the
+ * host, the arithmetic of the reference OpenCL kernels (sam3_kernels.cl)
+ * and of their host dispatch (sam3_model.c) for the attention path. It
+ * is the checker of the HIP path and the CPU baseline of bench.py; it is
+ * never linked into, loaded by or called from the product library.
+ *
+ * Conventions follow the reference: activations are token-major fp32,
+ * GEMM operands are (pointer, element offset, leading dimension, two
+ * batch strides) with batch index b split into (b / nb1, b % nb1)
+ * (sam3_kernels.cl:57-69). mad()/contracted a * b + c is taken as a
+ * fused multiply-add, the form clang emits for OpenCL C on both PoCL and
+ * ROCm; the runtime's exp/erf/rsqrt are taken from the C library. Both
+ * choices are only visible at the level of the last bit and are listed
+ * as unpinned where the oracle's tests document them.
+ */
+#ifndef SAM3_ORACLE_H
+#define SAM3_ORACLE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_ACT_NONE 0
+#define OR_ACT_GELU 1
+#define OR_ACT_RELU 2
+
+/* GEMM arithmetic variants of the reference. */
+#define OR_GEMM_SEQ 0   /* gemm, gemm_big, gemm_cpu_n: sequential mad over k */
+#define OR_GEMM_CPU_T 1 /* gemm_cpu_t: 8 float lanes along k, hsum8, tail */
+
+/* Batched C = act(alpha * A * op(B) + bias) + R with the reference's
+ * operand contract (sam3_kernels.cl:57-69). kind selects the arithmetic
+ * (OR_GEMM_SEQ / OR_GEMM_CPU_T). R may alias C. */
+void or_gemm(int kind, int M, int N, int K, const float *A, long aoff, int lda,
+             long sa0, long sa1, const float *B, long boff, int ldb, long sb0,
+             long sb1, int transb, float *C, long coff, int ldc, long sc0,
+             long sc1, int nb, int nb1, const float *bias, const float *R,
+             long roff, float alpha, int act);
+
+/* The host dispatcher gemm() of sam3_model.c:230-302: with profile=cpu
+ * (cpu != 0) gemm_cpu_t for transb, gemm_cpu_n otherwise; on a GPU
+ * profile gemm or gemm_big, which share the sequential arithmetic. */
+void or_gemm_dispatch(int cpu, int M, int N, int K, const float *A, long aoff,
+                      int lda, long sa0, long sa1, const float *B, long boff,
+                      int ldb, long sb0, long sb1, int transb, float *C,
+                      long coff, int ldc, long sc0, long sc1, int nb, int nb1,
+                      const float *bias, const float *R, long roff,
+                      float alpha, int act);
+
+/* In-place row softmax, one reference work-group of ls items per row
+ * (sam3_kernels.cl:637-656, host sam3_model.c:332-341). */
+void or_softmax_rows(float *S, long rows, int L);
+
+/* Row LayerNorm, Y may alias X (sam3_kernels.cl:489-514, host
+ * sam3_model.c:314-330). */
+void or_layernorm(const float *X, float *Y, long rows, int C, const float *g,
+                  const float *b, float eps, int act);
+
+/* In-place 2D RoPE of the q and k thirds of fused qkv rows
+ * (sam3_kernels.cl:679-698, host sam3_model.c:965-978). cs holds
+ * (cos, sin) pairs, hd / 2 per position. */
+void or_rope_apply(float *qkv, long rows, int E, int hd, int npos,
+                   const float *cs);
+
+/* Window partition / inverse with residual add (sam3_kernels.cl:712-741,
+ * host sam3_model.c:360-392). */
+void or_window_partition(const float *X, float *out, int H, int W, int C,
+                         int ws, int nwx);
+void or_window_unpartition_add(float *X, const float *Wd, int H, int W, int C,
+                               int ws, int nwx);
+
+/* out[i] = a[i] + b[i % bmod] (sam3_kernels.cl:700-708). */
+void or_add_bcast(float *out, const float *a, const float *b, long n,
+                  long bmod);
+
+/* Decoder attention kernels (sam3_kernels.cl:527-633) and their
+ * dispatcher mha() (sam3_model.c:413-451); 8 heads, head width
+ * c = dint / 8. Returns 0, or -1 for the shape mha() rejects. */
+void or_attn_fewkeys(const float *Q, long sq, const float *K, long sk,
+                     const float *V, long sv, float *O, int P, int Nq, int Nk,
+                     int dint, int c, float scale);
+void or_attn_manykeys(const float *Q, long sq, const float *K, long sk,
+                      const float *V, long sv, float *O, int P, int Nq,
+                      int Nk, int dint, int c, float scale);
+int or_mha(int P, int Nq, int Nk, int dint, const float *qp, long sq,
+           const float *kp, long sk, const float *vp, long sv, float *o);
+
+/* Attention region of one ViT block (sam3_model.c:981-1013):
+ * layernorm(norm1) -> [window_partition] -> linear(qkv) -> rope_apply ->
+ * per head chunk {gemm(Q K^T, alpha 1/sqrt(hd)) -> softmax_rows ->
+ * gemm(P V)}. x is the grid x grid x E token map; ws = 0 is global
+ * attention. Writes the attention output (rows x E, window-partitioned
+ * order for windowed blocks) to attn and, if qkv_out is not NULL, the
+ * post-RoPE qkv rows (rows x 3E). score_cap is the score buffer size in
+ * floats (sam3_model.c:826-828). Returns the head chunk used, or -1 if
+ * one head does not fit. */
+int or_vit_attention(int cpu, const float *x, int grid, int E, int heads,
+                     int hd, int ws, const float *n1w, const float *n1b,
+                     const float *qkvw, const float *qkvb, const float *rope,
+                     long score_cap, float *attn, float *qkv_out);
+
+/* Brute-force scaled dot-product attention in double precision,
+ * O[i, :] = sum_j softmax_j(scale * q_i . k_j) v_j, for pinning. */
+void or_sdpa_f64(int Nq, int Nk, int d, const double *Q, int ldq,
+                 const double *K, int ldk, const double *V, int ldv, double *O,
+                 int ldo, double scale);
+
+/* Number of OpenMP threads the oracle runs on. */
+int or_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAM3_ORACLE_H */

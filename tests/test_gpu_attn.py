@@ -1,0 +1,184 @@
+"""GPU parity of the fused attention path against the oracle.
+
+Oracle = the reference's profile=cpu operator sequence restated on the
+CPU (rope_apply, gemm_cpu_t with alpha 1/8, softmax_rows, gemm_cpu_n).
+Bars: rel-L2 <= 2e-5 for the fp32 path, <= 2e-2 for the bf16 path; the
+max-abs error is printed with every check.
+
+Full-size workloads (9 x 576 windows, 5184 global tokens) are checked on
+sampled (unit, head, query-row) sets: the QKV projection rows against the
+oracle's LayerNorm + linear, and the attention rows against the oracle's
+attention of the same rows computed from the device's qkv.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from gpu_common import block_inputs, oracle_attn_rows, rel_l2, report
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 2e-5, "bf16": 2e-2}
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam3_hip
+    return sam3_hip
+
+
+@pytest.fixture(scope="module", params=["fp32", "bf16"])
+def be(hip, request):
+    b = hip.Backend(precision=request.param)
+    b.precision = request.param
+    yield b
+    b.free()
+
+
+def _oracle_units(orc, qkv, N, nunits, heads, E, table):
+    """Oracle attention of every (unit, head) of a [nunits * N, 3E] qkv."""
+    out = np.zeros((nunits * N, E), np.float32)
+    for u in range(nunits):
+        unit = qkv[u * N:(u + 1) * N]
+        for h in range(heads):
+            out[u * N:(u + 1) * N, h * 64:(h + 1) * 64] = oracle_attn_rows(
+                unit, E, h, np.arange(N), table)
+    return out
+
+
+def test_single_window(hip, be, orc):
+    """One 576-token window, 16 heads x 64, N(0,1), no mask, no RoPE."""
+    N, H, E = 576, 16, 1024
+    m = hip.Model(be, embed=E, heads=H)
+    qkv = np.random.default_rng(11).standard_normal((N, 3 * E), np.float32)
+    dq = be.upload(qkv)
+    do = be.alloc(N * E * 4)
+    hip.attn_fused(m, N, H, H, hip.bmat(dq, 0, 3 * E, 0, 64),
+                   hip.bmat(dq, E, 3 * E, 0, 64),
+                   hip.bmat(dq, 2 * E, 3 * E, 0, 64),
+                   hip.bmat(do, 0, E, 0, 64), None, 1, 0.125)
+    got = be.read(do).reshape(N, E)
+    want = _oracle_units(orc, qkv, N, 1, H, E, None)
+    assert report("single window %s" % be.precision, got, want) <= TOL[be.precision]
+    be.release(dq)
+    be.release(do)
+
+
+@pytest.mark.parametrize("N,nunits", [(37, 3), (100, 2), (200, 1), (64, 2)])
+def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
+    """Token counts that are not multiples of the 32/64-key blocks or the
+    128-query tiles, RoPE on Q and K, several units with batch strides."""
+    H, E = 2, 128
+    m = hip.Model(be, embed=E, heads=H)
+    side = math.isqrt(N)
+    table = orc.rope_table(side + 1)[:N] if side * side != N else orc.rope_table(side)
+    qkv = np.random.default_rng(N).standard_normal((nunits * N, 3 * E), np.float32)
+    dq, dt = be.upload(qkv), be.upload(table)
+    do = be.alloc(nunits * N * E * 4)
+    st = N * 3 * E
+    hip.attn_fused(m, N, nunits * H, H, hip.bmat(dq, 0, 3 * E, st, 64),
+                   hip.bmat(dq, E, 3 * E, st, 64),
+                   hip.bmat(dq, 2 * E, 3 * E, st, 64),
+                   hip.bmat(do, 0, E, N * E, 64), dt, N, 0.125)
+    got = be.read(do).reshape(nunits * N, E)
+    want = _oracle_units(orc, qkv, N, nunits, H, E, table)
+    assert report("ragged N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
+
+
+def test_attention_closed_forms(hip, be):
+    """Zero queries give the mean of V; one token gives V itself."""
+    E, H = 128, 2
+    m = hip.Model(be, embed=E, heads=H)
+    for N in (1, 300):
+        qkv = np.random.default_rng(N).standard_normal((N, 3 * E), np.float32)
+        qkv[:, :E] = 0.0
+        dq = be.upload(qkv)
+        do = be.alloc(N * E * 4)
+        hip.attn_fused(m, N, H, H, hip.bmat(dq, 0, 3 * E, 0, 64),
+                       hip.bmat(dq, E, 3 * E, 0, 64),
+                       hip.bmat(dq, 2 * E, 3 * E, 0, 64),
+                       hip.bmat(do, 0, E, 0, 64), None, 1, 0.125)
+        got = be.read(do).reshape(N, E)
+        want = np.broadcast_to(qkv[:, 2 * E:].astype(np.float64).mean(0), (N, E))
+        tol = 1e-6 if be.precision == "fp32" else 1e-2
+        assert rel_l2(got, want) <= tol
+
+
+def _vit_small(hip, be, orc, grid, ws, unfused=False, E=128):
+    H = E // 64
+    x, n1w, n1b, w, b = block_inputs(grid + ws, grid, E)
+    s = ws if ws else grid
+    table = orc.rope_table(s)
+    blk = hip.VitBlock()
+    blk.n1w, blk.n1b = be.upload(n1w), be.upload(n1b)
+    blk.qkvw, blk.qkvb = be.upload_weight(w), be.upload(b)
+    blk.window = ws
+    m = hip.Model(be, grid=grid, embed=E, heads=H, blocks=[blk])
+    if ws:
+        m.m.rope_win = be.upload(table)
+    else:
+        m.m.rope_glob = be.upload(table)
+    be.write(m.m.x, 0, x)
+    hip.vit_attention(m, blk, unfused)
+    nwx = -(-grid // s)
+    rows = nwx * nwx * s * s
+    got = be.read(m.m.attn, rows * E).reshape(rows, E)
+    want = orc.vit_attention(x, grid, E, H, 64, ws, n1w, n1b, w, b, table)
+    m.free()
+    return got, want
+
+
+@pytest.mark.parametrize("grid,ws", [(12, 6), (12, 0), (10, 4)])
+@pytest.mark.parametrize("unfused", [False, True])
+def test_vit_attention_small(hip, be, orc, grid, ws, unfused):
+    got, want = _vit_small(hip, be, orc, grid, ws, unfused)
+    assert report("vit_attention grid=%d ws=%d unfused=%d %s" %
+                  (grid, ws, unfused, be.precision), got, want) <= TOL[be.precision]
+
+
+@pytest.mark.parametrize("ws", [24, 0])
+def test_vit_attention_full_size(hip, be, orc, ws):
+    """72 x 72 grid, width 1024, 16 heads: 9 windows of 576 tokens (ws=24)
+    or global attention over 5184 tokens (ws=0)."""
+    grid, E, H = 72, 1024, 16
+    x, n1w, n1b, w, b = block_inputs(7 + ws, grid, E)
+    s = ws if ws else grid
+    N = s * s
+    table = orc.rope_table(s)
+    blk = hip.VitBlock()
+    blk.n1w, blk.n1b = be.upload(n1w), be.upload(n1b)
+    blk.qkvw, blk.qkvb = be.upload_weight(w), be.upload(b)
+    blk.window = ws
+    m = hip.Model(be, grid=grid, embed=E, heads=H, blocks=[blk])
+    if ws:
+        m.m.rope_win = be.upload(table)
+    else:
+        m.m.rope_glob = be.upload(table)
+    be.write(m.m.x, 0, x)
+    hip.vit_attention(m, blk)
+    rows = grid * grid
+    attn = be.read(m.m.attn, rows * E).reshape(rows, E)
+    qkv = be.read(m.m.qkv, rows * 3 * E).reshape(rows, 3 * E)
+
+    # QKV projection of sampled rows against LayerNorm + linear.
+    xn = orc.layernorm(x, n1w, n1b)
+    xw = orc.window_partition(xn, grid, grid, E, s) if ws else xn
+    pick = np.random.default_rng(0).choice(rows, 64, replace=False)
+    want_qkv = orc.linear(xw[pick], w, b, cpu=True)
+    assert report("qkv rows ws=%d %s" % (ws, be.precision), qkv[pick],
+                  want_qkv) <= TOL[be.precision]
+
+    # Attention of sampled (unit, head, rows) from the device's qkv.
+    g = np.random.default_rng(1)
+    nunits = rows // N
+    got, want = [], []
+    for trial in range(3):
+        u, h = int(g.integers(nunits)), int(g.integers(H))
+        qrows = np.sort(g.choice(N, 64, replace=False))
+        unit = qkv[u * N:(u + 1) * N]
+        want.append(oracle_attn_rows(unit, E, h, qrows, table))
+        got.append(attn[u * N + qrows, h * 64:(h + 1) * 64])
+    assert report("attention rows ws=%d %s" % (ws, be.precision),
+                  np.concatenate(got), np.concatenate(want)) <= TOL[be.precision]
+    m.free()

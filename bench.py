@@ -1,0 +1,301 @@
+"""Attention-path benchmark on one MI355X.
+
+Step = one pass of the fused attention of a global ViT block: 5184 tokens
+(72 x 72 grid), 16 heads of 64, 2D RoPE, bf16 MFMA with f32 accumulation,
+operands resident in HBM (packed by the block's LayerNorm -> QKV
+projection -> packing, which run before the timed region). `value` is
+attention TFLOP/s = 4 * 5184^2 * 64 * 16 FLOP per step / step time; the
+same JSON line reports the 9 x 576 windowed batch, the fp32 exact path,
+the QKV projection GEMM, the whole attention region, the mask-decoder
+cross-attention (GB/s), the dominant kernel's roofline and the CPU
+baseline (the oracle's restatement of the reference's profile=cpu
+sequence on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import importlib.util
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "i.sam3.opencl_amd")
+
+METRIC = ("attention TFLOP/s + % MFMA peak (5184-tok global, 9×576 "
+          "window); backbone ms/img")
+PEAK_BF16 = 2516.6   # TFLOP/s, dense bf16 MFMA, MI355X
+PEAK_F32 = 157.3     # TFLOP/s, f32 MFMA
+PEAK_HBM = 8000.0    # GB/s
+
+
+def load_hip():
+    spec = importlib.util.spec_from_file_location(
+        "sam3_hip", os.path.join(PKG, "sam3_hip.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["sam3_hip"] = mod
+    spec.loader.exec_module(mod)
+    mod.lib()
+    return mod
+
+
+def rope_table(side, hd=64, theta=10000.0):
+    """Axial 2D RoPE (cos, sin) table: pair k < 16 rotates by x * f_k,
+    pair 16 + k by y * f_k, f_k = theta^(-4k/64), position y * side + x."""
+    f = theta ** (-4.0 * np.arange(hd // 4) / hd)
+    pos = np.arange(side * side)
+    ang = np.concatenate([np.outer(pos % side, f), np.outer(pos // side, f)], 1)
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+def block_inputs(seed, grid=72, E=1024):
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((grid * grid, E), dtype=np.float32)
+    bound = math.sqrt(6.0 / (E + 3 * E))
+    w = g.uniform(-bound, bound, (3 * E, E)).astype(np.float32)
+    b = g.uniform(-1 / math.sqrt(E), 1 / math.sqrt(E), 3 * E).astype(np.float32)
+    return x, w, b
+
+
+class Block:
+    """One ViT block's attention region on the device (random init)."""
+
+    def __init__(self, hip, be, ws, seed, grid=72, E=1024, H=16):
+        self.hip, self.be, self.ws, self.E, self.H = hip, be, ws, E, H
+        x, w, b = block_inputs(seed, grid, E)
+        s = ws if ws else grid
+        self.N = s * s
+        self.nunits = ((grid + s - 1) // s) ** 2
+        blk = hip.VitBlock()
+        blk.n1w = be.upload(np.ones(E, np.float32))
+        blk.n1b = be.upload(np.zeros(E, np.float32))
+        blk.qkvw = be.upload_weight(w)
+        blk.qkvb = be.upload(b)
+        blk.window = ws
+        self.blk = blk
+        self.m = hip.Model(be, grid=grid, embed=E, heads=H, blocks=[blk])
+        tab = be.upload(rope_table(s))
+        if ws:
+            self.m.m.rope_win = tab
+        else:
+            self.m.m.rope_glob = tab
+        be.write(self.m.m.x, 0, x)
+        self.rows = self.nunits * self.N
+        self.out = hip.bmat(self.m.m.attn, 0, E, self.N * E, 64)
+
+    def flops(self):
+        return 4.0 * self.N * self.N * 64 * self.H * self.nunits
+
+    def region(self):
+        self.hip.vit_attention(self.m, self.blk)
+
+    def attn(self):
+        """The attention kernel alone on the packed operands."""
+        self.hip.attn_packed(self.m, self.N, self.nunits * self.H, self.H,
+                             self.out)
+
+    def attn_f32(self):
+        E, N = self.E, self.N
+        q = self.m.m.qkv
+        tab = self.m.m.rope_win if self.ws else self.m.m.rope_glob
+        self.hip.attn_fused(self.m, N, self.nunits * self.H, self.H,
+                            self.hip.bmat(q, 0, 3 * E, N * 3 * E, 64),
+                            self.hip.bmat(q, E, 3 * E, N * 3 * E, 64),
+                            self.hip.bmat(q, 2 * E, 3 * E, N * 3 * E, 64),
+                            self.out, tab, N, 0.125)
+
+    def qkv_gemm(self):
+        E = self.E
+        src = self.m.m.xn16 if self.m.m.xn16 else self.m.m.xn
+        self.hip.linear(self.m, self.rows, E, 3 * E, src, 0, self.blk.qkvw,
+                        self.blk.qkvb, self.m.m.qkv, 0, 0, 0)
+
+
+def timed(be, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    be.finish()
+    be.timer_start()
+    for _ in range(steps):
+        fn()
+    ms = be.timer_stop()
+    return ms / steps
+
+
+def cpu_baseline(steps=3):
+    """The oracle's restatement of the reference's profile=cpu attention of
+    the global block (gemm_cpu_t Q K^T with alpha 1/8 -> softmax_rows ->
+    gemm_cpu_n P V, 4 heads per score-buffer chunk), timed on the host
+    cores; median of `steps` after one warm-up."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+
+    N, H, E, hc = 5184, 16, 1024, 4
+    g = np.random.default_rng(5)
+    qkv = g.standard_normal((N, 3 * E), dtype=np.float32)
+    out = np.zeros((N, E), np.float32)
+    S = np.zeros((hc, N, N), np.float32)
+    lib = orc.lib()
+
+    def one():
+        for h0 in range(0, H, hc):
+            orc.gemm(orc.GEMM_CPU_T, N, N, 64, qkv, h0 * 64, 3 * E, 0, 64, qkv,
+                     E + h0 * 64, 3 * E, 0, 64, 1, S, 0, N, 0, N * N, hc, hc,
+                     alpha=0.125)
+            lib.or_softmax_rows(S.ctypes.data, hc * N, N)
+            orc.gemm(orc.GEMM_SEQ, N, 64, N, S, 0, N, 0, N * N, qkv,
+                     2 * E + h0 * 64, 3 * E, 0, 64, 0, out, h0 * 64, E, 0, 64,
+                     hc, hc)
+
+    one()
+    times = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    return {"value": round(4.0 * N * N * 64 * H / sec / 1e12, 5),
+            "unit": "TFLOP/s", "cores": orc.threads(), "kind": "port",
+            "sample": "full 5184-token global attention, 16 heads x 64, "
+                      "fp32, reference profile=cpu sequence restated in C "
+                      "(median of %d, %.2f s each)" % (steps, sec)}
+
+
+def decoder(hip, be, steps, warmup):
+    """Mask-decoder cross-attention, 64 prompts, per-prompt image keys
+    (layer >= 1 semantics): token->image (7 x 4096 keys) and
+    image->token (4096 queries x 7 keys), 8 heads x 16, fp32; GB/s of the
+    algorithmic bytes (Q, K, V read once, O written once)."""
+    P, T, NT, dint = 64, 4096, 7, 128
+    m = hip.Model(be, embed=128, heads=2)
+    g = np.random.default_rng(3)
+    img = be.upload(g.standard_normal((P * T, dint), dtype=np.float32))
+    img2 = be.upload(g.standard_normal((P * T, dint), dtype=np.float32))
+    tok = be.upload(g.standard_normal((P * NT, dint), dtype=np.float32))
+    tok2 = be.upload(g.standard_normal((P * NT, dint), dtype=np.float32))
+    o_t = be.alloc(P * NT * dint * 4)
+    o_i = be.alloc(P * T * dint * 4)
+    t2i = timed(be, lambda: hip.mha(m, P, NT, T, dint, tok, NT * dint, img,
+                                    T * dint, img2, T * dint, o_t), steps, warmup)
+    i2t = timed(be, lambda: hip.mha(m, P, T, NT, dint, img, T * dint, tok,
+                                    NT * dint, tok2, NT * dint, o_i), steps, warmup)
+    bytes_t2i = 4.0 * (P * NT * dint * 2 + 2 * P * T * dint)
+    bytes_i2t = 4.0 * (2 * P * T * dint + 2 * P * NT * dint)
+    for d in (img, img2, tok, tok2, o_t, o_i):
+        be.release(d)
+    return {
+        "t2i_ms": round(t2i, 4), "t2i_GBps": round(bytes_t2i / t2i / 1e6, 1),
+        "i2t_ms": round(i2t, 4), "i2t_GBps": round(bytes_i2t / i2t / 1e6, 1),
+        "pct_hbm_peak": round(100 * (bytes_t2i + bytes_i2t) / (t2i + i2t) /
+                              1e6 / PEAK_HBM, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the global bf16 attention kernel (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; the attention path "
+              "shards by image/crop with no exchange, see DESIGN.md. "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    hip = load_hip()
+    be = hip.Backend(precision="bf16")
+    glob = Block(hip, be, 0, seed=3)
+    glob.region()          # LN -> QKV -> pack -> attention; packs operands
+    be.finish()
+    if args.kernel_only:
+        ms = timed(be, glob.attn, args.steps, args.warmup)
+        print(json.dumps({"kernel": "attn_bf16 global", "ms": ms,
+                          "TFLOP/s": glob.flops() / ms / 1e9}))
+        return
+
+    ms = timed(be, glob.attn, args.steps, args.warmup)
+    tflops = glob.flops() / ms / 1e9
+    region_ms = timed(be, glob.region, max(5, args.steps // 5), 2)
+    qkv_ms = timed(be, glob.qkv_gemm, max(5, args.steps // 5), 2)
+    glob.region()
+    be.finish()
+
+    win = Block(hip, be, 24, seed=2)
+    win.region()
+    be.finish()
+    wms = timed(be, win.attn, args.steps, args.warmup)
+    w_region = timed(be, win.region, max(5, args.steps // 5), 2)
+
+    # fp32 exact path (f32 MFMA), same shapes, its own backend.
+    be32 = hip.Backend(precision="fp32")
+    g32 = Block(hip, be32, 0, seed=3)
+    g32.region()
+    be32.finish()
+    g32_ms = timed(be32, g32.attn_f32, max(3, args.steps // 10), 2)
+    w32 = Block(hip, be32, 24, seed=2)
+    w32.region()
+    be32.finish()
+    w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), 2)
+
+    dec = decoder(hip, be32, max(5, args.steps // 5), 2)
+
+    qkv_flops = 2.0 * 5184 * 1024 * 3072
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (x ~ N(0,1), LayerNorm, Xavier-uniform QKV, "
+                "axial RoPE theta 1e4; random init)",
+        "config": {"workload": "global self-attention of one ViT block: 5184 "
+                               "tokens (72x72), 16 heads x 64, 2D RoPE, bf16 "
+                               "MFMA f32 accumulate",
+                   "tokens": 5184, "heads": 16, "head_dim": 64,
+                   "parallelism": "none (1 GPU)"},
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16, 2),
+        "windowed": {"workload": "9 windows x 576 tokens, 16 heads x 64, bf16",
+                     "ms": round(wms, 5),
+                     "TFLOP/s": round(win.flops() / wms / 1e9, 2),
+                     "pct_bf16_peak": round(100 * win.flops() / wms / 1e9 /
+                                            PEAK_BF16, 2),
+                     "region_ms": round(w_region, 4)},
+        "global_region_ms": round(region_ms, 4),
+        "qkv_gemm_bf16": {"ms": round(qkv_ms, 4),
+                          "TFLOP/s": round(qkv_flops / qkv_ms / 1e9, 1)},
+        "fp32_exact": {
+            "global_ms": round(g32_ms, 4),
+            "global_TFLOP/s": round(glob.flops() / g32_ms / 1e9, 2),
+            "global_pct_f32_peak": round(100 * glob.flops() / g32_ms / 1e9 /
+                                         PEAK_F32, 1),
+            "windowed_ms": round(w32_ms, 4),
+            "windowed_TFLOP/s": round(win.flops() / w32_ms / 1e9, 2)},
+        "decoder_fp32": dec,
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": PEAK_BF16, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16, 4), "traffic": None,
+                     "kernel": "k_attn_bf16 (global, 5184 tokens x 16 heads)",
+                     "flops_per_launch": glob.flops()},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -473,6 +473,43 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
     hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)N * hd * nb);
 }
 
+void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
+{
+    struct hipb_backend *b = m->hip;
+    const size_t np = ((size_t)N + 63) / 64 * 64;
+    struct attn_desc d;
+    int err;
+
+    if (N < 1 || nb < 1 || nb1 < 1) {
+        hipb_fatal("attn_packed: invalid shape N=%d nb=%d nb1=%d", N, nb, nb1);
+        return;
+    }
+    if (!buf_ok("attn_packed", "q16", m->q16, (size_t)nb * np * 64, HIPB_BF16) ||
+        !buf_ok("attn_packed", "k16", m->k16, (size_t)nb * np * 64, HIPB_BF16) ||
+        !buf_ok("attn_packed", "vt16", m->vt16, (size_t)nb * np * 64,
+                HIPB_BF16) ||
+        !opnd_ok("attn_packed", "O", O, N, 64, nb, nb1))
+        return;
+    if (O.buf->dtype == HIPB_F16) {
+        hipb_fatal("attn_packed: O must be float or bf16");
+        return;
+    }
+    memset(&d, 0, sizeof(d));
+    d.N = N;
+    d.nb = nb;
+    d.nb1 = nb1;
+    d.O = O.buf->ptr;
+    d.ooff = O.off;
+    d.ldo = O.ld;
+    d.so0 = O.s0;
+    d.so1 = O.s1;
+    d.odt = O.buf->dtype;
+    hipb_run_begin(b);
+    err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                           b->stream);
+    hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
+}
+
 /* Attention geometry of a block (block_geom, sam3_model.c:777-791). */
 struct geom {
     int s, nwx, nwin, N;

@@ -33,7 +33,7 @@ EXPORTS = [
     "sam_path_init", "sam_path_free", "mat", "bmat", "gemm", "linear",
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
     "window_partition", "window_unpartition_add", "mha", "attn_fused",
-    "vit_attention",
+    "attn_packed", "vit_attention",
 ]
 
 
@@ -155,6 +155,7 @@ def lib():
                       c_long, Mem, c_long, Mem]
     L.attn_fused.argtypes = [MP, c_int, c_int, c_int, Opnd, Opnd, Opnd, Opnd,
                              Mem, c_int, c_float]
+    L.attn_packed.argtypes = [MP, c_int, c_int, c_int, Opnd]
     L.vit_attention.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
@@ -369,6 +370,10 @@ def mha(m, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o):
 
 def attn_fused(m, N, nb, nb1, Q, K, V, O, rope=None, npos=1, scale=0.125):
     _call(_lib.attn_fused, m.ptr, N, nb, nb1, Q, K, V, O, rope, npos, scale)
+
+
+def attn_packed(m, N, nb, nb1, O):
+    _call(_lib.attn_packed, m.ptr, N, nb, nb1, O)
 
 
 def vit_attention(m, block, unfused=False):

@@ -259,6 +259,13 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
                 struct opnd K, struct opnd V, struct opnd O, hipb_mem rope,
                 int npos, float scale);
 
+/* The attention stage of the precision=bf16 path alone, on the packed
+ * operands that attn_fused / vit_attention left in m->q16, m->k16 and
+ * m->vt16 (nb units of N tokens, RoPE and scale applied); O as in
+ * attn_fused. No counterpart in the reference: it is for callers that
+ * produce packed operands themselves and for timing the kernel. */
+void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O);
+
 /* Attention region of one ViT block (sam3_model.c:981-1013): norm1,
  * window partition, QKV projection, RoPE and attention of m->x into
  * m->attn (rows = nwin * N, window-partitioned for windowed blocks).

@@ -23,6 +23,9 @@ HIP_FLAGS = [
     # Packed fp32 VALU instructions are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # MFMA accumulators in VGPRs: no AGPR <-> VGPR copies around the
+    # VALU work on scores and outputs.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra",
            "-Wno-unused-parameter", "-D__HIP_PLATFORM_AMD__"]

@@ -25,6 +25,8 @@
  */
 #include "k_common.h"
 
+#include <type_traits>
+
 /* ------------------------------------------------------------ fp32 path */
 
 /* fp32 operands in the reference row layout (Q/K/V/O opnds of
@@ -201,8 +203,9 @@ extern "C" int launch_attn_f32(const attn_desc *d, void *stream)
 
 /* fp32 reference-layout Q/K/V -> packed bf16 of the fast path, 64 rows
  * of one unit per workgroup: q16/k16 [unit][Np][64] with RoPE applied
- * (q also scaled), vt16 [unit][64][Np] transposed through LDS; rows past
- * N are zero. */
+ * (q also scaled by scale * log2 e, so Q K^T comes out in log2 units for
+ * exp2), vt16 [unit][64][Np] transposed through LDS; rows past N are
+ * zero. */
 __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
                                                   uint16_t *__restrict__ q16,
                                                   uint16_t *__restrict__ k16,
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
             }
         }
         for (int e = 0; e < 16; e++)
-            q[e] *= d.scale;
+            q[e] *= d.scale * LOG2E_F;
     }
     else
         for (int e = 0; e < 16; e++) {
@@ -308,21 +311,67 @@ __device__ __forceinline__ int kperm(int i)
     return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
 }
 
-/* Lazy rescale threshold: the running max is only moved (and O, l
- * rescaled) when a new score exceeds it by more than 8 ln 2, so P stays
- * below 2^8; the final O / l is unchanged in exact arithmetic. */
-#define RESCALE_TH 5.545177444479562f
+/* Max of 16 scores. The operands are MFMA results (or sums with a -inf
+ * mask), which the compiler knows are canonical, so this becomes eight
+ * v_max3_f32 without NaN-quieting canonicalisation. */
+__device__ __forceinline__ float max16(const f32x16 &s, float m)
+{
+    for (int r = 0; r < 16; r++)
+        m = __builtin_fmaxf(m, s[r]);
+    return m;
+}
+
+/* Lazy rescale threshold, in log2 units: the running max m is only
+ * moved (and O, l rescaled) when a score exceeds it by more than 8, so
+ * P stays below 2^8; the final O / l is unchanged in exact arithmetic.
+ * Before the first move m is 0, and a first block whose max lies below
+ * -RESCALE_LO also moves it, so that P cannot underflow wholesale. */
+#define RESCALE_TH 8.0f
+#define RESCALE_LO 16.0f
+
+/* LDS rows of K [key][d] and V^T [d][key] blocks are 64 bf16 (128 B, no
+ * padding); the 16-byte chunk c of row r is stored at chunk
+ * c ^ ((r >> 1) & 7). A 16-lane group of 16-byte reads then touches 16
+ * distinct bank groups whenever it reads one logical chunk of 16
+ * different rows (MFMA operand reads) or 8 chunks of two adjacent rows
+ * (staging writes). */
+__device__ __forceinline__ int swz(int row, int chunk)
+{
+    return 8 * (chunk ^ ((row >> 1) & 7));
+}
+
+/* Online-softmax state of one wave: 32 queries (one per lane pair l,
+ * l ^ 32), O^T accumulators for d 0..31 and 32..63. */
+struct SoftState {
+    f32x16 o0, o1;
+    float m, l;
+};
+
+/* Asynchronous 16-byte global -> LDS copy (global_load_lds_dwordx4):
+ * lane i of the wave writes lds_base + 16 i. */
+__device__ __forceinline__ void g2lds16(const void *g, void *lds_base)
+{
+    __builtin_amdgcn_global_load_lds(
+        (const void __attribute__((address_space(1))) *)g,
+        (void __attribute__((address_space(3))) *)lds_base, 16, 0, 0);
+}
 
 /* Packed bf16 operands (k_qkv_pack layout), v_mfma_f32_32x32x16_bf16 with
- * f32 accumulation, 64-key blocks. LDS: K block [key][d] and V^T block
- * [d][key], rows of 72 bf16 (144 B). */
-__global__ __launch_bounds__(256) void k_attn_bf16(attn_desc d,
-                                                   const uint16_t *__restrict__ q16,
-                                                   const uint16_t *__restrict__ k16,
-                                                   const uint16_t *__restrict__ vt16)
+ * f32 accumulation, 64-key blocks.
+ *
+ * Small per-wave state (<= 128 VGPRs) keeps four waves on every SIMD, so
+ * the Q K^T / P V MFMAs of some waves overlap the softmax VALU work of
+ * others. K / V^T blocks move HBM -> LDS with asynchronous
+ * global_load_lds (no staging registers) into two swizzled slots; the
+ * next block's copy is issued right after the barrier that retires the
+ * slot it overwrites, so one barrier per block suffices. */
+__global__ __launch_bounds__(256, 4) void k_attn_bf16(attn_desc d,
+                                                      const uint16_t *__restrict__ q16,
+                                                      const uint16_t *__restrict__ k16,
+                                                      const uint16_t *__restrict__ vt16)
 {
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][72];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][72];
+    __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][64];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][64];
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
     const int N = d.N, Np = (N + 63) / 64 * 64, nblk = Np / 64;
@@ -332,11 +381,10 @@ __global__ __launch_bounds__(256) void k_attn_bf16(attn_desc d,
     const uint16_t *Vu = vt16 + unit * 64 * Np;
     const int qi = blockIdx.x * 128 + w * 32 + l32;
     const int krow = kperm(l32);
-    bf16x8 qb[4];
-    u32x4 kpre[2], vpre[2];
-    f32x16 o0, o1;
-    float m_run = -INFINITY, l_run = 0.0f;
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    bf16x8 qb[4];
+    SoftState st;
+    bool fresh = true;
 
     for (int s = 0; s < 4; s++) {
         if (qi < Np)
@@ -346,121 +394,121 @@ __global__ __launch_bounds__(256) void k_attn_bf16(attn_desc d,
                 qb[s][e] = (__bf16)0.0f;
     }
     for (int r = 0; r < 16; r++) {
-        o0[r] = 0.0f;
-        o1[r] = 0.0f;
+        st.o0[r] = 0.0f;
+        st.o1[r] = 0.0f;
     }
+    st.m = 0.0f;
+    st.l = 0.0f;
 
-    auto fetch = [&](int kb) {
+    /* Async copy of block kb into `slot`: wave w, pass j fills LDS rows
+     * 8 (2 w + j) .. +7; lane i lands on row + i / 8, physical chunk
+     * i % 8, so it fetches logical chunk (i % 8) ^ ((row >> 1) & 7). The
+     * per-lane element offsets do not depend on the block. */
+    int koff[2], voff[2];
+    for (int j = 0; j < 2; j++) {
+        const int row = 8 * (2 * w + j) + (l >> 3);
+        const int chunk = (l & 7) ^ ((row >> 1) & 7);
+
+        koff[j] = row * 64 + 8 * chunk;
+        voff[j] = row * Np + 8 * chunk;
+    }
+    auto load_block = [&](int kb, int slot) {
+        const uint16_t *kb_ = Ku + (long)kb * 64 * 64, *vb_ = Vu + kb * 64;
+
         for (int j = 0; j < 2; j++) {
-            const int c = t + 256 * j, row = c >> 3, ch = (c & 7) * 8;
-
-            kpre[j] = *(const u32x4 *)(Ku + ((long)kb * 64 + row) * 64 + ch);
-            vpre[j] = *(const u32x4 *)(Vu + (long)row * Np + kb * 64 + ch);
+            g2lds16(kb_ + koff[j], &Ks[slot][8 * (2 * w + j)][0]);
+            g2lds16(vb_ + voff[j], &Vt[slot][8 * (2 * w + j)][0]);
         }
     };
-    auto stage = [&](int buf) {
-        for (int j = 0; j < 2; j++) {
-            const int c = t + 256 * j, row = c >> 3, ch = (c & 7) * 8;
 
-            *(u32x4 *)&Ks[buf][row][ch] = kpre[j];
-            *(u32x4 *)&Vt[buf][row][ch] = vpre[j];
-        }
-    };
-
-    fetch(0);
-    stage(0);
-    __syncthreads();
+    load_block(0, 0);
     for (int kb = 0; kb < nblk; kb++) {
-        const int buf = kb & 1;
-        f32x16 s0, s1;
-        float mx = -INFINITY, m_new, mc;
-        bf16x8 pb[4];
+        const int slot = kb & 1;
 
-        if (kb + 1 < nblk)
-            fetch(kb + 1);
-        for (int r = 0; r < 16; r++) {
-            s0[r] = 0.0f;
-            s1[r] = 0.0f;
-        }
-#pragma unroll
-        for (int ds = 0; ds < 4; ds++) {
-            const bf16x8 a0 = *(const bf16x8 *)&Ks[buf][krow][16 * ds + 8 * h];
-            const bf16x8 a1 = *(const bf16x8 *)&Ks[buf][32 + krow][16 * ds + 8 * h];
-
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qb[ds], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qb[ds], s1, 0, 0, 0);
-        }
-        if (kb * 64 + 64 > N) {
-            for (int r = 0; r < 16; r++) {
-                const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
-
-                if (key >= N)
-                    s0[r] = -INFINITY;
-                if (key + 32 >= N)
-                    s1[r] = -INFINITY;
-            }
-        }
-        for (int r = 0; r < 16; r++)
-            mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        m_new = fmaxf(m_run, mx);
-        if (__ballot(m_new - m_run > RESCALE_TH) != 0) {
-            const float corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E_F);
-
-            l_run *= corr;
-            for (int r = 0; r < 16; r++) {
-                o0[r] *= corr;
-                o1[r] *= corr;
-            }
-            m_run = m_new;
-        }
-        mc = m_run * LOG2E_F;
-        for (int r = 0; r < 16; r++) {
-            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], LOG2E_F, -mc));
-            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], LOG2E_F, -mc));
-        }
-        for (int a = 0; a < 2; a++)
-            for (int e = 0; e < 8; e++) {
-                pb[a][e] = (__bf16)s0[8 * a + e];
-                pb[2 + a][e] = (__bf16)s1[8 * a + e];
-            }
-        for (int j = 0; j < 4; j++)
-            for (int e = 0; e < 4; e++) {
-                bf16x2 p2;
-
-                p2.x = pb[j][2 * e];
-                p2.y = pb[j][2 * e + 1];
-                l_run = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, l_run, false);
-            }
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const bf16x8 v0 = *(const bf16x8 *)&Vt[buf][l32][16 * st + 8 * h];
-            const bf16x8 v1 = *(const bf16x8 *)&Vt[buf][32 + l32][16 * st + 8 * h];
-
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, pb[st], o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, pb[st], o1, 0, 0, 0);
-        }
-        if (kb + 1 < nblk)
-            stage(buf ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if (kb + 1 < nblk)
+            load_block(kb + 1, slot ^ 1);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+            const int row = 32 * c + krow;
+            bf16x8 kf[4], vf[4], pb[2];
+            f32x16 s;
+            float mx;
+
+            for (int ds = 0; ds < 4; ds++)
+                kf[ds] = *(const bf16x8 *)&Ks[slot][row][swz(row, 2 * ds + h)];
+            for (int r = 0; r < 16; r++)
+                s[r] = -st.m;
+            for (int ds = 0; ds < 4; ds++)
+                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s, 0, 0, 0);
+            if (kb * 64 + 64 > N)
+                for (int r = 0; r < 16; r++) {
+                    const int key = kb * 64 + 32 * c + 16 * (r >> 3) + 8 * h + (r & 7);
+
+                    s[r] += key < N ? 0.0f : -INFINITY;
+                }
+            mx = max16(s, -INFINITY);
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (__ballot(mx > RESCALE_TH || (fresh && mx < -RESCALE_LO)) != 0) {
+                /* Move m by this half's max (s and mx are relative to m). */
+                const float corr = __builtin_amdgcn_exp2f(-mx);
+
+                st.l *= corr;
+                for (int r = 0; r < 16; r++) {
+                    st.o0[r] *= corr;
+                    st.o1[r] *= corr;
+                    s[r] -= mx;
+                }
+                st.m += mx;
+            }
+            fresh = false;
+            for (int a = 0; a < 2; a++) {
+                const int chunk = 2 * (2 * c + a) + h;
+
+                vf[2 * a] = *(const bf16x8 *)&Vt[slot][l32][swz(l32, chunk)];
+                vf[2 * a + 1] = *(const bf16x8 *)&Vt[slot][32 + l32][swz(32 + l32, chunk)];
+            }
+            for (int r = 0; r < 16; r++)
+                s[r] = __builtin_amdgcn_exp2f(s[r]);
+            for (int a = 0; a < 2; a++)
+                for (int e = 0; e < 8; e++)
+                    pb[a][e] = (__bf16)s[8 * a + e];
+            for (int a = 0; a < 2; a++) {
+                st.o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * a], pb[a], st.o0, 0, 0, 0);
+                st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * a + 1], pb[a], st.o1, 0, 0, 0);
+            }
+            for (int a = 0; a < 2; a++)
+                for (int e = 0; e < 4; e++) {
+                    bf16x2 p2;
+
+                    p2.x = pb[a][2 * e];
+                    p2.y = pb[a][2 * e + 1];
+                    st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
+                }
+        }
     }
 
-    l_run += __shfl_xor(l_run, 32, 64);
+    st.l += __shfl_xor(st.l, 32, 64);
     if (qi < N) {
-        const float inv = 1.0f / l_run;
+        const float inv = 1.0f / st.l;
         const long b0 = unit / d.nb1, b1 = unit % d.nb1;
         const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
 
-        for (int r = 0; r < 16; r++) {
-            const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+        if (d.odt == DT_F32) {
+            for (int r = 0; r < 16; r++) {
+                const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
-            if (d.odt == DT_F32) {
-                ((float *)d.O)[orow + dd] = o0[r] * inv;
-                ((float *)d.O)[orow + 32 + dd] = o1[r] * inv;
+                ((float *)d.O)[orow + dd] = st.o0[r] * inv;
+                ((float *)d.O)[orow + 32 + dd] = st.o1[r] * inv;
             }
-            else {
-                ((uint16_t *)d.O)[orow + dd] = f2bf(o0[r] * inv);
-                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(o1[r] * inv);
+        }
+        else {
+            for (int r = 0; r < 16; r++) {
+                const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+
+                ((uint16_t *)d.O)[orow + dd] = f2bf(st.o0[r] * inv);
+                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
             }
         }
     }

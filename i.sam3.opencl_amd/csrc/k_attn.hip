@@ -347,13 +347,25 @@ struct SoftState {
     float m, l;
 };
 
+/* XCDs (L2 domains) of an MI355X. */
+#define NXCD 8
+
 /* Asynchronous 16-byte global -> LDS copy (global_load_lds_dwordx4):
- * lane i of the wave writes lds_base + 16 i. */
+ * lane i of the wave writes lds_base + 16 i (lds_base wave-uniform, via
+ * M0). Issued as inline assembly so that the compiler does not treat the
+ * copy as a store that later LDS reads of the other slot must wait for:
+ * the kernel waits for it itself (s_waitcnt vmcnt(0)) before the barrier
+ * that hands the slot to the readers. */
 __device__ __forceinline__ void g2lds16(const void *g, void *lds_base)
 {
-    __builtin_amdgcn_global_load_lds(
-        (const void __attribute__((address_space(1))) *)g,
-        (void __attribute__((address_space(3))) *)lds_base, 16, 0, 0);
+    /* The low 32 bits of a flat LDS address are the LDS offset. */
+    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_base);
+
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "global_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(g)
+                 : "memory", "m0");
 }
 
 /* Packed bf16 operands (k_qkv_pack layout), v_mfma_f32_32x32x16_bf16 with
@@ -365,7 +377,7 @@ __device__ __forceinline__ void g2lds16(const void *g, void *lds_base)
  * global_load_lds (no staging registers) into two swizzled slots; the
  * next block's copy is issued right after the barrier that retires the
  * slot it overwrites, so one barrier per block suffices. */
-__global__ __launch_bounds__(256, 4) void k_attn_bf16(attn_desc d,
+__global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
                                                       const uint16_t *__restrict__ vt16)
@@ -375,11 +387,20 @@ __global__ __launch_bounds__(256, 4) void k_attn_bf16(attn_desc d,
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
     const int N = d.N, Np = (N + 63) / 64 * 64, nblk = Np / 64;
-    const long unit = blockIdx.y;
+    const int ntiles = (N + 127) / 128;
+    const long total = (long)d.nb * ntiles, per_xcd = (total + NXCD - 1) / NXCD;
+    /* XCD-aware order: workgroups are dispatched to the XCDs round-robin,
+     * so workgroup g runs on XCD g % NXCD; give each XCD a contiguous run
+     * of (unit, tile) items, i.e. whole units, whose K / V then stay in
+     * that XCD's L2 instead of every XCD streaming every unit. */
+    const long item = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
+    if (item >= total)
+        return;
+    const long unit = item / ntiles;
     const uint16_t *Qu = q16 + unit * Np * 64;
     const uint16_t *Ku = k16 + unit * Np * 64;
     const uint16_t *Vu = vt16 + unit * 64 * Np;
-    const int qi = blockIdx.x * 128 + w * 32 + l32;
+    const int qi = (int)(item % ntiles) * 128 + w * 32 + l32;
     const int krow = kperm(l32);
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     bf16x8 qb[4];
@@ -424,69 +445,80 @@ __global__ __launch_bounds__(256, 4) void k_attn_bf16(attn_desc d,
     load_block(0, 0);
     for (int kb = 0; kb < nblk; kb++) {
         const int slot = kb & 1;
+        bf16x8 kf[8], vf[8], pb[4];
+        f32x16 s0, s1;
+        float mx;
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (kb + 1 < nblk)
             load_block(kb + 1, slot ^ 1);
-#pragma unroll
+        /* Both 32-key halves at once: two independent Q K^T chains, one
+         * max / exchange / rescale decision per 64-key block. */
         for (int c = 0; c < 2; c++) {
             const int row = 32 * c + krow;
-            bf16x8 kf[4], vf[4], pb[2];
-            f32x16 s;
-            float mx;
 
             for (int ds = 0; ds < 4; ds++)
-                kf[ds] = *(const bf16x8 *)&Ks[slot][row][swz(row, 2 * ds + h)];
-            for (int r = 0; r < 16; r++)
-                s[r] = -st.m;
-            for (int ds = 0; ds < 4; ds++)
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s, 0, 0, 0);
-            if (kb * 64 + 64 > N)
-                for (int r = 0; r < 16; r++) {
-                    const int key = kb * 64 + 32 * c + 16 * (r >> 3) + 8 * h + (r & 7);
-
-                    s[r] += key < N ? 0.0f : -INFINITY;
-                }
-            mx = max16(s, -INFINITY);
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-            if (__ballot(mx > RESCALE_TH || (fresh && mx < -RESCALE_LO)) != 0) {
-                /* Move m by this half's max (s and mx are relative to m). */
-                const float corr = __builtin_amdgcn_exp2f(-mx);
-
-                st.l *= corr;
-                for (int r = 0; r < 16; r++) {
-                    st.o0[r] *= corr;
-                    st.o1[r] *= corr;
-                    s[r] -= mx;
-                }
-                st.m += mx;
-            }
-            fresh = false;
-            for (int a = 0; a < 2; a++) {
-                const int chunk = 2 * (2 * c + a) + h;
-
-                vf[2 * a] = *(const bf16x8 *)&Vt[slot][l32][swz(l32, chunk)];
-                vf[2 * a + 1] = *(const bf16x8 *)&Vt[slot][32 + l32][swz(32 + l32, chunk)];
-            }
-            for (int r = 0; r < 16; r++)
-                s[r] = __builtin_amdgcn_exp2f(s[r]);
-            for (int a = 0; a < 2; a++)
-                for (int e = 0; e < 8; e++)
-                    pb[a][e] = (__bf16)s[8 * a + e];
-            for (int a = 0; a < 2; a++) {
-                st.o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * a], pb[a], st.o0, 0, 0, 0);
-                st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * a + 1], pb[a], st.o1, 0, 0, 0);
-            }
-            for (int a = 0; a < 2; a++)
-                for (int e = 0; e < 4; e++) {
-                    bf16x2 p2;
-
-                    p2.x = pb[a][2 * e];
-                    p2.y = pb[a][2 * e + 1];
-                    st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
-                }
+                kf[4 * c + ds] = *(const bf16x8 *)&Ks[slot][row][swz(row, 2 * ds + h)];
         }
+        for (int t4 = 0; t4 < 4; t4++) {
+            const int chunk = 2 * t4 + h;
+
+            vf[2 * t4] = *(const bf16x8 *)&Vt[slot][l32][swz(l32, chunk)];
+            vf[2 * t4 + 1] = *(const bf16x8 *)&Vt[slot][32 + l32][swz(32 + l32, chunk)];
+        }
+        for (int r = 0; r < 16; r++) {
+            s0[r] = -st.m;
+            s1[r] = -st.m;
+        }
+        for (int ds = 0; ds < 4; ds++) {
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4 + ds], qb[ds], s1, 0, 0, 0);
+        }
+        if (kb * 64 + 64 > N)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
+
+                s0[r] += key < N ? 0.0f : -INFINITY;
+                s1[r] += key + 32 < N ? 0.0f : -INFINITY;
+            }
+        mx = max16(s1, max16(s0, -INFINITY));
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+        if (__ballot(mx > RESCALE_TH || (fresh && mx < -RESCALE_LO)) != 0) {
+            /* Move m by this block's max (s and mx are relative to m). */
+            const float corr = __builtin_amdgcn_exp2f(-mx);
+
+            st.l *= corr;
+            for (int r = 0; r < 16; r++) {
+                st.o0[r] *= corr;
+                st.o1[r] *= corr;
+                s0[r] -= mx;
+                s1[r] -= mx;
+            }
+            st.m += mx;
+        }
+        fresh = false;
+        for (int r = 0; r < 16; r++) {
+            s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r]);
+        }
+        for (int a = 0; a < 2; a++)
+            for (int e = 0; e < 8; e++) {
+                pb[a][e] = (__bf16)s0[8 * a + e];
+                pb[2 + a][e] = (__bf16)s1[8 * a + e];
+            }
+        for (int t4 = 0; t4 < 4; t4++) {
+            st.o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4], pb[t4], st.o0, 0, 0, 0);
+            st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4 + 1], pb[t4], st.o1, 0, 0, 0);
+        }
+        for (int a = 0; a < 4; a++)
+            for (int e = 0; e < 4; e++) {
+                bf16x2 p2;
+
+                p2.x = pb[a][2 * e];
+                p2.y = pb[a][2 * e + 1];
+                st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
+            }
     }
 
     st.l += __shfl_xor(st.l, 32, 64);
@@ -518,10 +550,13 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 const void *k16, const void *vt16,
                                 void *stream)
 {
-    if (d->nb > 65535)
+    const long total = (long)d->nb * ((d->N + 127) / 128);
+    const long grid = (total + NXCD - 1) / NXCD * NXCD;
+
+    if (grid > 0x7fffffffL)
         return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(k_attn_bf16, dim3((d->N + 127) / 128, d->nb),
-                       dim3(256), 0, (hipStream_t)stream, *d,
+    hipLaunchKernelGGL(k_attn_bf16, dim3((unsigned)grid), dim3(256), 0,
+                       (hipStream_t)stream, *d,
                        (const uint16_t *)q16, (const uint16_t *)k16,
                        (const uint16_t *)vt16);
     return hipGetLastError();

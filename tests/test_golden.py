@@ -1,0 +1,55 @@
+"""The CPU oracle against the golden vectors of the reference's own
+kernels (tests/golden/vectors, written by tests/golden/gen_golden.py from
+sam3_kernels.cl run unchanged through the OpenCL runtime).
+
+Data movement and RoPE must match bit for bit; arithmetic within
+rel-L2 1e-6 (the differences are the last bits of the runtimes' exp / erf
+and of dot() contraction order, which nothing in the reference pins)."""
+import hashlib
+import os
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+
+import golden_cases as gc  # noqa: E402
+
+VEC = os.path.join(HERE, "golden", "vectors")
+EXACT = {"rope", "window"}
+
+
+def load(name):
+    case = gc.CASES[name]()
+    gold = np.load(os.path.join(VEC, name + ".npz"))
+    h = hashlib.sha1()
+    for a in case["inputs"]:
+        h.update(np.ascontiguousarray(a).tobytes())
+    assert h.hexdigest() == str(gold["input_sha1"]), "regenerated inputs differ"
+    return case, gold
+
+
+def compare(name, got, gold, tol):
+    rows = gold["sample_rows"] if "sample_rows" in gold.files else None
+    for k, v in got.items():
+        if rows is not None and v.ndim == 2:
+            v = v[rows]
+        ref = gold[k]
+        if name in EXACT:
+            np.testing.assert_array_equal(v, ref)
+        else:
+            err = np.linalg.norm(v.astype(np.float64) - ref) / np.linalg.norm(ref)
+            assert err <= tol, (name, k, err)
+
+
+@pytest.mark.parametrize("name", list(gc.CASES))
+def test_oracle_matches_reference_kernels(orc, name):
+    case, gold = load(name)
+    compare(name, gc.run_reference(name, case, gc.OracleImpl(orc)), gold, 1e-6)
+
+
+def test_every_case_has_vectors():
+    have = {f[:-4] for f in os.listdir(VEC) if f.endswith(".npz")}
+    assert have == set(gc.CASES)

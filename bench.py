@@ -184,6 +184,13 @@ def decoder(hip, be, steps, warmup):
                                     T * dint, img2, T * dint, o_t), steps, warmup)
     i2t = timed(be, lambda: hip.mha(m, P, T, NT, dint, img, T * dint, tok,
                                     NT * dint, tok2, NT * dint, o_i), steps, warmup)
+    # Practical HBM ceiling: the runtime's device-to-device copy of
+    # COPY_BYTES (read + write).
+    src = be.alloc(COPY_BYTES, "copy src")
+    dst = be.alloc(COPY_BYTES, "copy dst")
+    cp = timed(be, lambda: be.copy(src, dst, 0, 0, COPY_BYTES), steps, warmup)
+    be.release(src)
+    be.release(dst)
     bytes_t2i = 4.0 * (P * NT * dint * 2 + 2 * P * T * dint)
     bytes_i2t = 4.0 * (2 * P * T * dint + 2 * P * NT * dint)
     for d in (img, img2, tok, tok2, o_t, o_i):
@@ -193,6 +200,7 @@ def decoder(hip, be, steps, warmup):
         "i2t_ms": round(i2t, 4), "i2t_GBps": round(bytes_i2t / i2t / 1e6, 1),
         "pct_hbm_peak": round(100 * (bytes_t2i + bytes_i2t) / (t2i + i2t) /
                               1e6 / PEAK_HBM, 1),
+        "device_copy_GBps": round(2.0 * COPY_BYTES / cp / 1e6, 1),
     }
 
 
@@ -205,6 +213,8 @@ def main():
                     help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the global bf16 attention kernel (profiling)")
+    ap.add_argument("--decoder-only", action="store_true",
+                    help="only the mask-decoder cross-attention (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the attention path "
@@ -213,6 +223,11 @@ def main():
         sys.exit(2)
 
     hip = load_hip()
+    if args.decoder_only:
+        be32 = hip.Backend(precision="fp32")
+        print(json.dumps({"decoder_fp32": decoder(hip, be32, args.steps,
+                                                  args.warmup)}))
+        return
     be = hip.Backend(precision="bf16")
     glob = Block(hip, be, 0, seed=3)
     glob.region()          # LN -> QKV -> pack -> attention; packs operands

@@ -112,7 +112,8 @@ int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,
                        const float *V, long sv, float *O, int P, int Nq,
                        int Nk, int dint, float scale, void *stream);
 /* Split-K token->image attention for c == 16; scratch holds the
- * partial results, mha_manykeys_scratch() bytes. */
+ * partial results, mha_manykeys_scratch() bytes (0 when the key range is
+ * not split: scratch may then be NULL). */
 size_t mha_manykeys_scratch(int P, int Nq, int Nk);
 int launch_mha_manykeys(const float *Q, long sq, const float *K, long sk,
                         const float *V, long sv, float *O, int P, int Nq,

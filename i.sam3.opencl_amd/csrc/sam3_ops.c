@@ -347,6 +347,12 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
         hipb_fatal("mha: unsupported shape");
         return;
     }
+    /* The many-keys kernel reads rows as 16-byte vectors. */
+    if (many && (sq % 4 || sk % 4 || sv % 4)) {
+        hipb_fatal("mha: per-prompt strides must be multiples of 4 floats "
+                   "with many keys (sq=%ld sk=%ld sv=%ld)", sq, sk, sv);
+        return;
+    }
     if (!buf_ok("mha", "q", qp, dec_extent(P, sq, Nq, dint), HIPB_F32) ||
         !buf_ok("mha", "k", kp, dec_extent(P, sk, Nk, dint), HIPB_F32) ||
         !buf_ok("mha", "v", vp, dec_extent(P, sv, Nk, dint), HIPB_F32) ||
@@ -354,9 +360,10 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
         return;
     hipb_run_begin(be);
     if (many) {
-        void *scr = hipb_scratch(be, mha_manykeys_scratch(P, Nq, Nk));
+        const size_t need = mha_manykeys_scratch(P, Nq, Nk);
+        void *scr = need ? hipb_scratch(be, need) : NULL;
 
-        if (!scr)
+        if (need && !scr)
             return;
         err = launch_mha_manykeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
                                   o->ptr, P, Nq, Nk, dint, scale, scr,

@@ -205,6 +205,10 @@ def _dec(seed, P, Nq, Nk, dint, shared_k=False, shared_q=False):
     (64, 4096, 7, 128, False, False),    # image -> token, per-prompt queries
     (16, 5184, 8, 128, False, True),     # image -> token, shared queries
     (64, 8, 8, 256, False, False),       # token self-attention, c = 32
+    (8, 2048, 65, 128, False, False),    # many keys, key range not split
+    (2, 3, 261, 128, False, False),      # many keys, ragged last step
+    (3, 20, 40, 128, False, False),      # 9..64 keys, generic few-keys
+    (5, 17, 1, 128, False, False),       # one key: O = V
 ])
 def test_mha(hip, be, orc, P, Nq, Nk, dint, shk, shq):
     m = model(hip, be)
@@ -218,6 +222,29 @@ def test_mha(hip, be, orc, P, Nq, Nk, dint, shk, shq):
                   want) <= FP32_TOL
     for d in (dq, dk, dv, do):
         be.release(d)
+
+
+def test_mha_unaligned_prompt_strides(hip, be, orc):
+    """Per-prompt strides that are not a multiple of 4 floats take the
+    generic few-keys kernel; with many keys they are a fatal error."""
+    m = model(hip, be)
+    P, Nq, Nk, dint = 3, 11, 7, 128
+    g = rng(5)
+    sq, sk = Nq * dint + 2, Nk * dint + 1
+    q = g.standard_normal(P * sq).astype(np.float32)
+    k = g.standard_normal(P * sk).astype(np.float32)
+    v = g.standard_normal(P * sk).astype(np.float32)
+    dq, dk, dv = be.upload(q), be.upload(k), be.upload(v)
+    do = be.alloc(P * Nq * dint * 4)
+    hip.mha(m, P, Nq, Nk, dint, dq, sq, dk, sk, dv, sk, do)
+    got = be.read(do).reshape(P * Nq, dint)
+    want = orc.mha(P, Nq, Nk, dint, q, sq, k, sk, v, sk)
+    assert report("mha unaligned strides", got, want) <= FP32_TOL
+    d = be.alloc(P * 100 * dint * 4 + 64)
+    with pytest.raises(hip.Sam3HipError, match="multiples of 4"):
+        hip.mha(m, P, 4, 100, dint, d, 0, d, 100 * dint + 2, d, 0, d)
+    for x in (dq, dk, dv, do, d):
+        be.release(x)
 
 
 def test_mha_rejects_wide_heads_with_many_keys(hip, be):

@@ -33,6 +33,14 @@ PEAK_F32 = 157.3     # TFLOP/s, f32 MFMA
 PEAK_HBM = 8000.0    # GB/s
 COPY_BYTES = 256 << 20
 
+# HBM bytes per k_attn_bf16 launch (global, 5184 tokens x 16 heads), from
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --kernel-only`
+# (KiB per dispatch), each scaled by what the counter reads for the
+# runtime's 256 MiB copy in the same run (FETCH_SIZE 2.0, WRITE_SIZE 1.0).
+# Summary and commands: profiles/attn_bf16_global_5184.md.
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15618.0, 20736.0
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+
 
 def load_hip():
     spec = importlib.util.spec_from_file_location(
@@ -90,6 +98,12 @@ class Block:
 
     def flops(self):
         return 4.0 * self.N * self.N * 64 * self.H * self.nunits
+
+    def bytes(self):
+        """Algorithmic bytes of the packed-operand kernel: bf16 Q, K, V^T
+        read once, fp32 O written once."""
+        units = self.nunits * self.H
+        return units * self.N * 64 * (3 * 2 + 4)
 
     def region(self):
         self.hip.vit_attention(self.m, self.blk)
@@ -313,7 +327,10 @@ def main():
         "decoder_fp32": dec,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16, 4), "traffic": None,
+                     "frac": round(tflops / PEAK_BF16, 4),
+                     "traffic": round(1024 * (ATTN_FETCH_KIB * FETCH_SCALE +
+                                              ATTN_WRITE_KIB * WRITE_SCALE)),
+                     "traffic_algorithmic": glob.bytes(),
                      "kernel": "k_attn_bf16 (global, 5184 tokens x 16 heads)",
                      "flops_per_launch": glob.flops()},
     }

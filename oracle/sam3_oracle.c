@@ -20,9 +20,12 @@
  *   or_window_partition/_add    index algebra: round trip, padding
  *   or_attn_fewkeys/_manykeys   fp64 SDPA, Nk = 1, Q = 0, key permutation
  *   or_vit_attention            fp64 pipeline, window = grid == global
- * The last-bit choices (mad as fma, the runtime's exp/erf/rsqrt, dot()'s
- * internal order) are parity unpinned: the reference holds no vector
- * that fixes them.
+ * and, for every function, the golden vectors of the reference's own
+ * kernels (tests/golden, sam3_kernels.cl run unchanged through the ROCm
+ * OpenCL runtime): bit-exact for RoPE and window data movement, rel-L2
+ * <= 1e-6 elsewhere (tests/test_golden.py). The last-bit choices (mad as
+ * fma, the runtime's exp/erf/rsqrt, dot()'s internal order) stay parity
+ * unpinned: those vectors bound them, none fixes them.
  */
 #include "sam3_oracle.h"
 

@@ -210,9 +210,11 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
                                                   uint16_t *__restrict__ q16,
                                                   uint16_t *__restrict__ k16,
                                                   uint16_t *__restrict__ vt16,
+                                                  float *__restrict__ knorm,
                                                   int Np)
 {
     __shared__ uint16_t Vl[64][66];
+    __shared__ float kred[4];
     const int t = threadIdx.x, row = t >> 2, ds = (t & 3) * 16;
     const int unit = blockIdx.y, i = blockIdx.x * 64 + row;
     const long b0 = unit / d.nb1, b1 = unit % d.nb1;
@@ -273,6 +275,23 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
         *(u32x4 *)(k16 + o) = a;
         *(u32x4 *)(k16 + o + 8) = b;
     }
+    {
+        /* Largest |k| of this 64-key block, over the bf16 values the
+         * attention multiplies: squares summed over the row's 4 threads,
+         * max over the 4 waves' 16 rows each. */
+        float ss = 0.0f, mx;
+
+        for (int e = 0; e < 16; e++) {
+            const float kv = bf2f(f2bf(k[e]));
+
+            ss = fmaf(kv, kv, ss);
+        }
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        mx = wave_max(ss);
+        if ((t & 63) == 0)
+            kred[t >> 6] = mx;
+    }
     for (int e = 0; e < 16; e++)
         Vl[ds + e][row] = f2bf(v[e]);
     __syncthreads();
@@ -284,10 +303,17 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
         for (int e = 0; e < 16; e++)
             dst[e] = Vl[dd][k0 + e];
     }
+    if (t == 0) {
+        const float m2 = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
+
+        /* Rounded up by 2^-10 relative: covers the square root's and the
+         * sum's roundings. */
+        knorm[(long)unit * (Np / 64) + blockIdx.x] = sqrtf(m2) * (1.0f + 0x1p-10f);
+    }
 }
 
 extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
-                               void *vt16, void *stream)
+                               void *vt16, float *knorm, void *stream)
 {
     const int Np = (d->N + 63) / 64 * 64;
 
@@ -295,7 +321,7 @@ extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
         return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_qkv_pack, dim3(Np / 64, d->nb), dim3(256), 0,
                        (hipStream_t)stream, *d, (uint16_t *)q16,
-                       (uint16_t *)k16, (uint16_t *)vt16, Np);
+                       (uint16_t *)k16, (uint16_t *)vt16, knorm, Np);
     return hipGetLastError();
 }
 
@@ -320,14 +346,6 @@ __device__ __forceinline__ float max16(const f32x16 &s, float m)
         m = __builtin_fmaxf(m, s[r]);
     return m;
 }
-
-/* Lazy rescale threshold, in log2 units: the running max m is only
- * moved (and O, l rescaled) when a score exceeds it by more than 8, so
- * P stays below 2^8; the final O / l is unchanged in exact arithmetic.
- * Before the first move m is 0, and a first block whose max lies below
- * -RESCALE_LO also moves it, so that P cannot underflow wholesale. */
-#define RESCALE_TH 8.0f
-#define RESCALE_LO 16.0f
 
 /* LDS rows of K [key][d] and V^T [d][key] blocks are 64 bf16 (128 B, no
  * padding); the 16-byte chunk c of row r is stored at chunk
@@ -368,19 +386,36 @@ __device__ __forceinline__ void g2lds16(const void *g, void *lds_base)
                  : "memory", "m0");
 }
 
+/* Scores may run this far (log2 units) above or below the reference
+ * point m before it must move: exp2 of them stays far inside the float
+ * and bf16 ranges, and the accumulated O and l with it (5184 keys x 2^64
+ * x |v|). */
+#define SAFE_SPAN 64.0f
+
 /* Packed bf16 operands (k_qkv_pack layout), v_mfma_f32_32x32x16_bf16 with
  * f32 accumulation, 64-key blocks.
  *
- * Small per-wave state (<= 128 VGPRs) keeps four waves on every SIMD, so
- * the Q K^T / P V MFMAs of some waves overlap the softmax VALU work of
- * others. K / V^T blocks move HBM -> LDS with asynchronous
- * global_load_lds (no staging registers) into two swizzled slots; the
- * next block's copy is issued right after the barrier that retires the
- * slot it overwrites, so one barrier per block suffices. */
+ * Small per-wave state keeps three waves on every SIMD, so the Q K^T /
+ * P V MFMAs of some waves overlap the softmax VALU work of others. K /
+ * V^T blocks move HBM -> LDS with asynchronous global_load_lds (no
+ * staging registers) into two swizzled slots; the next block's copy is
+ * issued right after the barrier that retires the slot it overwrites, so
+ * one barrier per block suffices.
+ *
+ * The softmax reference point m (P = exp2(s - m), O and l scaled alike,
+ * so O / l does not depend on it) starts at 0 and only moves when a
+ * score could leave [m - SAFE_SPAN, m + SAFE_SPAN]. |q . k| <= |q| |k|,
+ * and the packing kernel records each block's largest |k|, so a wave
+ * first checks the bound |q| max|k| - m <= SAFE_SPAN for all its lanes
+ * (three VALU operations); only blocks it cannot clear, and the first
+ * block (which also guards against a row whose scores all lie far below
+ * 0), take the exact block max with its cross-lane exchange. While every
+ * m of the wave is 0 the scores feed exp2 directly. */
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
-                                                      const uint16_t *__restrict__ vt16)
+                                                      const uint16_t *__restrict__ vt16,
+                                                      const float *__restrict__ knorm)
 {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][64];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][64];
@@ -400,12 +435,15 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     const uint16_t *Qu = q16 + unit * Np * 64;
     const uint16_t *Ku = k16 + unit * Np * 64;
     const uint16_t *Vu = vt16 + unit * 64 * Np;
+    const float *kn = knorm + unit * nblk;
     const int qi = (int)(item % ntiles) * 128 + w * 32 + l32;
     const int krow = kperm(l32);
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+    const f32x16 zero16 = {};
     bf16x8 qb[4];
     SoftState st;
-    bool fresh = true;
+    float qn; /* |q| of this lane's query, rounded up */
+    bool fresh = true, shifted = false; /* shifted: some lane's m != 0 */
 
     for (int s = 0; s < 4; s++) {
         if (qi < Np)
@@ -414,6 +452,11 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             for (int e = 0; e < 8; e++)
                 qb[s][e] = (__bf16)0.0f;
     }
+    qn = 0.0f;
+    for (int s = 0; s < 4; s++)
+        for (int e = 0; e < 8; e++)
+            qn = fmaf((float)qb[s][e], (float)qb[s][e], qn);
+    qn = sqrtf(qn + __shfl_xor(qn, 32, 64)) * (1.0f + 0x1p-10f);
     for (int r = 0; r < 16; r++) {
         st.o0[r] = 0.0f;
         st.o1[r] = 0.0f;
@@ -447,14 +490,14 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         const int slot = kb & 1;
         bf16x8 kf[8], vf[8], pb[4];
         f32x16 s0, s1;
-        float mx;
+        /* Can this block's scores exceed m + SAFE_SPAN for some lane? */
+        const bool check = __ballot(fresh || qn * kn[kb] - st.m > SAFE_SPAN) != 0;
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (kb + 1 < nblk)
             load_block(kb + 1, slot ^ 1);
-        /* Both 32-key halves at once: two independent Q K^T chains, one
-         * max / exchange / rescale decision per 64-key block. */
+        /* Both 32-key halves at once: two independent Q K^T chains. */
         for (int c = 0; c < 2; c++) {
             const int row = 32 * c + krow;
 
@@ -467,14 +510,17 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             vf[2 * t4] = *(const bf16x8 *)&Vt[slot][l32][swz(l32, chunk)];
             vf[2 * t4 + 1] = *(const bf16x8 *)&Vt[slot][32 + l32][swz(32 + l32, chunk)];
         }
-        for (int r = 0; r < 16; r++) {
-            s0[r] = -st.m;
-            s1[r] = -st.m;
-        }
-        for (int ds = 0; ds < 4; ds++) {
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qb[0], zero16, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4], qb[0], zero16, 0, 0, 0);
+        for (int ds = 1; ds < 4; ds++) {
             s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s0, 0, 0, 0);
             s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4 + ds], qb[ds], s1, 0, 0, 0);
         }
+        if (shifted)
+            for (int r = 0; r < 16; r++) {
+                s0[r] -= st.m;
+                s1[r] -= st.m;
+            }
         if (kb * 64 + 64 > N)
             for (int r = 0; r < 16; r++) {
                 const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
@@ -482,22 +528,27 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 s0[r] += key < N ? 0.0f : -INFINITY;
                 s1[r] += key + 32 < N ? 0.0f : -INFINITY;
             }
-        mx = max16(s1, max16(s0, -INFINITY));
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-        if (__ballot(mx > RESCALE_TH || (fresh && mx < -RESCALE_LO)) != 0) {
-            /* Move m by this block's max (s and mx are relative to m). */
-            const float corr = __builtin_amdgcn_exp2f(-mx);
+        if (check) {
+            /* Exact block max relative to m; move m (rescaling O, l and
+             * this block's scores) if it leaves the safe span. */
+            float mx = max16(s1, max16(s0, -INFINITY));
 
-            st.l *= corr;
-            for (int r = 0; r < 16; r++) {
-                st.o0[r] *= corr;
-                st.o1[r] *= corr;
-                s0[r] -= mx;
-                s1[r] -= mx;
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (__ballot(mx > SAFE_SPAN || (fresh && mx < -SAFE_SPAN)) != 0) {
+                const float corr = __builtin_amdgcn_exp2f(-mx);
+
+                st.l *= corr;
+                for (int r = 0; r < 16; r++) {
+                    st.o0[r] *= corr;
+                    st.o1[r] *= corr;
+                    s0[r] -= mx;
+                    s1[r] -= mx;
+                }
+                st.m += mx;
+                shifted = true;
             }
-            st.m += mx;
+            fresh = false;
         }
-        fresh = false;
         for (int r = 0; r < 16; r++) {
             s0[r] = __builtin_amdgcn_exp2f(s0[r]);
             s1[r] = __builtin_amdgcn_exp2f(s1[r]);
@@ -548,7 +599,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
 
 extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 const void *k16, const void *vt16,
-                                void *stream)
+                                const float *knorm, void *stream)
 {
     const long total = (long)d->nb * ((d->N + 127) / 128);
     const long grid = (total + NXCD - 1) / NXCD * NXCD;
@@ -558,6 +609,6 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     hipLaunchKernelGGL(k_attn_bf16, dim3((unsigned)grid), dim3(256), 0,
                        (hipStream_t)stream, *d,
                        (const uint16_t *)q16, (const uint16_t *)k16,
-                       (const uint16_t *)vt16);
+                       (const uint16_t *)vt16, knorm);
     return hipGetLastError();
 }

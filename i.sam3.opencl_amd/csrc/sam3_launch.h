@@ -99,13 +99,15 @@ int launch_attn_f32(const struct attn_desc *d, void *stream);
 
 /* Packed bf16 staging of the fast path, Np = N rounded up to 64:
  * q16/k16 [nb][Np][64] (RoPE applied, q scaled), vt16 [nb][64][Np],
- * zero in the padding. */
+ * zero in the padding; knorm [nb][Np / 64] floats, the largest |k| of
+ * each 64-key block (of the bf16 keys, rounded up). */
 int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
-                    void *vt16, void *stream);
+                    void *vt16, float *knorm, void *stream);
 
 /* bf16 MFMA attention on the packed operands; O addressed as in d. */
 int launch_attn_bf16(const struct attn_desc *d, const void *q16,
-                     const void *k16, const void *vt16, void *stream);
+                     const void *k16, const void *vt16, const float *knorm,
+                     void *stream);
 
 /* Decoder attention (8 heads, head width c = dint / 8). */
 int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,

@@ -381,9 +381,10 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
 
 /* ------------------------------------------------------------ attention */
 
-/* Grow a model-owned bf16 staging buffer to count elements. */
-static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
-                       const char *what)
+/* Grow a model-owned staging buffer of element type dt to count
+ * elements. */
+static int ensure_typed(struct hipb_backend *b, hipb_mem *buf, size_t count,
+                        int dt, const char *what)
 {
     if (*buf && hipb_count(*buf) >= count)
         return 1;
@@ -391,8 +392,14 @@ static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
         hipb_finish(b);
         hipb_release(buf);
     }
-    *buf = hipb_alloc_typed(b, count, HIPB_BF16, what);
+    *buf = hipb_alloc_typed(b, count, dt, what);
     return *buf != NULL;
+}
+
+static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
+                       const char *what)
+{
+    return ensure_typed(b, buf, count, HIPB_BF16, what);
 }
 
 void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
@@ -461,17 +468,19 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
 
         if (!ensure_bf16(b, &m->q16, cnt, "packed q") ||
             !ensure_bf16(b, &m->k16, cnt, "packed k") ||
-            !ensure_bf16(b, &m->vt16, cnt, "packed v^T"))
+            !ensure_bf16(b, &m->vt16, cnt, "packed v^T") ||
+            !ensure_typed(b, &m->knorm, (size_t)nb * (np / 64), HIPB_F32,
+                          "key block norms"))
             return;
         hipb_run_begin(b);
         err = launch_qkv_pack(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                              b->stream);
+                              (float *)m->knorm->ptr, b->stream);
         hipb_run_end(b, err, "qkv_pack", 0.0);
         if (hipb_failed())
             return;
         hipb_run_begin(b);
         err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                               b->stream);
+                               (const float *)m->knorm->ptr, b->stream);
         hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * hd * nb);
         return;
     }
@@ -495,6 +504,8 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
         !buf_ok("attn_packed", "k16", m->k16, (size_t)nb * np * 64, HIPB_BF16) ||
         !buf_ok("attn_packed", "vt16", m->vt16, (size_t)nb * np * 64,
                 HIPB_BF16) ||
+        !buf_ok("attn_packed", "knorm", m->knorm, (size_t)nb * (np / 64),
+                HIPB_F32) ||
         !opnd_ok("attn_packed", "O", O, N, 64, nb, nb1))
         return;
     if (O.buf->dtype == HIPB_F16) {
@@ -513,7 +524,7 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.odt = O.buf->dtype;
     hipb_run_begin(b);
     err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                           b->stream);
+                           (const float *)m->knorm->ptr, b->stream);
     hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
 }
 
@@ -715,4 +726,5 @@ void sam_path_free(struct sam_model *m)
     hipb_release(&m->q16);
     hipb_release(&m->k16);
     hipb_release(&m->vt16);
+    hipb_release(&m->knorm);
 }

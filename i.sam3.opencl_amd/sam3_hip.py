@@ -81,7 +81,7 @@ class SamModel(ctypes.Structure):
                 ("rope_win", Mem), ("rope_glob", Mem),
                 ("score_cap", ctypes.c_long)] + \
         [(n, Mem) for n in ("x", "xn", "xw", "qkv", "scores", "attn", "xn16",
-                            "q16", "k16", "vt16")]
+                            "q16", "k16", "vt16", "knorm")]
 
 
 _lib = None

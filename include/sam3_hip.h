@@ -187,6 +187,9 @@ struct sam_model {
     hipb_mem x, xn, xw, qkv, scores, attn;
     /* precision=bf16 staging: LN output and packed Q, K, V^T. */
     hipb_mem xn16, q16, k16, vt16;
+    /* Largest |k| of each 64-key block of the packed keys (float,
+     * [unit][Np / 64]): bounds the scores of a block. */
+    hipb_mem knorm;
 };
 
 /* Set up m for the attention path on backend b and allocate its work
@@ -260,9 +263,9 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
                 int npos, float scale);
 
 /* The attention stage of the precision=bf16 path alone, on the packed
- * operands that attn_fused / vit_attention left in m->q16, m->k16 and
- * m->vt16 (nb units of N tokens, RoPE and scale applied); O as in
- * attn_fused. No counterpart in the reference: it is for callers that
+ * operands that attn_fused / vit_attention left in m->q16, m->k16,
+ * m->vt16 and m->knorm (nb units of N tokens, RoPE and scale applied);
+ * O as in attn_fused. No counterpart in the reference: it is for callers that
  * produce packed operands themselves and for timing the kernel. */
 void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O);
 

@@ -38,7 +38,9 @@ def test_every_declared_symbol_is_exported(hip):
 def test_struct_layouts_match_header(hip):
     # Field order of the ctypes mirrors, checked against the header text.
     src = open(HEADER).read()
-    for cls, cname in ((hip.HipbBuf, "hipb_buf"), (hip.Opnd, "opnd")):
+    for cls, cname in ((hip.HipbBuf, "hipb_buf"), (hip.Opnd, "opnd"),
+                       (hip.HipbBackend, "hipb_backend"),
+                       (hip.VitBlock, "vit_block"), (hip.SamModel, "sam_model")):
         body = re.search(r"struct %s \{(.*?)\};" % cname, src, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         fields = re.findall(r"([A-Za-z_][A-Za-z0-9_]*)\s*(?:\[[^\]]*\])?\s*[,;]",

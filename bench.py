@@ -221,8 +221,9 @@ def decoder(hip, be, steps, warmup):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    # Enough untimed launches (about 30 ms) for the engine clock to settle.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline")
     ap.add_argument("--kernel-only", action="store_true",
@@ -263,8 +264,9 @@ def main():
 
     ms = timed(be, glob.attn, args.steps, args.warmup)
     tflops = glob.flops() / ms / 1e9
-    region_ms = timed(be, glob.region, max(5, args.steps // 5), 2)
-    qkv_ms = timed(be, glob.qkv_gemm, max(5, args.steps // 5), 2)
+    sub_steps, sub_warm = max(5, args.steps // 5), max(2, args.warmup // 10)
+    region_ms = timed(be, glob.region, sub_steps, sub_warm)
+    qkv_ms = timed(be, glob.qkv_gemm, sub_steps, sub_warm)
     glob.region()
     be.finish()
 
@@ -272,20 +274,20 @@ def main():
     win.region()
     be.finish()
     wms = timed(be, win.attn, args.steps, args.warmup)
-    w_region = timed(be, win.region, max(5, args.steps // 5), 2)
+    w_region = timed(be, win.region, sub_steps, sub_warm)
 
     # fp32 exact path (f32 MFMA), same shapes, its own backend.
     be32 = hip.Backend(precision="fp32")
     g32 = Block(hip, be32, 0, seed=3)
     g32.region()
     be32.finish()
-    g32_ms = timed(be32, g32.attn_f32, max(3, args.steps // 10), 2)
+    g32_ms = timed(be32, g32.attn_f32, max(3, args.steps // 10), sub_warm)
     w32 = Block(hip, be32, 24, seed=2)
     w32.region()
     be32.finish()
-    w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), 2)
+    w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), sub_warm)
 
-    dec = decoder(hip, be32, max(5, args.steps // 5), 2)
+    dec = decoder(hip, be32, sub_steps, sub_warm)
 
     qkv_flops = 2.0 * 5184 * 1024 * 3072
     result = {

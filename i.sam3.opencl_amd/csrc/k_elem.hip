@@ -183,6 +183,44 @@ extern "C" int launch_rope_apply(float *qkv, long rows, int E, int hd,
     return hipGetLastError();
 }
 
+/* ------------------------------------------------------------ patches */
+
+/* Patch im2col (sam3_kernels.cl:661-672): row t = ty * grid + tx of out
+ * holds the 3 x ps x ps patch at (ty, tx), column c * ps^2 + ky * ps + kx;
+ * out is float or bf16 (ydt). One thread per output element, consecutive
+ * threads along a patch row read consecutive image floats. */
+__global__ __launch_bounds__(256) void k_patch_im2col(
+    const float *__restrict__ img, void *__restrict__ out, int ydt,
+    long total, int side, int grid, int ps)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= total)
+        return;
+    const int K = 3 * ps * ps;
+    const long t = gid / K;
+    const int col = (int)(gid % K);
+    const int c = col / (ps * ps), ky = (col % (ps * ps)) / ps, kx = col % ps;
+    const int ty = (int)(t / grid), tx = (int)(t % grid);
+    const float v = img[((long)c * side + ty * ps + ky) * side + tx * ps + kx];
+
+    if (ydt == DT_BF16)
+        ((uint16_t *)out)[gid] = f2bf(v);
+    else
+        ((float *)out)[gid] = v;
+}
+
+extern "C" int launch_patch_im2col(const float *img, void *out, int ydt,
+                                   int side, int grid, int ps, void *stream)
+{
+    const long total = (long)grid * grid * 3 * ps * ps;
+
+    hipLaunchKernelGGL(k_patch_im2col, dim3((total + 255) / 256), dim3(256),
+                       0, (hipStream_t)stream, img, out, ydt, total, side,
+                       grid, ps);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------ windows */
 
 __global__ __launch_bounds__(256) void k_window_partition(

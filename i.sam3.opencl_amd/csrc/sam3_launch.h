@@ -68,6 +68,10 @@ int launch_window_unpartition_add(float *X, const float *Wd, int H, int W,
                                   int C, int ws, int nwx, void *stream);
 int launch_add_bcast(float *out, const float *a, const float *b, long n,
                      long bmod, void *stream);
+/* Patch im2col of a 3 x side x side image into grid^2 rows of 3 ps^2
+ * float (ydt DT_F32) or bf16 (DT_BF16) columns. */
+int launch_patch_im2col(const float *img, void *out, int ydt, int side,
+                        int grid, int ps, void *stream);
 
 /* Fused attention over nb units of N tokens, head width 64. */
 struct attn_desc {

@@ -21,6 +21,7 @@
 #include <string.h>
 
 #define ENC_EPS 1e-5f   /* ViT LayerNorm eps (sam3_model.c:30) */
+#define SAM_PATCH 14    /* ViT patch side (sam3_model.h:10) */
 #define DEC_HEADS 8     /* decoder heads (sam3_model.c:36) */
 
 struct opnd mat(hipb_mem buf, long off, int ld)
@@ -665,11 +666,103 @@ void vit_attention(struct sam_model *m, const struct vit_block *blk,
     }
 }
 
+/* ------------------------------------------------------------ trunk */
+
+void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused)
+{
+    struct hipb_backend *b = m->hip;
+    const struct geom g = block_geom(m, blk);
+    const int T = m->grid * m->grid, E = m->embed, mlp = m->mlp;
+    const long rows = (long)g.nwin * g.N;
+
+    if (mlp < 1 || !m->tmp || !m->mlpbuf) {
+        hipb_fatal("vit_block: no MLP work buffers (sam_path_init with "
+                   "mlp > 0)");
+        return;
+    }
+    vit_attention(m, blk, unfused);
+    if (hipb_failed())
+        return;
+    /* Projection with residual (sam3_model.c:1015-1022). */
+    if (blk->window) {
+        linear(m, (int)rows, E, E, m->attn, 0, blk->projw, blk->projb, m->tmp,
+               0, ACT_NONE, 0);
+        window_unpartition_add(m, m->x, m->tmp, m->grid, E, g.s, g.nwx);
+    }
+    else
+        linear(m, T, E, E, m->attn, 0, blk->projw, blk->projb, m->x, 0,
+               ACT_NONE, 1);
+    if (hipb_failed())
+        return;
+    /* norm2 and the MLP (sam3_model.c:1024-1027); with precision=bf16 the
+     * normalised tokens and the hidden layer are stored as bf16. */
+    if (b->bf16 && !unfused) {
+        if (!ensure_bf16(b, &m->xn16, (size_t)T * E, "normalized tokens "
+                                                     "(bf16)") ||
+            !ensure_bf16(b, &m->mlp16, (size_t)T * mlp, "mlp (bf16)"))
+            return;
+        layernorm(m, T, E, m->x, m->xn16, blk->n2w, blk->n2b, ENC_EPS,
+                  ACT_NONE);
+        linear(m, T, E, mlp, m->xn16, 0, blk->l1w, blk->l1b, m->mlp16, 0,
+               ACT_GELU, 0);
+        linear(m, T, mlp, E, m->mlp16, 0, blk->l2w, blk->l2b, m->x, 0,
+               ACT_NONE, 1);
+    }
+    else {
+        layernorm(m, T, E, m->x, m->xn, blk->n2w, blk->n2b, ENC_EPS,
+                  ACT_NONE);
+        linear(m, T, E, mlp, m->xn, 0, blk->l1w, blk->l1b, m->mlpbuf, 0,
+               ACT_GELU, 0);
+        linear(m, T, mlp, E, m->mlpbuf, 0, blk->l2w, blk->l2b, m->x, 0,
+               ACT_NONE, 1);
+    }
+}
+
+void sam_encode_trunk(struct sam_model *m, const float *img)
+{
+    struct hipb_backend *b = m->hip;
+    const int G = m->grid, ps = m->patch, E = m->embed, K = 3 * ps * ps;
+    const long T = (long)G * G, side = (long)G * ps;
+    int i, err;
+
+    if (ps < 1 || !img || !m->pe_w || !m->pos || !m->lnpw || !m->lnpb) {
+        hipb_fatal("sam_encode_trunk: no image, patch size or trunk weights");
+        return;
+    }
+    if (!m->mlpbuf || hipb_count(m->mlpbuf) < (size_t)T * K) {
+        hipb_fatal("sam_encode_trunk: work buffers hold fewer than %ld patch "
+                   "columns",
+                   T * K);
+        return;
+    }
+    if (!buf_ok("sam_encode_trunk", "pe_w", m->pe_w, (size_t)E * K, -1) ||
+        !buf_ok("sam_encode_trunk", "pos", m->pos, (size_t)T * E, HIPB_F32) ||
+        !ensure_typed(b, &m->img, (size_t)3 * side * side, HIPB_F32, "image"))
+        return;
+    hipb_write(b, m->img, 0, img, (size_t)3 * side * side * sizeof(float));
+    if (hipb_failed())
+        return;
+    /* Patch embedding (no bias), tiled position embedding, ln_pre
+     * (sam3_model.c:1119-1130). */
+    hipb_run_begin(b);
+    err = launch_patch_im2col(m->img->ptr, m->mlpbuf->ptr, HIPB_F32,
+                              (int)side, G, ps, b->stream);
+    hipb_run_end(b, err, "patch_im2col", 0.0);
+    if (hipb_failed())
+        return;
+    linear(m, (int)T, K, E, m->mlpbuf, 0, m->pe_w, NULL, m->x, 0, ACT_NONE,
+           0);
+    add_bcast(m, m->x, m->x, m->pos, T * E, T * E);
+    layernorm(m, T, E, m->x, m->x, m->lnpw, m->lnpb, ENC_EPS, ACT_NONE);
+    for (i = 0; i < m->depth && !hipb_failed(); i++)
+        vit_block(m, &m->blocks[i], 0);
+}
+
 /* ------------------------------------------------------------ setup */
 
 void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
-                   int embed, int heads, int hd, struct vit_block *blocks,
-                   int depth)
+                   int embed, int heads, int hd, int mlp,
+                   struct vit_block *blocks, int depth)
 {
     const size_t f = sizeof(float);
     const long T = (long)grid * grid;
@@ -685,7 +778,9 @@ void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
     m->hd = hd;
     m->blocks = blocks;
     m->depth = depth;
-    if (grid < 1 || hd != 64 || embed != heads * hd) {
+    m->mlp = mlp;
+    m->patch = SAM_PATCH;
+    if (grid < 1 || hd != 64 || embed != heads * hd || mlp < 0) {
         hipb_fatal("Unsupported attention head width %d", hd);
         return;
     }
@@ -710,6 +805,15 @@ void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
     m->xw = hipb_alloc(b, rows * embed * f, "window partition");
     m->qkv = hipb_alloc(b, rows * 3 * embed * f, "qkv");
     m->attn = hipb_alloc(b, rows * embed * f, "attention output");
+    if (mlp > 0) {
+        /* MLP hidden, also the patch columns (sam3_model.c:841-843). */
+        const long cols = mlp > 3 * SAM_PATCH * SAM_PATCH
+                              ? mlp
+                              : 3 * SAM_PATCH * SAM_PATCH;
+
+        m->tmp = hipb_alloc(b, rows * embed * f, "projection");
+        m->mlpbuf = hipb_alloc(b, T * cols * f, "mlp");
+    }
 }
 
 void sam_path_free(struct sam_model *m)
@@ -727,4 +831,8 @@ void sam_path_free(struct sam_model *m)
     hipb_release(&m->k16);
     hipb_release(&m->vt16);
     hipb_release(&m->knorm);
+    hipb_release(&m->img);
+    hipb_release(&m->tmp);
+    hipb_release(&m->mlpbuf);
+    hipb_release(&m->mlp16);
 }

@@ -33,7 +33,7 @@ EXPORTS = [
     "sam_path_init", "sam_path_free", "mat", "bmat", "gemm", "linear",
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
     "window_partition", "window_unpartition_add", "mha", "attn_fused",
-    "attn_packed", "vit_attention",
+    "attn_packed", "vit_attention", "vit_block", "sam_encode_trunk",
 ]
 
 
@@ -81,7 +81,10 @@ class SamModel(ctypes.Structure):
                 ("rope_win", Mem), ("rope_glob", Mem),
                 ("score_cap", ctypes.c_long)] + \
         [(n, Mem) for n in ("x", "xn", "xw", "qkv", "scores", "attn", "xn16",
-                            "q16", "k16", "vt16", "knorm")]
+                            "q16", "k16", "vt16", "knorm")] + \
+        [("patch", ctypes.c_int)] + \
+        [(n, Mem) for n in ("pe_w", "pos", "lnpw", "lnpb", "img", "tmp",
+                            "mlpbuf", "mlp16")]
 
 
 _lib = None
@@ -132,7 +135,7 @@ def lib():
     L.hipb_timer_start.argtypes = [BP]
     L.hipb_timer_stop.argtypes = [BP]
     L.hipb_timer_stop.restype = c_float
-    L.sam_path_init.argtypes = [MP, BP, c_int, c_int, c_int, c_int,
+    L.sam_path_init.argtypes = [MP, BP, c_int, c_int, c_int, c_int, c_int,
                                 ctypes.POINTER(VitBlock), c_int]
     L.sam_path_free.argtypes = [MP]
     L.mat.argtypes = [Mem, c_long, c_int]
@@ -157,6 +160,8 @@ def lib():
                              Mem, c_int, c_float]
     L.attn_packed.argtypes = [MP, c_int, c_int, c_int, Opnd]
     L.vit_attention.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
+    L.vit_block.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
+    L.sam_encode_trunk.argtypes = [MP, ctypes.c_void_p]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
     return L
@@ -295,13 +300,13 @@ class Model:
     """struct sam_model for the attention path (sam_path_init)."""
 
     def __init__(self, backend, grid=0, embed=1024, heads=16, hd=64,
-                 blocks=()):
+                 blocks=(), mlp=0):
         self.backend = backend
         self.m = SamModel()
         self._blocks = (VitBlock * max(1, len(blocks)))(*blocks)
         if grid:
             _lib.sam_path_init(ctypes.byref(self.m), backend.ptr, grid, embed,
-                               heads, hd, self._blocks, len(blocks))
+                               heads, hd, mlp, self._blocks, len(blocks))
             _check()
         else:
             self.m.hip = ctypes.pointer(backend._b)
@@ -378,6 +383,16 @@ def attn_packed(m, N, nb, nb1, O):
 
 def vit_attention(m, block, unfused=False):
     _call(_lib.vit_attention, m.ptr, ctypes.byref(block), int(bool(unfused)))
+
+
+def vit_block(m, block, unfused=False):
+    _call(_lib.vit_block, m.ptr, ctypes.byref(block), int(bool(unfused)))
+
+
+def sam_encode_trunk(m, img):
+    """img: float32 [3, side, side] host array."""
+    img = np.ascontiguousarray(img, np.float32)
+    _call(_lib.sam_encode_trunk, m.ptr, img.ctypes.data)
 
 
 def prof_table():

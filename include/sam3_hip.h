@@ -175,7 +175,7 @@ struct vit_block {
 };
 
 /* The part of struct sam_model (sam3_model.h:41-117) the attention path
- * reads and writes. */
+ * and the image encoder trunk read and write. */
 struct sam_model {
     struct hipb_backend *hip; /* the reference's m->ocl */
     int embed, depth, heads, hd, mlp;
@@ -190,17 +190,27 @@ struct sam_model {
     /* Largest |k| of each 64-key block of the packed keys (float,
      * [unit][Np / 64]): bounds the scores of a block. */
     hipb_mem knorm;
+    /* Trunk prologue (sam3_model.h:46-49): patch side, patch embedding
+     * [E][3 patch^2] (no bias), position embedding tiled to [grid^2][E]
+     * (sam3_model.c:482-502), ln_pre. */
+    int patch;
+    hipb_mem pe_w, pos, lnpw, lnpb;
+    /* Trunk work buffers (sam3_model.c:853-861): image
+     * [3][grid patch]^2, projection output [rows][E], MLP hidden /
+     * patch columns; mlp16 the bf16 MLP hidden of precision=bf16. */
+    hipb_mem img, tmp, mlpbuf, mlp16;
 };
 
-/* Set up m for the attention path on backend b and allocate its work
- * buffers for the given blocks, sized like alloc_buffers
- * (sam3_model.c:815-854): rows = max over blocks of nwin * N, score
- * buffer = min(max_alloc, 512 MiB); fatal if one head's scores do not
- * fit (sam3_model.c:833-837). No counterpart: the reference does this
- * inside sam_load. */
+/* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =
+ * MLP width) on backend b and allocate its work buffers for the given
+ * blocks, sized like alloc_buffers (sam3_model.c:815-861): rows = max
+ * over blocks of nwin * N, score buffer = min(max_alloc, 512 MiB); fatal
+ * if one head's scores do not fit (sam3_model.c:833-837). The weights
+ * (blocks, pe_w, pos, lnpw, lnpb, rope tables) are the caller's. No
+ * counterpart: the reference does this inside sam_load. */
 void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
-                   int embed, int heads, int hd, struct vit_block *blocks,
-                   int depth);
+                   int embed, int heads, int hd, int mlp,
+                   struct vit_block *blocks, int depth);
 void sam_path_free(struct sam_model *m);
 
 struct opnd mat(hipb_mem buf, long off, int ld);                 /* ops.h:48 */
@@ -276,6 +286,21 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O);
  * (gemm -> softmax_rows -> gemm per head chunk, through m->scores). */
 void vit_attention(struct sam_model *m, const struct vit_block *blk,
                    int unfused);
+
+/* One ViT block on m->x in place (vit_block, sam3_model.c:981-1028):
+ * the attention region, the projection with residual (windowed blocks
+ * through m->tmp and window_unpartition_add), norm2 and the erf-GELU MLP
+ * with residual. With precision=bf16 the GEMM operands are bf16 (norm2
+ * output and MLP hidden stored as bf16), accumulation and the residual
+ * stream float. unfused: the reference's attention operator sequence. */
+void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused);
+
+/* Image encoder trunk (sam_encode_trunk, sam3_model.c:1112-1135): the
+ * host image img (3 x side x side floats, side = grid * patch) is
+ * written to the device, patch im2col + patch GEMM (no bias) + position
+ * embedding + ln_pre give m->x, then the m->depth blocks run in order.
+ * The result stays in m->x; the caller synchronises (hipb_finish). */
+void sam_encode_trunk(struct sam_model *m, const float *img);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,14 @@ def lib():
         L.or_sdpa_f64.argtypes = [_i, _i, _i, _p, _i, _p, _i, _p, _i, _p, _i,
                                   ctypes.c_double]
         L.or_threads.restype = _i
+        L.or_patch_im2col.argtypes = [_p, _p, _i, _i, _i]
+        L.or_vit_block.argtypes = [_i, _p, _i, _i, _i, _i, _i,
+                                   ctypes.POINTER(BlockW), _p, _l]
+        L.or_vit_block.restype = _i
+        L.or_encode_trunk.argtypes = [_i, _p, _i, _i, _i, _i, _i, _i, _p, _p,
+                                      _p, _p, ctypes.POINTER(BlockW), _i, _p,
+                                      _p, _l, _p]
+        L.or_encode_trunk.restype = _i
         _lib = L
     return _lib
 
@@ -203,6 +211,69 @@ def vit_attention(x, grid, E, heads, hd, ws, n1w, n1b, qkvw, qkvb, rope,
     if hc < 1:
         raise ValueError("score buffer cannot hold one head")
     return (attn, qkv) if want_qkv else attn
+
+
+class BlockW(ctypes.Structure):
+    """struct or_block_w."""
+    _fields_ = [(n, _p) for n in ("n1w", "n1b", "qkvw", "qkvb", "projw",
+                                  "projb", "n2w", "n2b", "l1w", "l1b", "l2w",
+                                  "l2b")] + [("window", _i)]
+
+
+BLOCK_KEYS = ("n1w", "n1b", "qkvw", "qkvb", "projw", "projb", "n2w", "n2b",
+              "l1w", "l1b", "l2w", "l2b")
+
+
+def _block_w(w, keep):
+    """BlockW from a dict of weight arrays (float32 copies kept alive in
+    `keep`)."""
+    b = BlockW()
+    for k in BLOCK_KEYS:
+        a = _f32(w[k])
+        keep.append(a)
+        setattr(b, k, a.ctypes.data)
+    b.window = int(w["window"])
+    return b
+
+
+def patch_im2col(img, side, grid, ps):
+    img = _f32(img)
+    out = np.zeros((grid * grid, 3 * ps * ps), np.float32)
+    lib().or_patch_im2col(_ptr(img), _ptr(out), side, grid, ps)
+    return out
+
+
+def vit_block(x, grid, E, heads, hd, mlp, w, rope,
+              score_cap=(512 << 20) // 4, cpu=True):
+    """One ViT block (dict w of weights, w["window"] the window side) on
+    x [grid^2, E]; returns the new x."""
+    keep = []
+    b = _block_w(w, keep)
+    x = np.array(x, np.float32, copy=True)
+    rope = _f32(rope)
+    if lib().or_vit_block(int(cpu), _ptr(x), grid, E, heads, hd, mlp,
+                          ctypes.byref(b), _ptr(rope), score_cap) < 1:
+        raise ValueError("score buffer cannot hold one head")
+    return x
+
+
+def encode_trunk(img, grid, ps, E, heads, hd, mlp, pe_w, pos, lnpw, lnpb,
+                 blocks, rope_win, rope_glob, score_cap=(512 << 20) // 4,
+                 cpu=True):
+    """Image encoder trunk: img [3, side, side] -> x [grid^2, E]."""
+    keep = []
+    arr = (BlockW * len(blocks))(*[_block_w(w, keep) for w in blocks])
+    img, pe_w, pos = _f32(img), _f32(pe_w), _f32(pos)
+    lnpw, lnpb = _f32(lnpw), _f32(lnpb)
+    rw = _f32(rope_win) if rope_win is not None else None
+    rg = _f32(rope_glob) if rope_glob is not None else None
+    x = np.zeros((grid * grid, E), np.float32)
+    if lib().or_encode_trunk(int(cpu), _ptr(img), grid, ps, E, heads, hd, mlp,
+                             _ptr(pe_w), _ptr(pos), _ptr(lnpw), _ptr(lnpb),
+                             arr, len(blocks), _ptr(rw), _ptr(rg), score_cap,
+                             _ptr(x)) < 0:
+        raise ValueError("score buffer cannot hold one head")
+    return x
 
 
 def sdpa_f64(Q, K, V, scale):

@@ -20,6 +20,8 @@
  *   or_window_partition/_add    index algebra: round trip, padding
  *   or_attn_fewkeys/_manykeys   fp64 SDPA, Nk = 1, Q = 0, key permutation
  *   or_vit_attention            fp64 pipeline, window = grid == global
+ *   or_patch_im2col             index algebra (numpy reshape of patches)
+ *   or_vit_block / _encode_trunk fp64 textbook block and trunk
  * and, for every function, the golden vectors of the reference's own
  * kernels (tests/golden, sam3_kernels.cl run unchanged through the ROCm
  * OpenCL runtime): bit-exact for RoPE and window data movement, rel-L2
@@ -595,6 +597,97 @@ int or_vit_attention(int cpu, const float *x, int grid, int E, int heads,
     if (!qkv_out)
         free(qkv);
     return (int)hc;
+}
+
+void or_patch_im2col(const float *img, float *out, int side, int grid, int ps)
+{
+    const int K = 3 * ps * ps;
+    const long T = (long)grid * grid;
+    long t;
+
+#pragma omp parallel for schedule(static)
+    for (t = 0; t < T; t++) {
+        const int ty = (int)(t / grid), tx = (int)(t % grid);
+        int col;
+
+        for (col = 0; col < K; col++) {
+            const int c = col / (ps * ps), ky = (col % (ps * ps)) / ps,
+                      kx = col % ps;
+
+            out[t * K + col] =
+                img[((long)c * side + ty * ps + ky) * side + tx * ps + kx];
+        }
+    }
+}
+
+int or_vit_block(int cpu, float *x, int grid, int E, int heads, int hd,
+                 int mlp, const struct or_block_w *b, const float *rope,
+                 long score_cap)
+{
+    const int s = b->window ? b->window : grid;
+    const int nwx = (grid + s - 1) / s, N = s * s;
+    const long T = (long)grid * grid, rows = (long)nwx * nwx * N;
+    float *attn = malloc(sizeof(float) * rows * E);
+    float *xn = malloc(sizeof(float) * T * E);
+    float *h = malloc(sizeof(float) * T * mlp);
+    int hc = or_vit_attention(cpu, x, grid, E, heads, hd, b->window, b->n1w,
+                              b->n1b, b->qkvw, b->qkvb, rope, score_cap, attn,
+                              NULL);
+
+    if (hc > 0) {
+        /* Projection (sam3_model.c:1015-1022). */
+        if (b->window) {
+            float *tmp = malloc(sizeof(float) * rows * E);
+
+            or_gemm_dispatch(cpu, (int)rows, E, E, attn, 0, E, 0, 0, b->projw,
+                             0, E, 0, 0, 1, tmp, 0, E, 0, 0, 1, 1, b->projb,
+                             NULL, 0, 1.0f, OR_ACT_NONE);
+            or_window_unpartition_add(x, tmp, grid, grid, E, s, nwx);
+            free(tmp);
+        }
+        else
+            or_gemm_dispatch(cpu, (int)T, E, E, attn, 0, E, 0, 0, b->projw, 0,
+                             E, 0, 0, 1, x, 0, E, 0, 0, 1, 1, b->projb, x, 0,
+                             1.0f, OR_ACT_NONE);
+        /* norm2 and the MLP (sam3_model.c:1024-1027). */
+        or_layernorm(x, xn, T, E, b->n2w, b->n2b, 1e-5f, OR_ACT_NONE);
+        or_gemm_dispatch(cpu, (int)T, mlp, E, xn, 0, E, 0, 0, b->l1w, 0, E, 0,
+                         0, 1, h, 0, mlp, 0, 0, 1, 1, b->l1b, NULL, 0, 1.0f,
+                         OR_ACT_GELU);
+        or_gemm_dispatch(cpu, (int)T, E, mlp, h, 0, mlp, 0, 0, b->l2w, 0, mlp,
+                         0, 0, 1, x, 0, E, 0, 0, 1, 1, b->l2b, x, 0, 1.0f,
+                         OR_ACT_NONE);
+    }
+    free(attn);
+    free(xn);
+    free(h);
+    return hc;
+}
+
+int or_encode_trunk(int cpu, const float *img, int grid, int ps, int E,
+                    int heads, int hd, int mlp, const float *pe_w,
+                    const float *pos, const float *lnpw, const float *lnpb,
+                    const struct or_block_w *blocks, int depth,
+                    const float *rope_win, const float *rope_glob,
+                    long score_cap, float *x)
+{
+    const long T = (long)grid * grid;
+    const int K = 3 * ps * ps;
+    float *col = malloc(sizeof(float) * T * K);
+    int i, ok = 0;
+
+    or_patch_im2col(img, col, grid * ps, grid, ps);
+    or_gemm_dispatch(cpu, (int)T, E, K, col, 0, K, 0, 0, pe_w, 0, K, 0, 0, 1,
+                     x, 0, E, 0, 0, 1, 1, NULL, NULL, 0, 1.0f, OR_ACT_NONE);
+    or_add_bcast(x, x, pos, T * E, T * E);
+    or_layernorm(x, x, T, E, lnpw, lnpb, 1e-5f, OR_ACT_NONE);
+    free(col);
+    for (i = 0; i < depth && ok == 0; i++)
+        if (or_vit_block(cpu, x, grid, E, heads, hd, mlp, &blocks[i],
+                         blocks[i].window ? rope_win : rope_glob,
+                         score_cap) < 0)
+            ok = -1;
+    return ok;
 }
 
 /* Textbook softmax attention in double precision. */

@@ -101,6 +101,41 @@ int or_vit_attention(int cpu, const float *x, int grid, int E, int heads,
                      const float *qkvw, const float *qkvb, const float *rope,
                      long score_cap, float *attn, float *qkv_out);
 
+/* Patch im2col of a 3 x side x side channel-major image into grid^2
+ * rows of 3 * ps * ps columns, column order c * ps^2 + ky * ps + kx
+ * (sam3_kernels.cl:661-672). */
+void or_patch_im2col(const float *img, float *out, int side, int grid, int ps);
+
+/* Weights of one ViT block (struct vit_block, sam3_model.h); window is
+ * the window side, 0 for a global block. */
+struct or_block_w {
+    const float *n1w, *n1b, *qkvw, *qkvb, *projw, *projb;
+    const float *n2w, *n2b, *l1w, *l1b, *l2w, *l2b;
+    int window;
+};
+
+/* One ViT block on x [grid^2, E] in place (vit_block,
+ * sam3_model.c:981-1028): the attention region of or_vit_attention, the
+ * projection with residual (windowed: into a temporary, then
+ * window_unpartition_add), norm2 and the erf-GELU MLP with residual.
+ * rope is the block's table (windowed: window^2 positions, global:
+ * grid^2). Returns the heads per score chunk, or -1. */
+int or_vit_block(int cpu, float *x, int grid, int E, int heads, int hd,
+                 int mlp, const struct or_block_w *b, const float *rope,
+                 long score_cap);
+
+/* Trunk of the image encoder (sam_encode_trunk, sam3_model.c:1112-1135):
+ * patch im2col of img (3 x side x side, side = grid * ps) and the patch
+ * GEMM without bias, + pos [grid^2, E], ln_pre in place, then `depth`
+ * blocks (windowed blocks use rope_win, global ones rope_glob). x [grid^2,
+ * E] receives the result. Returns 0, or -1 for an unsupported shape. */
+int or_encode_trunk(int cpu, const float *img, int grid, int ps, int E,
+                    int heads, int hd, int mlp, const float *pe_w,
+                    const float *pos, const float *lnpw, const float *lnpb,
+                    const struct or_block_w *blocks, int depth,
+                    const float *rope_win, const float *rope_glob,
+                    long score_cap, float *x);
+
 /* Brute-force scaled dot-product attention in double precision,
  * O[i, :] = sum_j softmax_j(scale * q_i . k_j) v_j, for pinning. */
 void or_sdpa_f64(int Nq, int Nk, int d, const double *Q, int ldq,

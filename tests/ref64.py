@@ -102,3 +102,35 @@ def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def patch_im2col(img, grid, ps):
+    """[3, side, side] -> [grid^2, 3 * ps^2], column c * ps^2 + ky * ps + kx
+    (numpy reshape of the patch grid)."""
+    p = img.reshape(3, grid, ps, grid, ps).transpose(1, 3, 0, 2, 4)
+    return p.reshape(grid * grid, 3 * ps * ps)
+
+
+def vit_block(x, grid, E, heads, hd, mlp, w, cs):
+    """One ViT block: x + proj(attn(LN1 x)) (windowed: unpartitioned),
+    then + fc2(gelu(fc1(LN2 x)))."""
+    ws = w["window"]
+    attn, _ = vit_attention(x, grid, E, heads, hd, ws, w["n1w"], w["n1b"],
+                            w["qkvw"], w["qkvb"], cs)
+    y = attn @ w["projw"].astype(np.float64).T + w["projb"]
+    if ws:
+        y = window_unpartition(y, grid, grid, ws)
+    x = x.astype(np.float64) + y
+    h = gelu(layernorm(x, w["n2w"], w["n2b"]) @ w["l1w"].astype(np.float64).T
+             + w["l1b"])
+    return x + h @ w["l2w"].astype(np.float64).T + w["l2b"]
+
+
+def encode_trunk(img, grid, ps, E, heads, hd, mlp, pe_w, pos, lnpw, lnpb,
+                 blocks, rope_win, rope_glob):
+    x = patch_im2col(img.astype(np.float64), grid, ps) @ pe_w.astype(np.float64).T
+    x = layernorm(x + pos, lnpw, lnpb)
+    for w in blocks:
+        x = vit_block(x, grid, E, heads, hd, mlp, w,
+                      rope_win if w["window"] else rope_glob)
+    return x

@@ -1,0 +1,120 @@
+"""GPU parity of the image encoder trunk against the oracle: whole ViT
+blocks (vit_block, sam3_model.c:981-1028: attention region, projection
+with residual / window_unpartition_add, norm2, erf-GELU MLP with residual)
+and the trunk prologue (sam_encode_trunk, sam3_model.c:1112-1135: patch
+im2col, patch GEMM, tiled position embedding, ln_pre).
+
+Bars: rel-L2 <= 2e-5 on the fp32 path, <= 2e-2 on the bf16 path, on the
+block's output tokens; max-abs printed with every check. Inputs are
+random-init weights (tests/backbone_case.py) and N(0, 1) tokens.
+"""
+import numpy as np
+import pytest
+
+import backbone_case as bc
+from gpu_common import report
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 2e-5, "bf16": 2e-2}
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam3_hip
+    return sam3_hip
+
+
+@pytest.fixture(scope="module", params=["fp32", "bf16"])
+def be(hip, request):
+    b = hip.Backend(precision=request.param)
+    b.precision = request.param
+    yield b
+    b.free()
+
+
+def upload_block(hip, be, w):
+    blk = hip.VitBlock()
+    for k in ("n1w", "n1b", "qkvb", "projb", "n2w", "n2b", "l1b", "l2b"):
+        setattr(blk, k, be.upload(w[k]))
+    for k in ("qkvw", "projw", "l1w", "l2w"):
+        setattr(blk, k, be.upload_weight(w[k]))
+    blk.window = w["window"]
+    return blk
+
+
+def run_block(hip, be, orc, grid, E, heads, mlp, ws, seed, unfused=False):
+    g = np.random.default_rng(seed)
+    w = bc.block_weights(g, E, mlp, ws)
+    x = g.standard_normal((grid * grid, E), dtype=np.float32)
+    table = orc.rope_table(ws if ws else grid)
+    blk = upload_block(hip, be, w)
+    m = hip.Model(be, grid=grid, embed=E, heads=heads, blocks=[blk], mlp=mlp)
+    if ws:
+        m.m.rope_win = be.upload(table)
+    else:
+        m.m.rope_glob = be.upload(table)
+    be.write(m.m.x, 0, x)
+    print("vit_block grid=%d E=%d mlp=%d ws=%d unfused=%d %s" %
+          (grid, E, mlp, ws, unfused, be.precision), flush=True)
+    hip.vit_block(m, blk, unfused)
+    got = be.read(m.m.x, grid * grid * E).reshape(grid * grid, E)
+    m.free()
+    want = orc.vit_block(x, grid, E, heads, 64, mlp, w, table)
+    return got, want
+
+
+@pytest.mark.parametrize("grid,ws", [(12, 6), (12, 0), (10, 4)])
+@pytest.mark.parametrize("unfused", [False, True])
+def test_vit_block_small(hip, be, orc, grid, ws, unfused):
+    got, want = run_block(hip, be, orc, grid, 128, 2, 256, ws, 70 + grid + ws,
+                          unfused)
+    assert report("vit_block grid=%d ws=%d unfused=%d %s" %
+                  (grid, ws, unfused, be.precision), got, want) <= TOL[be.precision]
+
+
+@pytest.mark.parametrize("ws", [24, 0])
+def test_vit_block_full_size(hip, be, orc, ws):
+    """One block of the 72 x 72 x 1024 trunk, 16 heads, MLP 4096."""
+    got, want = run_block(hip, be, orc, 72, 1024, 16, 4096, ws, 80 + ws)
+    assert report("vit_block full ws=%d %s" % (ws, be.precision), got,
+                  want) <= TOL[be.precision]
+
+
+def trunk(hip, be, orc, grid, ps, E, heads, mlp, windows, seed):
+    img, pe_w, pos, lnpw, lnpb, blocks = bc.trunk_case(seed, grid, ps, E, mlp,
+                                                       windows)
+    blks = [upload_block(hip, be, w) for w in blocks]
+    wins = [w for w in windows if w]
+    rw = orc.rope_table(wins[0]) if wins else None
+    rg = orc.rope_table(grid)
+    m = hip.Model(be, grid=grid, embed=E, heads=heads, blocks=blks, mlp=mlp)
+    m.m.patch = ps
+    m.m.pe_w = be.upload_weight(pe_w)
+    m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(lnpw), be.upload(lnpb)
+    if rw is not None:
+        m.m.rope_win = be.upload(rw)
+    m.m.rope_glob = be.upload(rg)
+    print("trunk grid=%d ps=%d E=%d depth=%d %s" %
+          (grid, ps, E, len(windows), be.precision), flush=True)
+    hip.sam_encode_trunk(m, img)
+    be.finish()
+    got = be.read(m.m.x, grid * grid * E).reshape(grid * grid, E)
+    m.free()
+    want = orc.encode_trunk(img, grid, ps, E, heads, 64, mlp, pe_w, pos, lnpw,
+                            lnpb, blocks, rw, rg)
+    return got, want
+
+
+def test_encode_trunk_small(hip, be, orc):
+    got, want = trunk(hip, be, orc, 8, 4, 128, 2, 256, [4, 0, 4], 90)
+    assert report("trunk small %s" % be.precision, got,
+                  want) <= TOL[be.precision]
+
+
+def test_trunk_prologue_full_size(hip, be, orc):
+    """Patch embedding of a 1008 x 1008 image (patch 14 -> 72 x 72 tokens
+    of width 1024), position embedding and ln_pre, no blocks."""
+    got, want = trunk(hip, be, orc, 72, 14, 1024, 16, 4096, [], 91)
+    assert report("trunk prologue full %s" % be.precision, got,
+                  want) <= TOL[be.precision]

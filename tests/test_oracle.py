@@ -358,3 +358,54 @@ def test_vit_attention_structure(orc):
     with pytest.raises(ValueError):
         orc.vit_attention(x, grid, E, heads, hd, 0, n1w, n1b, qkvw, qkvb, cs,
                           score_cap=10)
+
+
+# ---------------------------------------------------------------- backbone
+
+def test_patch_im2col(orc):
+    g = rng(41)
+    grid, ps = 5, 3
+    img = g.standard_normal((3, grid * ps, grid * ps)).astype(np.float32)
+    got = orc.patch_im2col(img, grid * ps, grid, ps)
+    np.testing.assert_array_equal(got, ref64.patch_im2col(img, grid, ps))
+
+
+@pytest.mark.parametrize("ws", [0, 4])
+@pytest.mark.parametrize("cpu", [1, 0])
+def test_vit_block_vs_float64(orc, ws, cpu):
+    import backbone_case as bc
+    grid, E, heads, hd, mlp = 8, 128, 2, 64, 256
+    g = rng(50 + ws)
+    w = bc.block_weights(g, E, mlp, ws)
+    x = g.standard_normal((grid * grid, E)).astype(np.float32)
+    cs = orc.rope_table(ws if ws else grid, hd)
+    got = orc.vit_block(x, grid, E, heads, hd, mlp, w, cs, cpu=cpu)
+    want = ref64.vit_block(x, grid, E, heads, hd, mlp, w, cs)
+    assert ref64.rel_l2(got, want) < 5e-6
+
+
+def test_vit_block_teeth(orc):
+    """A block whose residual skips the MLP input normalisation (norm2
+    weights swapped for norm1's) is caught by the float64 check."""
+    import backbone_case as bc
+    grid, E, heads, hd, mlp = 6, 128, 2, 64, 256
+    g = rng(57)
+    w = bc.block_weights(g, E, mlp, 0)
+    x = g.standard_normal((grid * grid, E)).astype(np.float32)
+    cs = orc.rope_table(grid, hd)
+    bad = dict(w, n2w=w["n1w"], n2b=w["n1b"])
+    got = orc.vit_block(x, grid, E, heads, hd, mlp, bad, cs)
+    assert ref64.rel_l2(got, ref64.vit_block(x, grid, E, heads, hd, mlp, w, cs)) > 1e-3
+
+
+def test_encode_trunk_vs_float64(orc):
+    import backbone_case as bc
+    grid, ps, E, heads, hd, mlp = 8, 4, 128, 2, 64, 256
+    img, pe_w, pos, lnpw, lnpb, blocks = bc.trunk_case(60, grid, ps, E, mlp,
+                                                       [4, 0, 4])
+    rw, rg = orc.rope_table(4, hd), orc.rope_table(grid, hd)
+    got = orc.encode_trunk(img, grid, ps, E, heads, hd, mlp, pe_w, pos, lnpw,
+                           lnpb, blocks, rw, rg)
+    want = ref64.encode_trunk(img, grid, ps, E, heads, hd, mlp, pe_w, pos,
+                              lnpw, lnpb, blocks, rw, rg)
+    assert ref64.rel_l2(got, want) < 2e-5

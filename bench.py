@@ -141,6 +141,101 @@ def timed(be, fn, steps, warmup):
     return ms / steps
 
 
+def backbone_flops(grid=72, E=1024, mlp=4096, ps=14, depth=32, ws=24,
+                   glob_at=(7, 15, 23, 31)):
+    """Algorithmic FLOPs of one image through the trunk: patch GEMM, per
+    block QKV / projection / MLP GEMMs and attention (4 N^2 64 per window
+    and head)."""
+    T = grid * grid
+    f = 2.0 * T * 3 * ps * ps * E
+    for i in range(depth):
+        s = grid if i in glob_at else ws
+        nwin = (-(-grid // s)) ** 2
+        f += 2.0 * T * E * (3 * E + E + 2 * mlp)
+        f += 4.0 * (s * s) ** 2 * 64 * (E // 64) * nwin
+    return f
+
+
+def backbone(hip, steps, warmup):
+    """Image encoder trunk, end to end (sam_encode_trunk): 1008 x 1008 x 3
+    image ~ U(0, 1) normalised (x - 0.5) / 0.5, patch 14 -> 72 x 72 tokens
+    of width 1024, 32 blocks (global attention at blocks 7, 15, 23, 31,
+    24 x 24 windows elsewhere), 16 heads x 64, MLP 4096 erf-GELU, 2D RoPE;
+    random-init weights (Xavier-uniform linears, U(+-1/sqrt(fan_in))
+    biases, LayerNorm 1 / 0, position embedding tiled from a 24 x 24
+    grid). ms per image for precision=bf16 and =fp32, and the attention
+    kernels' share of a profiled pass."""
+    grid, E, H, mlp, ps, depth = 72, 1024, 16, 4096, 14, 32
+    glob_at = (7, 15, 23, 31)
+    g = np.random.default_rng(17)
+
+    def xavier(o, i):
+        b = math.sqrt(6.0 / (i + o))
+        return (g.random((o, i), dtype=np.float32) * (2 * b) - b)
+
+    def bias(n, fan):
+        b = 1.0 / math.sqrt(fan)
+        return (g.random(n, dtype=np.float32) * (2 * b) - b)
+
+    bes = {p: hip.Backend(precision=p) for p in ("bf16", "fp32")}
+    blocks = {p: [] for p in bes}
+    ones, zeros = np.ones(E, np.float32), np.zeros(E, np.float32)
+    for i in range(depth):
+        w = {"qkvw": xavier(3 * E, E), "qkvb": bias(3 * E, E),
+             "projw": xavier(E, E), "projb": bias(E, E),
+             "l1w": xavier(mlp, E), "l1b": bias(mlp, E),
+             "l2w": xavier(E, mlp), "l2b": bias(E, mlp)}
+        for p, be in bes.items():
+            blk = hip.VitBlock()
+            for k in ("qkvw", "projw", "l1w", "l2w"):
+                setattr(blk, k, be.upload_weight(w[k]))
+            for k in ("qkvb", "projb", "l1b", "l2b"):
+                setattr(blk, k, be.upload(w[k]))
+            blk.n1w, blk.n2w = be.upload(ones), be.upload(ones)
+            blk.n1b, blk.n2b = be.upload(zeros), be.upload(zeros)
+            blk.window = 0 if i in glob_at else 24
+            blocks[p].append(blk)
+    pe_w = xavier(E, 3 * ps * ps)
+    pe = (0.02 * g.standard_normal((24 * 24, E))).astype(np.float32)
+    yy, xx = np.divmod(np.arange(grid * grid), grid)
+    pos = np.ascontiguousarray(pe[(yy % 24) * 24 + xx % 24])
+    side = grid * ps
+    img = ((g.random((3, side, side), dtype=np.float32) - 0.5) / 0.5)
+    out = {"workload": "image encoder trunk: 1008x1008x3 image, patch 14 -> "
+                       "72x72 tokens x 1024, 32 blocks (global at 7/15/23/31, "
+                       "24x24 windows), 16 heads x 64, MLP 4096, 2D RoPE",
+           "tflop_per_img": round(backbone_flops() / 1e12, 3)}
+    for p, be in bes.items():
+        m = hip.Model(be, grid=grid, embed=E, heads=H, blocks=blocks[p],
+                      mlp=mlp)
+        m.m.patch = ps
+        m.m.pe_w = be.upload_weight(pe_w)
+        m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(ones), be.upload(zeros)
+        m.m.rope_win = be.upload(rope_table(24))
+        m.m.rope_glob = be.upload(rope_table(grid))
+        ms = timed(be, lambda: hip.sam_encode_trunk(m, img), steps, warmup)
+        # One profiled pass (per-operator events, the reference's
+        # I_SAM3_OPENCL_PROFILE table) for the attention share.
+        hip.prof_reset()
+        be._b.profile = 1
+        hip.sam_encode_trunk(m, img)
+        be.finish()
+        be._b.profile = 0
+        tab = hip.prof_table()
+        tot = sum(r[1] for r in tab)
+        att = sum(r[1] for r in tab if r[0] in ("attn_bf16", "qkv_pack",
+                                                "attn_f32"))
+        out[p] = {"ms_per_img": round(ms, 3),
+                  "TFLOP/s": round(backbone_flops() / ms / 1e9, 1),
+                  "attention_share": round(att / tot, 4),
+                  "profile_ms": {r[0]: round(r[1], 3) for r in
+                                 sorted(tab, key=lambda r: -r[1])[:8]}}
+        m.free()
+    for be in bes.values():
+        be.free()
+    return out
+
+
 def cpu_baseline(steps=3):
     """The oracle's restatement of the reference's profile=cpu attention of
     the global block (gemm_cpu_t Q K^T with alpha 1/8 -> softmax_rows ->
@@ -230,6 +325,8 @@ def main():
                     help="only the global bf16 attention kernel (profiling)")
     ap.add_argument("--decoder-only", action="store_true",
                     help="only the mask-decoder cross-attention (profiling)")
+    ap.add_argument("--backbone-only", action="store_true",
+                    help="only the image encoder trunk (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the attention path "
@@ -238,6 +335,9 @@ def main():
         sys.exit(2)
 
     hip = load_hip()
+    if args.backbone_only:
+        print(json.dumps({"backbone": backbone(hip, args.steps, args.warmup)}))
+        return
     if args.decoder_only:
         be32 = hip.Backend(precision="fp32")
         print(json.dumps({"decoder_fp32": decoder(hip, be32, args.steps,
@@ -288,6 +388,7 @@ def main():
     w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), sub_warm)
 
     dec = decoder(hip, be32, sub_steps, sub_warm)
+    bb = backbone(hip, 3, 1)
 
     qkv_flops = 2.0 * 5184 * 1024 * 3072
     result = {
@@ -327,6 +428,7 @@ def main():
             "windowed_ms": round(w32_ms, 4),
             "windowed_TFLOP/s": round(win.flops() / w32_ms / 1e9, 2)},
         "decoder_fp32": dec,
+        "backbone": bb,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16, 4),

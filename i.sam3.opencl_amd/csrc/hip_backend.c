@@ -337,7 +337,20 @@ hipb_mem hipb_alloc_typed(struct hipb_backend *b, size_t count, int dtype,
                    (unsigned long)(b->max_alloc >> 20));
         return NULL;
     }
-    m = calloc(1, sizeof(*m));
+    /* The name is copied behind the descriptor: callers may pass a
+     * temporary string (bindings do). */
+    {
+        const size_t len = what ? strlen(what) : 0;
+
+        m = calloc(1, sizeof(*m) + len + 1);
+        if (!m) {
+            hipb_fatal("HIP: out of host memory for buffer <%s>", what);
+            return NULL;
+        }
+        if (what)
+            memcpy((char *)(m + 1), what, len);
+        m->what = (const char *)(m + 1);
+    }
     e = hipMalloc(&m->ptr, n);
     if (e != hipSuccess) {
         free(m);
@@ -347,7 +360,6 @@ hipb_mem hipb_alloc_typed(struct hipb_backend *b, size_t count, int dtype,
     }
     m->bytes = n;
     m->dtype = dtype;
-    m->what = what;
     return m;
 }
 

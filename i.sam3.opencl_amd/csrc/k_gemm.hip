@@ -305,6 +305,12 @@ extern "C" int launch_gemm(const gemm_desc *d, void *stream)
 
     if (d->nb > 65535 || grid.y > 65535)
         return hipErrorInvalidConfiguration;
+    {
+        const int r = launch_gemm_nt(d, stream);
+
+        if (r != -1)
+            return r;
+    }
     if (d->mode == MODE_BF16) {
         if (d->transb)
             hipLaunchKernelGGL(k_gemm_bf16<true>, grid, dim3(256), 0, s, *d,

@@ -1,0 +1,246 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * bf16 "NT" GEMM of the precision=bf16 path on gfx950:
+ *   C = act(alpha * A B^T + bias) + R      (sam3_kernels.cl:57-69)
+ * with A [M][K] bf16 activations and B [N][K] bf16 weight rows (the
+ * Linear layout, transb), float or bf16 C, R possibly aliasing C. This is
+ * the shape of every projection of the image encoder (QKV 1024 -> 3072,
+ * attention projection 1024 -> 1024, MLP 1024 -> 4096 -> 1024 over the
+ * 5184 tokens), so it gets its own kernel; other shapes and types take
+ * the general kernels of k_gemm.hip.
+ *
+ * A workgroup owns a BM x BN tile of C; each wave a 128 x 64 sub-tile as
+ * 4 x 2 blocks of 32 x 32 v_mfma_f32_32x32x16_bf16 accumulators. K moves
+ * in stages of 64: the BM + BN rows of the stage (128 bytes each) go HBM
+ * -> LDS with asynchronous global_load_lds_dwordx4 (no staging registers,
+ * no conversion) into one of two slots, 16-byte chunk c of row r stored
+ * at chunk c ^ ((r >> 1) & 7) so that the MFMA operand reads (16 bytes of
+ * one chunk from 16 different rows per 16-lane group) hit distinct
+ * banks. One barrier per stage hands a slot from the readers back to the
+ * copy of the stage after next.
+ *
+ * LDS operand bytes per MFMA: (4 + 2) fragments of 1 KiB per 8 MFMAs,
+ * 0.75 KiB, against the 1 KiB per MFMA the LDS can deliver to four SIMDs
+ * at the MFMA peak.
+ */
+#include "k_common.h"
+
+#define NT_KS 64 /* K per stage */
+#define NT_WM 128
+#define NT_WN 64
+
+/* XCDs (L2 domains) of an MI355X. */
+#define NT_NXCD 8
+
+__device__ __forceinline__ int nt_swz(int row, int chunk)
+{
+    return 8 * (chunk ^ ((row >> 1) & 7));
+}
+
+/* Asynchronous 16-byte global -> LDS copy: lane i of the wave writes
+ * lds_base + 16 i (lds_base wave-uniform, via M0). Inline assembly so the
+ * compiler does not wait for it before unrelated LDS reads; the kernel
+ * waits itself (s_waitcnt vmcnt(0)) before the barrier that publishes the
+ * slot. */
+__device__ __forceinline__ void nt_g2lds16(const void *g, void *lds_base)
+{
+    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_base);
+
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "global_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(g)
+                 : "memory", "m0");
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__((BM / NT_WM) * (BN / NT_WN) * 64, 1) void
+k_gemm_nt(gemm_desc d)
+{
+    constexpr int NW = (BM / NT_WM) * (BN / NT_WN);
+    constexpr int ROWS = BM + BN;           /* LDS rows per stage */
+    constexpr int LPW = ROWS / (8 * NW);    /* copies per wave per stage */
+    __shared__ __attribute__((aligned(16))) uint16_t S[2][ROWS][NT_KS];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
+              l32 = l & 31;
+    const int wm = w / (BN / NT_WN), wn = w % (BN / NT_WN);
+    const int tiles_n = (d.N + BN - 1) / BN;
+    const long total = (long)tiles_n * ((d.M + BM - 1) / BM);
+    const long per_xcd = (total + NT_NXCD - 1) / NT_NXCD;
+    /* Workgroup g runs on XCD g % 8: give each XCD a contiguous run of
+     * tiles (row-major over the tile grid), so its L2 sees the same A rows
+     * and a window of B rows. */
+    const long tile = (blockIdx.x % NT_NXCD) * per_xcd + blockIdx.x / NT_NXCD;
+    if (tile >= total)
+        return;
+    const int m0 = (int)(tile / tiles_n) * BM, n0 = (int)(tile % tiles_n) * BN;
+    const uint16_t *A = (const uint16_t *)d.A + d.aoff;
+    const uint16_t *B = (const uint16_t *)d.B + d.boff;
+    const int nk = d.K / NT_KS;
+    f32x16 acc[4][2];
+    long goff[LPW];
+
+    for (int i = 0; i < 4; i++)
+        for (int j = 0; j < 2; j++)
+            for (int r = 0; r < 16; r++)
+                acc[i][j][r] = 0.0f;
+
+    /* Copy j of wave w fills stage rows 8 (w LPW + j) .. +7; lane i lands
+     * on row + i / 8, physical chunk i % 8 and so fetches logical chunk
+     * (i % 8) ^ ((row >> 1) & 7). Rows past M or N read the last row
+     * (their products are never stored). */
+    for (int j = 0; j < LPW; j++) {
+        const int row = 8 * (w * LPW + j) + (l >> 3);
+        const int chunk = (l & 7) ^ ((row >> 1) & 7);
+
+        if (row < BM) {
+            const int gm = min(m0 + row, d.M - 1);
+
+            goff[j] = (long)gm * d.lda + 8 * chunk;
+        }
+        else {
+            const int gn = min(n0 + row - BM, d.N - 1);
+
+            goff[j] = (long)gn * d.ldb + 8 * chunk;
+        }
+    }
+    auto load_stage = [&](int ks, int slot) {
+        for (int j = 0; j < LPW; j++) {
+            const int row0 = 8 * (w * LPW + j);
+            const uint16_t *base = row0 < BM ? A : B;
+
+            nt_g2lds16(base + goff[j] + (long)ks * NT_KS, &S[slot][row0][0]);
+        }
+    };
+
+    load_stage(0, 0);
+    for (int ks = 0; ks < nk; ks++) {
+        const int slot = ks & 1;
+
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (ks + 1 < nk)
+            load_stage(ks + 1, slot ^ 1);
+#pragma unroll
+        for (int s = 0; s < NT_KS / 16; s++) {
+            bf16x8 a[4], b[2];
+
+            for (int i = 0; i < 4; i++) {
+                const int row = wm * NT_WM + 32 * i + l32;
+
+                a[i] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
+            }
+            for (int j = 0; j < 2; j++) {
+                const int row = BM + wn * NT_WN + 32 * j + l32;
+
+                b[j] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
+            }
+            for (int i = 0; i < 4; i++)
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    /* Epilogue (store_one, sam3_kernels.cl:306-319): lane l holds column
+     * n0 + wn 64 + 32 j + l % 32 of rows 8 (r / 4) + 4 h + r % 4 of each
+     * 32 x 32 block, so each row segment is one 128-byte store. */
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn * NT_WN + 32 * j + l32;
+
+        if (n >= d.N)
+            continue;
+        const float bn = d.bias ? d.bias[n] : 0.0f;
+
+        for (int i = 0; i < 4; i++)
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm * NT_WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+
+                if (m >= d.M)
+                    continue;
+                const long idx = d.coff + (long)m * d.ldc + n;
+                float v = act_k(d.alpha * acc[i][j][r] + bn, d.act);
+
+                if (d.cdt == DT_F32) {
+                    if (d.R)
+                        v += ((const float *)d.R)[idx - d.coff + d.roff];
+                    ((float *)d.C)[idx] = v;
+                }
+                else {
+                    if (d.R)
+                        v += bf2f(((const uint16_t *)d.R)[idx - d.coff + d.roff]);
+                    ((uint16_t *)d.C)[idx] = f2bf(v);
+                }
+            }
+    }
+}
+
+static int cu_count(void)
+{
+    static int n;
+
+    if (!n) {
+        int dev = 0;
+
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                                  dev) != hipSuccess || n < 1)
+            n = 256;
+    }
+    return n;
+}
+
+/* The NT kernel applies to unbatched bf16 x bf16 (weights as [N][K])
+ * products with K a multiple of 64 and 16-byte aligned rows. */
+extern "C" int gemm_nt_ok(const gemm_desc *d)
+{
+    return d->mode == MODE_BF16 && d->adt == DT_BF16 && d->bdt == DT_BF16 &&
+           d->transb && d->nb == 1 && d->K >= NT_KS && d->K % NT_KS == 0 &&
+           d->lda % 8 == 0 && d->ldb % 8 == 0 && d->aoff % 8 == 0 &&
+           d->boff % 8 == 0 && d->M >= 1 && d->N >= 1;
+}
+
+/* Returns -1 when the NT kernel does not apply, else a hipError_t. */
+extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
+{
+    hipStream_t s = (hipStream_t)stream;
+    long t256, t128;
+    int bm, bn;
+
+    if (!gemm_nt_ok(d))
+        return -1;
+    /* The largest tile that still gives every CU a workgroup; smaller
+     * tiles for narrow outputs. */
+    t256 = (long)((d->M + 255) / 256) * ((d->N + 255) / 256);
+    t128 = (long)((d->M + 255) / 256) * ((d->N + 127) / 128);
+    if (t256 >= cu_count() * 9 / 10) {
+        bm = 256;
+        bn = 256;
+    }
+    else if (t128 >= cu_count() * 9 / 10) {
+        bm = 256;
+        bn = 128;
+    }
+    else {
+        bm = 128;
+        bn = 128;
+    }
+    {
+        const long tiles = (long)((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn);
+        const long grid = (tiles + NT_NXCD - 1) / NT_NXCD * NT_NXCD;
+        const int threads = (bm / NT_WM) * (bn / NT_WN) * 64;
+
+        if (grid > 0x7fffffffL)
+            return hipErrorInvalidConfiguration;
+        if (bm == 256 && bn == 256)
+            hipLaunchKernelGGL((k_gemm_nt<256, 256>), dim3((unsigned)grid),
+                               dim3(threads), 0, s, *d);
+        else if (bm == 256)
+            hipLaunchKernelGGL((k_gemm_nt<256, 128>), dim3((unsigned)grid),
+                               dim3(threads), 0, s, *d);
+        else
+            hipLaunchKernelGGL((k_gemm_nt<128, 128>), dim3((unsigned)grid),
+                               dim3(threads), 0, s, *d);
+    }
+    return hipGetLastError();
+}

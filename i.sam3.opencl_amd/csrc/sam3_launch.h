@@ -51,6 +51,10 @@ struct gemm_desc {
     int mode;
 };
 int launch_gemm(const struct gemm_desc *d, void *stream);
+/* The bf16 x bf16 "NT" kernel (A [M][K], B [N][K], K % 64 == 0,
+ * unbatched); -1 if d does not have that form, else a hipError_t. */
+int launch_gemm_nt(const struct gemm_desc *d, void *stream);
+int gemm_nt_ok(const struct gemm_desc *d);
 
 /* Row LayerNorm of rows x C floats into Y (float or bf16). With ws > 0
  * the output rows are the window-partitioned order of an H x H grid

@@ -168,7 +168,9 @@ void gemm(struct sam_model *m, int M, int N, int K, struct opnd A,
     d.mode = (b->bf16 || d.adt == HIPB_BF16 || d.bdt == HIPB_BF16)
                  ? MODE_BF16
                  : MODE_F32;
-    what = d.mode == MODE_BF16 ? "gemm_bf16" : "gemm_f32";
+    what = gemm_nt_ok(&d)           ? "gemm_nt_bf16"
+           : d.mode == MODE_BF16 ? "gemm_bf16"
+                                 : "gemm_f32";
     hipb_run_begin(b);
     err = launch_gemm(&d, b->stream);
     hipb_run_end(b, err, what, 2.0 * M * N * K * (double)nb);
@@ -555,8 +557,10 @@ static int head_chunk(const struct sam_model *m, const struct geom *g)
     return hc > m->heads ? m->heads : (int)hc;
 }
 
-void vit_attention(struct sam_model *m, const struct vit_block *blk,
-                   int unfused)
+/* The attention region of vit_attention with its output operand O
+ * (rows of the block's window order, head h at column h * hd). */
+static void attention_region(struct sam_model *m, const struct vit_block *blk,
+                             int unfused, hipb_mem obuf)
 {
     struct hipb_backend *b = m->hip;
     const struct geom g = block_geom(m, blk);
@@ -603,7 +607,7 @@ void vit_attention(struct sam_model *m, const struct vit_block *blk,
                    bmat(m->qkv, 0, 3 * E, (long)g.N * 3 * E, hd),
                    bmat(m->qkv, E, 3 * E, (long)g.N * 3 * E, hd),
                    bmat(m->qkv, 2L * E, 3 * E, (long)g.N * 3 * E, hd),
-                   bmat(m->attn, 0, E, (long)g.N * E, hd), table, g.N, scale);
+                   bmat(obuf, 0, E, (long)g.N * E, hd), table, g.N, scale);
         return;
     }
 
@@ -622,7 +626,7 @@ void vit_attention(struct sam_model *m, const struct vit_block *blk,
                    bmat(m->qkv, 0, 3 * E, (long)g.N * 3 * E, hd),
                    bmat(m->qkv, E, 3 * E, (long)g.N * 3 * E, hd),
                    bmat(m->qkv, 2L * E, 3 * E, (long)g.N * 3 * E, hd),
-                   bmat(m->attn, 0, E, (long)g.N * E, hd), table, g.N, scale);
+                   bmat(obuf, 0, E, (long)g.N * E, hd), table, g.N, scale);
         return;
     }
 
@@ -660,10 +664,16 @@ void vit_attention(struct sam_model *m, const struct vit_block *blk,
             softmax_rows(m, m->scores, (long)g.nwin * hcc * g.N, g.N);
             gemm(m, g.N, hd, g.N, bmat(m->scores, 0, g.N, hcc * plane, plane),
                  bmat(m->qkv, 2L * E + (long)h0 * hd, 3 * E, tstride, hd), 0,
-                 bmat(m->attn, (long)h0 * hd, E, (long)g.N * E, hd),
+                 bmat(obuf, (long)h0 * hd, E, (long)g.N * E, hd),
                  g.nwin * hcc, hcc, NULL, NULL, 0, 1.0f, ACT_NONE);
         }
     }
+}
+
+void vit_attention(struct sam_model *m, const struct vit_block *blk,
+                   int unfused)
+{
+    attention_region(m, blk, unfused, m->attn);
 }
 
 /* ------------------------------------------------------------ trunk */
@@ -674,24 +684,35 @@ void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused)
     const struct geom g = block_geom(m, blk);
     const int T = m->grid * m->grid, E = m->embed, mlp = m->mlp;
     const long rows = (long)g.nwin * g.N;
+    hipb_mem A = m->attn;
 
     if (mlp < 1 || !m->tmp || !m->mlpbuf) {
         hipb_fatal("vit_block: no MLP work buffers (sam_path_init with "
                    "mlp > 0)");
         return;
     }
-    vit_attention(m, blk, unfused);
+    /* With precision=bf16 the attention output goes to the MLP hidden
+     * buffer as bf16 (free until norm2): the A operand of the bf16
+     * projection. */
+    if (b->bf16 && !unfused) {
+        if (!ensure_bf16(b, &m->mlp16, (size_t)(rows > T ? rows : T) *
+                                           (mlp > E ? mlp : E),
+                         "mlp (bf16)"))
+            return;
+        A = m->mlp16;
+    }
+    attention_region(m, blk, unfused, A);
     if (hipb_failed())
         return;
     /* Projection with residual (sam3_model.c:1015-1022). */
     if (blk->window) {
-        linear(m, (int)rows, E, E, m->attn, 0, blk->projw, blk->projb, m->tmp,
-               0, ACT_NONE, 0);
+        linear(m, (int)rows, E, E, A, 0, blk->projw, blk->projb, m->tmp, 0,
+               ACT_NONE, 0);
         window_unpartition_add(m, m->x, m->tmp, m->grid, E, g.s, g.nwx);
     }
     else
-        linear(m, T, E, E, m->attn, 0, blk->projw, blk->projb, m->x, 0,
-               ACT_NONE, 1);
+        linear(m, T, E, E, A, 0, blk->projw, blk->projb, m->x, 0, ACT_NONE,
+               1);
     if (hipb_failed())
         return;
     /* norm2 and the MLP (sam3_model.c:1024-1027); with precision=bf16 the

@@ -64,7 +64,7 @@ struct hipb_buf {
     void *ptr;        /* device address */
     size_t bytes;     /* allocation size */
     int dtype;        /* HIPB_F32, HIPB_F16 or HIPB_BF16 */
-    const char *what; /* name given at allocation, for messages */
+    const char *what; /* copy of the name given at allocation */
 };
 
 struct hipb_backend {

@@ -158,6 +158,58 @@ def test_gemm_bf16(hip, be16, orc, transb):
     assert report("gemm bf16 transb=%d" % transb, got, want) <= BF16_TOL
 
 
+def to_bf16(x):
+    """float32 -> bf16 bits, round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u + ((u >> 16) & 1) + 0x7FFF) >> 16).astype(np.uint16)
+
+
+def from_bf16(u):
+    return (np.asarray(u, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K,act,res,cbf", [
+    (5184, 3072, 1024, 0, False, False),   # QKV projection
+    (5184, 1024, 1024, 0, True, False),    # attention projection + residual
+    (5184, 4096, 1024, 1, False, True),    # MLP fc1, GELU, bf16 hidden
+    (5184, 1024, 4096, 0, True, False),    # MLP fc2 + residual
+    (300, 200, 128, 1, True, False),       # ragged tiles on both sides
+    (257, 129, 192, 2, True, True),
+    (1, 1, 64, 0, False, False),
+])
+def test_gemm_nt_bf16(hip, be16, orc, M, N, K, act, res, cbf):
+    """bf16 activations x bf16 weight rows (the NT kernel): the oracle's
+    linear on the same bf16 values in float, sampled rows at full size."""
+    m = model(hip, be16)
+    g = rng(M + N + K)
+    A = to_bf16(g.standard_normal((M, K), dtype=np.float32))
+    W = to_bf16(g.uniform(-0.06, 0.06, (N, K)).astype(np.float32))
+    bias = g.standard_normal(N, dtype=np.float32)
+    C0 = g.standard_normal((M, N), dtype=np.float32)
+    if cbf:
+        C0 = from_bf16(to_bf16(C0))
+    dA, dW = be16.upload_typed(A, hip.BF16), be16.upload_typed(W, hip.BF16)
+    db = be16.upload(bias)
+    dC = be16.upload_typed(to_bf16(C0), hip.BF16) if cbf else be16.upload(C0)
+    hip.prof_reset()
+    be16._b.profile = 1
+    hip.linear(m, M, K, N, dA, 0, dW, db, dC, 0, act, int(res))
+    be16._b.profile = 0
+    assert "gemm_nt_bf16" in [r[0] for r in hip.prof_table()]
+    got = be16.read(dC)
+    got = (from_bf16(got) if cbf else got).reshape(M, N)
+    rows = np.sort(rng(1).choice(M, min(M, 96), replace=False))
+    want = orc.linear(from_bf16(A[rows]), from_bf16(W), bias, act=act,
+                      cpu=False)
+    if res:
+        want = want + C0[rows]
+    if cbf:
+        want = from_bf16(to_bf16(want))
+    tol = 1e-2 if cbf else 1e-5
+    assert report("gemm_nt bf16 %dx%dx%d act=%d res=%d cbf=%d" %
+                  (M, N, K, act, res, cbf), got[rows], want) <= tol
+
+
 def test_linear_fp16_weights(hip, orc):
     be = hip.Backend(precision="fp16")
     try:

@@ -23,10 +23,12 @@ HIP_FLAGS = [
     # Packed fp32 VALU instructions are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
-    # MFMA accumulators in VGPRs: no AGPR <-> VGPR copies around the
-    # VALU work on scores and outputs.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+# MFMA accumulators in VGPRs: no AGPR <-> VGPR copies around the VALU work
+# on scores and outputs. Not for the NT GEMM, whose 128 x 128 wave tiles
+# keep 256 accumulators per lane in the AGPRs.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+AGPR_FILES = {"k_gemm_nt.hip"}
 C_FLAGS = ["-O2", "-fPIC", "-std=gnu11", "-Wall", "-Wextra",
            "-Wno-unused-parameter", "-D__HIP_PLATFORM_AMD__"]
 
@@ -50,7 +52,8 @@ def build(verbose=False):
         src = os.path.join(CSRC, f)
         obj = os.path.join(OBJ, os.path.splitext(f)[0] + ".o")
         if f.endswith(".hip"):
-            jobs.append([os.path.join(ROCM, "bin", "hipcc")] + HIP_FLAGS + inc +
+            flags = HIP_FLAGS + ([] if f in AGPR_FILES else VGPR_FORM)
+            jobs.append([os.path.join(ROCM, "bin", "hipcc")] + flags + inc +
                         ["-c", src, "-o", obj])
         elif f.endswith(".c"):
             jobs.append(["gcc"] + C_FLAGS + inc + ["-c", src, "-o", obj])

@@ -9,8 +9,9 @@
  * 5184 tokens), so it gets its own kernel; other shapes and types take
  * the general kernels of k_gemm.hip.
  *
- * A workgroup owns a BM x BN tile of C; each wave a 128 x 64 sub-tile as
- * 4 x 2 blocks of 32 x 32 v_mfma_f32_32x32x16_bf16 accumulators. K moves
+ * A workgroup owns a BM x BN tile of C; each wave a WM x WN sub-tile as
+ * (WM / 32) x (WN / 32) blocks of 32 x 32 v_mfma_f32_32x32x16_bf16
+ * accumulators (the AGPRs hold them when they exceed the VGPRs). K moves
  * in stages of 64: the BM + BN rows of the stage (128 bytes each) go HBM
  * -> LDS with asynchronous global_load_lds_dwordx4 (no staging registers,
  * no conversion) into one of two slots, 16-byte chunk c of row r stored
@@ -19,15 +20,13 @@
  * banks. One barrier per stage hands a slot from the readers back to the
  * copy of the stage after next.
  *
- * LDS operand bytes per MFMA: (4 + 2) fragments of 1 KiB per 8 MFMAs,
- * 0.75 KiB, against the 1 KiB per MFMA the LDS can deliver to four SIMDs
- * at the MFMA peak.
+ * LDS operand bytes per MFMA: (WM + WN) / 32 fragments of 1 KiB per
+ * WM WN / 1024 MFMAs: 0.75 KiB for 128 x 64, 1 KiB for 64 x 64, against
+ * the 1 KiB per MFMA the LDS can deliver to four SIMDs at the MFMA peak.
  */
 #include "k_common.h"
 
 #define NT_KS 64 /* K per stage */
-#define NT_WM 128
-#define NT_WN 64
 
 /* XCDs (L2 domains) of an MI355X. */
 #define NT_NXCD 8
@@ -53,17 +52,19 @@ __device__ __forceinline__ void nt_g2lds16(const void *g, void *lds_base)
                  : "memory", "m0");
 }
 
-template <int BM, int BN>
-__global__ __launch_bounds__((BM / NT_WM) * (BN / NT_WN) * 64, 1) void
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt(gemm_desc d)
 {
-    constexpr int NW = (BM / NT_WM) * (BN / NT_WN);
+    constexpr int NW = (BM / WM) * (BN / WN);
+    constexpr int NA = WM / 32;             /* 32-row blocks per wave */
+    constexpr int NB = WN / 32;             /* 32-column blocks per wave */
     constexpr int ROWS = BM + BN;           /* LDS rows per stage */
     constexpr int LPW = ROWS / (8 * NW);    /* copies per wave per stage */
     __shared__ __attribute__((aligned(16))) uint16_t S[2][ROWS][NT_KS];
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
-    const int wm = w / (BN / NT_WN), wn = w % (BN / NT_WN);
+    const int wm = w / (BN / WN), wn = w % (BN / WN);
     const int tiles_n = (d.N + BN - 1) / BN;
     const long total = (long)tiles_n * ((d.M + BM - 1) / BM);
     const long per_xcd = (total + NT_NXCD - 1) / NT_NXCD;
@@ -77,13 +78,14 @@ k_gemm_nt(gemm_desc d)
     const uint16_t *A = (const uint16_t *)d.A + d.aoff;
     const uint16_t *B = (const uint16_t *)d.B + d.boff;
     const int nk = d.K / NT_KS;
-    f32x16 acc[4][2];
+    f32x16 acc[NA][NB];
     long goff[LPW];
 
-    for (int i = 0; i < 4; i++)
-        for (int j = 0; j < 2; j++)
-            for (int r = 0; r < 16; r++)
-                acc[i][j][r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NA; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            acc[i][j] = (f32x16){};
 
     /* Copy j of wave w fills stage rows 8 (w LPW + j) .. +7; lane i lands
      * on row + i / 8, physical chunk i % 8 and so fetches logical chunk
@@ -123,55 +125,61 @@ k_gemm_nt(gemm_desc d)
             load_stage(ks + 1, slot ^ 1);
 #pragma unroll
         for (int s = 0; s < NT_KS / 16; s++) {
-            bf16x8 a[4], b[2];
+            bf16x8 a[NA], b[NB];
 
-            for (int i = 0; i < 4; i++) {
-                const int row = wm * NT_WM + 32 * i + l32;
+#pragma unroll
+            for (int i = 0; i < NA; i++) {
+                const int row = wm * WM + 32 * i + l32;
 
                 a[i] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
             }
-            for (int j = 0; j < 2; j++) {
-                const int row = BM + wn * NT_WN + 32 * j + l32;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int row = BM + wn * WN + 32 * j + l32;
 
                 b[j] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
             }
-            for (int i = 0; i < 4; i++)
-                for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < NA; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         a[i], b[j], acc[i][j], 0, 0, 0);
         }
     }
 
     /* Epilogue (store_one, sam3_kernels.cl:306-319): lane l holds column
-     * n0 + wn 64 + 32 j + l % 32 of rows 8 (r / 4) + 4 h + r % 4 of each
+     * n0 + wn WN + 32 j + l % 32 of rows 8 (r / 4) + 4 h + r % 4 of each
      * 32 x 32 block, so each row segment is one 128-byte store. */
-    for (int j = 0; j < 2; j++) {
-        const int n = n0 + wn * NT_WN + 32 * j + l32;
+#pragma clang loop unroll(full)
+    for (int j = 0; j < NB; j++) {
+        const int n = n0 + wn * WN + 32 * j + l32;
+        const float bn = d.bias && n < d.N ? d.bias[n] : 0.0f;
 
-        if (n >= d.N)
-            continue;
-        const float bn = d.bias ? d.bias[n] : 0.0f;
+#pragma clang loop unroll(full)
+        for (int i = 0; i < NA; i++) {
+            const f32x16 cv = acc[i][j];
 
-        for (int i = 0; i < 4; i++)
+#pragma clang loop unroll(full)
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * NT_WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-
-                if (m >= d.M)
-                    continue;
+                const int m = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
                 const long idx = d.coff + (long)m * d.ldc + n;
-                float v = act_k(d.alpha * acc[i][j][r] + bn, d.act);
+                float v = act_k(d.alpha * cv[r] + bn, d.act);
 
-                if (d.cdt == DT_F32) {
-                    if (d.R)
-                        v += ((const float *)d.R)[idx - d.coff + d.roff];
-                    ((float *)d.C)[idx] = v;
-                }
-                else {
-                    if (d.R)
-                        v += bf2f(((const uint16_t *)d.R)[idx - d.coff + d.roff]);
-                    ((uint16_t *)d.C)[idx] = f2bf(v);
+                if (m < d.M && n < d.N) {
+                    if (d.cdt == DT_F32) {
+                        if (d.R)
+                            v += ((const float *)d.R)[idx - d.coff + d.roff];
+                        ((float *)d.C)[idx] = v;
+                    }
+                    else {
+                        if (d.R)
+                            v += bf2f(((const uint16_t *)d.R)[idx - d.coff + d.roff]);
+                        ((uint16_t *)d.C)[idx] = f2bf(v);
+                    }
                 }
             }
+        }
     }
 }
 
@@ -204,43 +212,33 @@ extern "C" int gemm_nt_ok(const gemm_desc *d)
 extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
 {
     hipStream_t s = (hipStream_t)stream;
-    long t256, t128;
+    long t256;
     int bm, bn;
 
     if (!gemm_nt_ok(d))
         return -1;
-    /* The largest tile that still gives every CU a workgroup; smaller
-     * tiles for narrow outputs. */
+    /* 128 x 128 tiles (4 waves of 64 x 64, two workgroups per CU, so one
+     * workgroup's pipeline fill and output drain overlap the other's
+     * products); 256 x 256 tiles (8 waves of 128 x 64, half the operand
+     * traffic per product) only for long reductions that still give
+     * (nearly) every CU a tile. Measured at M = 5184: K = 1024 runs at
+     * 646 vs 691 TFLOP/s (N = 3072) and 460 vs 585 (N = 4096), K = 4096
+     * at 1145 vs 1070 (N = 3072). */
     t256 = (long)((d->M + 255) / 256) * ((d->N + 255) / 256);
-    t128 = (long)((d->M + 255) / 256) * ((d->N + 127) / 128);
-    if (t256 >= cu_count() * 9 / 10) {
-        bm = 256;
-        bn = 256;
-    }
-    else if (t128 >= cu_count() * 9 / 10) {
-        bm = 256;
-        bn = 128;
-    }
-    else {
-        bm = 128;
-        bn = 128;
-    }
+    bm = t256 >= cu_count() * 9 / 10 && d->K >= 2048 ? 256 : 128;
+    bn = bm;
     {
         const long tiles = (long)((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn);
         const long grid = (tiles + NT_NXCD - 1) / NT_NXCD * NT_NXCD;
-        const int threads = (bm / NT_WM) * (bn / NT_WN) * 64;
 
         if (grid > 0x7fffffffL)
             return hipErrorInvalidConfiguration;
-        if (bm == 256 && bn == 256)
-            hipLaunchKernelGGL((k_gemm_nt<256, 256>), dim3((unsigned)grid),
-                               dim3(threads), 0, s, *d);
-        else if (bm == 256)
-            hipLaunchKernelGGL((k_gemm_nt<256, 128>), dim3((unsigned)grid),
-                               dim3(threads), 0, s, *d);
+        if (bm == 256)
+            hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64>),
+                               dim3((unsigned)grid), dim3(512), 0, s, *d);
         else
-            hipLaunchKernelGGL((k_gemm_nt<128, 128>), dim3((unsigned)grid),
-                               dim3(threads), 0, s, *d);
+            hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64>),
+                               dim3((unsigned)grid), dim3(256), 0, s, *d);
     }
     return hipGetLastError();
 }

@@ -86,15 +86,106 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
 }
 
+/* Rows of C = 256 V floats (V <= 16): one wave per output row, four
+ * rows per workgroup. Lane l holds floats 4 l + 256 i .. +3 (i < V) in
+ * registers from one 16-byte load each; the mean and variance close with
+ * wave butterflies (no LDS, no barrier); outputs leave as 16-byte (float)
+ * or 8-byte (bf16) stores. Window partition as in k_layernorm. */
+template <typename TY, int V>
+__global__ __launch_bounds__(256) void k_layernorm_w(
+    const float *__restrict__ X, TY *__restrict__ Y, const float *__restrict__ g,
+    const float *__restrict__ bt, long rows, float eps, int act, int H,
+    int ws, int nwx)
+{
+    constexpr int C = 256 * V;
+    const int l = threadIdx.x & 63;
+    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    long src = r;
+    f32x4 v[V];
+    float s = 0.0f, mean, var, rs;
+
+    if (r >= rows)
+        return;
+    TY *yr = Y + r * C + 4 * l;
+    if (ws > 0) {
+        const int w = (int)(r / ((long)ws * ws)), p = (int)(r % ((long)ws * ws));
+        const int y = (w / nwx) * ws + p / ws, x = (w % nwx) * ws + p % ws;
+
+        if (y >= H || x >= H) {
+            for (int i = 0; i < V; i++)
+                for (int e = 0; e < 4; e++)
+                    yr[256 * i + e] = (TY)0.0f;
+            return;
+        }
+        src = (long)y * H + x;
+    }
+    const float *xr = X + src * C + 4 * l;
+    for (int i = 0; i < V; i++) {
+        v[i] = *(const f32x4 *)(xr + 256 * i);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    mean = wave_sum(s) / (float)C;
+    s = 0.0f;
+    for (int i = 0; i < V; i++) {
+        const f32x4 dv = v[i] - mean;
+
+        s = fmaf(dv.x, dv.x, fmaf(dv.y, dv.y, fmaf(dv.z, dv.z, fmaf(dv.w, dv.w, s))));
+    }
+    var = wave_sum(s) / (float)C;
+    rs = 1.0f / sqrtf(var + eps);
+    for (int i = 0; i < V; i++) {
+        const int c = 4 * l + 256 * i;
+        const f32x4 gv = *(const f32x4 *)(g + c), bv = *(const f32x4 *)(bt + c);
+        f32x4 o;
+
+        o.x = act_k(fmaf((v[i].x - mean) * rs, gv.x, bv.x), act);
+        o.y = act_k(fmaf((v[i].y - mean) * rs, gv.y, bv.y), act);
+        o.z = act_k(fmaf((v[i].z - mean) * rs, gv.z, bv.z), act);
+        o.w = act_k(fmaf((v[i].w - mean) * rs, gv.w, bv.w), act);
+        if constexpr (sizeof(TY) == 4)
+            *(f32x4 *)(yr + 256 * i) = o;
+        else {
+            uint2 pk;
+
+            pk.x = pack_bf16x2(o.x, o.y);
+            pk.y = pack_bf16x2(o.z, o.w);
+            *(uint2 *)(yr + 256 * i) = pk;
+        }
+    }
+}
+
 extern "C" int launch_layernorm(const float *X, void *Y, int ydt,
                                 const float *g, const float *b, long rows,
                                 int C, float eps, int act, int H, int ws,
                                 int nwx, void *stream)
 {
     const long out_rows = ws > 0 ? (long)nwx * nwx * ws * ws : rows;
+    hipStream_t st = (hipStream_t)stream;
 
     if (out_rows == 0)
         return hipSuccess;
+    /* 16-byte rows of the wave-per-row kernel: C a multiple of 256 up to
+     * 4096 (the buffers are hipMalloc'd, so rows start 16-byte aligned). */
+    if (C % 256 == 0 && C <= 4096) {
+        const dim3 grid((unsigned)((out_rows + 3) / 4));
+
+#define LNW(V)                                                                \
+    case V:                                                                   \
+        if (ydt == DT_BF16)                                                   \
+            hipLaunchKernelGGL((k_layernorm_w<__bf16, V>), grid, dim3(256), 0, \
+                               st, X, (__bf16 *)Y, g, b, out_rows, eps, act,  \
+                               H, ws, nwx);                                   \
+        else                                                                  \
+            hipLaunchKernelGGL((k_layernorm_w<float, V>), grid, dim3(256), 0,  \
+                               st, X, (float *)Y, g, b, out_rows, eps, act,   \
+                               H, ws, nwx);                                   \
+        return hipGetLastError();
+        switch (C / 256) {
+            LNW(1) LNW(2) LNW(3) LNW(4) LNW(5) LNW(6) LNW(7) LNW(8) LNW(9)
+            LNW(10) LNW(11) LNW(12) LNW(13) LNW(14) LNW(15) LNW(16)
+        }
+#undef LNW
+    }
     if (ydt == DT_BF16)
         hipLaunchKernelGGL(k_layernorm<__bf16>, dim3(out_rows), dim3(256), 0,
                            (hipStream_t)stream, X, (__bf16 *)Y, g, b, C, eps,

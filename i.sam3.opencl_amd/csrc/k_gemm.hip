@@ -311,6 +311,8 @@ extern "C" int launch_gemm(const gemm_desc *d, void *stream)
         if (r != -1)
             return r;
     }
+    if (d->unpart_ws > 0)
+        return hipErrorInvalidValue; /* row remap: NT kernel only */
     if (d->mode == MODE_BF16) {
         if (d->transb)
             hipLaunchKernelGGL(k_gemm_bf16<true>, grid, dim3(256), 0, s, *d,

@@ -56,12 +56,21 @@ template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt(gemm_desc d)
 {
+    /* Epilogue rows staged per pass, and the LDS that needs. */
+    constexpr int EPI_ROWS = BM <= 128 ? BM : 64;
+    constexpr int EPI_BYTES = EPI_ROWS * (BN + 4) * 4;
     constexpr int NW = (BM / WM) * (BN / WN);
     constexpr int NA = WM / 32;             /* 32-row blocks per wave */
     constexpr int NB = WN / 32;             /* 32-column blocks per wave */
     constexpr int ROWS = BM + BN;           /* LDS rows per stage */
     constexpr int LPW = ROWS / (8 * NW);    /* copies per wave per stage */
-    __shared__ __attribute__((aligned(16))) uint16_t S[2][ROWS][NT_KS];
+    constexpr int LDS_BYTES = 2 * ROWS * NT_KS * 2 > EPI_BYTES
+                                  ? 2 * ROWS * NT_KS * 2
+                                  : EPI_BYTES;
+    /* Two operand slots during the K loop, the output tile in the
+     * epilogue (which may need a little more). */
+    __shared__ __attribute__((aligned(16))) uint16_t S_raw[LDS_BYTES / 2];
+    uint16_t(*S)[ROWS][NT_KS] = (uint16_t(*)[ROWS][NT_KS])S_raw;
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
     const int wm = w / (BN / WN), wn = w % (BN / WN);
@@ -148,38 +157,104 @@ k_gemm_nt(gemm_desc d)
         }
     }
 
-    /* Epilogue (store_one, sam3_kernels.cl:306-319): lane l holds column
-     * n0 + wn WN + 32 j + l % 32 of rows 8 (r / 4) + 4 h + r % 4 of each
-     * 32 x 32 block, so each row segment is one 128-byte store. */
-#pragma clang loop unroll(full)
-    for (int j = 0; j < NB; j++) {
-        const int n = n0 + wn * WN + 32 * j + l32;
-        const float bn = d.bias && n < d.N ? d.bias[n] : 0.0f;
+    /* Epilogue (store_one, sam3_kernels.cl:306-319), through LDS: in
+     * chunks of 64 rows, the waves owning the rows write alpha acc + bias
+     * (activation applied) into the freed operand slots as a row-major
+     * float tile (row stride BN + 4: the two 32-lane halves of a write
+     * fall on different banks), then every thread takes four consecutive
+     * columns of a row: one 16-byte LDS read, the residual and the store
+     * as 16-byte (float) or 8-byte (bf16) accesses. With the window row
+     * remap each row's grid token costs three divisions. */
+    constexpr int CR = EPI_ROWS, LD = BN + 4, T = NW * 64, RPI = T * 4 / BN;
+    float *E = (float *)S_raw;
+    const bool vec = d.ldc % 4 == 0 && d.coff % 4 == 0 && d.roff % 4 == 0;
 
+    __syncthreads();
+#pragma clang loop unroll(full)
+    for (int c = 0; c < BM / CR; c++) {
 #pragma clang loop unroll(full)
         for (int i = 0; i < NA; i++) {
-            const f32x16 cv = acc[i][j];
+            const int rb = wm * WM + 32 * i - c * CR; /* block row in chunk */
+
+            if (rb < 0 || rb >= CR)
+                continue;
+#pragma clang loop unroll(full)
+            for (int j = 0; j < NB; j++) {
+                const int col = wn * WN + 32 * j + l32, n = n0 + col;
+                const float bn = d.bias && n < d.N ? d.bias[n] : 0.0f;
+                const f32x16 cv = acc[i][j];
 
 #pragma clang loop unroll(full)
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm * WM + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-                const long idx = d.coff + (long)m * d.ldc + n;
-                float v = act_k(d.alpha * cv[r] + bn, d.act);
+                for (int r = 0; r < 16; r++)
+                    E[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * LD + col] =
+                        act_k(d.alpha * cv[r] + bn, d.act);
+            }
+        }
+        __syncthreads();
+        for (int it = 0; it < CR / RPI; it++) {
+            const int row = it * RPI + t / (BN / 4), col = (t % (BN / 4)) * 4;
+            const int m = m0 + c * CR + row, n = n0 + col;
+            long crow = m;
+            bool keep = m < d.M && n < d.N;
 
-                if (m < d.M && n < d.N) {
+            if (d.unpart_ws > 0) {
+                const int ws = d.unpart_ws, wsz = ws * ws;
+                const int w = m / wsz, p = m - w * wsz;
+                const int py = p / ws, wy = w / d.unpart_nwx;
+                const int y = wy * ws + py;
+                const int x = (w - wy * d.unpart_nwx) * ws + (p - py * ws);
+
+                keep = keep && y < d.unpart_H && x < d.unpart_H;
+                crow = (long)y * d.unpart_H + x;
+            }
+            if (!keep)
+                continue;
+            const f32x4 v4 = *(const f32x4 *)&E[row * LD + col];
+            const long idx = d.coff + crow * d.ldc + n;
+            const long ridx = d.roff + crow * d.ldc + n;
+
+            if (vec && n + 3 < d.N) {
+                if (d.cdt == DT_F32) {
+                    f32x4 o = v4;
+
+                    if (d.R)
+                        o += *(const f32x4 *)((const float *)d.R + ridx);
+                    *(f32x4 *)((float *)d.C + idx) = o;
+                }
+                else {
+                    f32x4 o = v4;
+                    uint2 pk;
+
+                    if (d.R) {
+                        const uint2 rv = *(const uint2 *)((const uint16_t *)d.R + ridx);
+
+                        o.x += __builtin_bit_cast(float, rv.x << 16);
+                        o.y += __builtin_bit_cast(float, rv.x & 0xffff0000u);
+                        o.z += __builtin_bit_cast(float, rv.y << 16);
+                        o.w += __builtin_bit_cast(float, rv.y & 0xffff0000u);
+                    }
+                    pk.x = pack_bf16x2(o.x, o.y);
+                    pk.y = pack_bf16x2(o.z, o.w);
+                    *(uint2 *)((uint16_t *)d.C + idx) = pk;
+                }
+            }
+            else
+                for (int e = 0; e < 4 && n + e < d.N; e++) {
+                    float v = v4[e];
+
                     if (d.cdt == DT_F32) {
                         if (d.R)
-                            v += ((const float *)d.R)[idx - d.coff + d.roff];
-                        ((float *)d.C)[idx] = v;
+                            v += ((const float *)d.R)[ridx + e];
+                        ((float *)d.C)[idx + e] = v;
                     }
                     else {
                         if (d.R)
-                            v += bf2f(((const uint16_t *)d.R)[idx - d.coff + d.roff]);
-                        ((uint16_t *)d.C)[idx] = f2bf(v);
+                            v += bf2f(((const uint16_t *)d.R)[ridx + e]);
+                        ((uint16_t *)d.C)[idx + e] = f2bf(v);
                     }
                 }
-            }
         }
+        __syncthreads();
     }
 }
 

@@ -49,6 +49,11 @@ struct gemm_desc {
     float alpha;
     int act;
     int mode;
+    /* NT kernel only: with ws > 0, output row m is window-partition
+     * position m of an H x H grid (nwx windows per side) and C / R rows
+     * are its grid token (padding rows are dropped): the projection's
+     * window_unpartition_add fused into the store. */
+    int unpart_H, unpart_ws, unpart_nwx;
 };
 int launch_gemm(const struct gemm_desc *d, void *stream);
 /* The bf16 x bf16 "NT" kernel (A [M][K], B [N][K], K % 64 == 0,

@@ -678,6 +678,55 @@ void vit_attention(struct sam_model *m, const struct vit_block *blk,
 
 /* ------------------------------------------------------------ trunk */
 
+/* x[token(r)] += A[r] W^T + b for the window-partitioned rows r of a
+ * windowed block: the projection and window_unpartition_add
+ * (sam3_model.c:1015-1019) in one bf16 NT GEMM whose epilogue maps each
+ * row to its grid token. Returns 0 (nothing queued) when the operands do
+ * not take the NT kernel. */
+static int proj_unpartition(struct sam_model *m, long rows, hipb_mem A,
+                            const struct vit_block *blk, int ws, int nwx)
+{
+    struct hipb_backend *b = m->hip;
+    const int E = m->embed, T = m->grid * m->grid;
+    struct gemm_desc d;
+    int err;
+
+    if (!opnd_ok("vit_block", "A", mat(A, 0, E), rows, E, 1, 1) ||
+        !opnd_ok("vit_block", "projw", mat(blk->projw, 0, E), E, E, 1, 1) ||
+        !buf_ok("vit_block", "x", m->x, (size_t)T * E, HIPB_F32) ||
+        !buf_ok("vit_block", "projb", blk->projb, (size_t)E, HIPB_F32))
+        return 1;
+    memset(&d, 0, sizeof(d));
+    d.M = (int)rows;
+    d.N = E;
+    d.K = E;
+    d.A = A->ptr;
+    d.lda = E;
+    d.adt = A->dtype;
+    d.B = blk->projw->ptr;
+    d.ldb = E;
+    d.bdt = blk->projw->dtype;
+    d.transb = 1;
+    d.C = m->x->ptr;
+    d.ldc = E;
+    d.cdt = HIPB_F32;
+    d.nb = d.nb1 = 1;
+    d.bias = (const float *)blk->projb->ptr;
+    d.R = m->x->ptr;
+    d.alpha = 1.0f;
+    d.act = ACT_NONE;
+    d.mode = b->bf16 ? MODE_BF16 : MODE_F32;
+    d.unpart_H = m->grid;
+    d.unpart_ws = ws;
+    d.unpart_nwx = nwx;
+    if (!gemm_nt_ok(&d))
+        return 0;
+    hipb_run_begin(b);
+    err = launch_gemm_nt(&d, b->stream);
+    hipb_run_end(b, err, "gemm_nt_bf16", 2.0 * rows * E * (double)E);
+    return 1;
+}
+
 void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused)
 {
     struct hipb_backend *b = m->hip;
@@ -705,7 +754,10 @@ void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused)
     if (hipb_failed())
         return;
     /* Projection with residual (sam3_model.c:1015-1022). */
-    if (blk->window) {
+    if (blk->window && proj_unpartition(m, rows, A, blk, g.s, g.nwx)) {
+        /* fused into the NT GEMM (or an operand check failed: reported) */
+    }
+    else if (blk->window) {
         linear(m, (int)rows, E, E, A, 0, blk->projw, blk->projb, m->tmp, 0,
                ACT_NONE, 0);
         window_unpartition_add(m, m->x, m->tmp, m->grid, E, g.s, g.nwx);

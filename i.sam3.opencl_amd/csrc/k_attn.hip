@@ -573,12 +573,67 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     }
 
     st.l += __shfl_xor(st.l, 32, 64);
-    if (qi < N) {
-        const float inv = 1.0f / st.l;
-        const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-        const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
+    const float inv = 1.0f / st.l;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+    const long obase = d.ooff + b0 * d.so0 + b1 * d.so1;
+    const bool f32out = d.odt == DT_F32;
 
-        if (d.odt == DT_F32) {
+    if ((((obase | (long)d.ldo) & (f32out ? 3 : 7)) | ((uintptr_t)d.O & 15)) == 0) {
+        /* Output rows 16-byte aligned: transpose the wave's O^T through
+         * LDS so that 8 lanes write one 128-byte line of one query row.
+         * The slot of block nblk - 2 (or the unused one) is free: every
+         * wave passed the last barrier after its final reads of it. Each
+         * wave takes 4 KB; 16-byte chunk c of staging row r sits at chunk
+         * c ^ (r & 7), which keeps both the writes (8 rows, one chunk)
+         * and the reads (one row, 8 chunks) free of bank conflicts. */
+        const int fs = nblk & 1;
+        char *stg = w < 2 ? (char *)&Ks[fs][32 * w][0] : (char *)&Vt[fs][32 * (w - 2)][0];
+        const int q0 = qi - l32, c = l & 7;
+
+        if (f32out) {
+            /* Two passes of 32 columns (128 B per row). */
+            for (int half = 0; half < 2; half++) {
+                const f32x16 &o = half ? st.o1 : st.o0;
+
+                for (int g = 0; g < 4; g++) {
+                    const f32x4 v = {o[4 * g] * inv, o[4 * g + 1] * inv,
+                                     o[4 * g + 2] * inv, o[4 * g + 3] * inv};
+
+                    *(f32x4 *)(stg + 128 * l32 + 16 * ((2 * g + h) ^ (l32 & 7))) = v;
+                }
+                for (int j = 0; j < 4; j++) {
+                    const int row = 8 * j + (l >> 3);
+                    const f32x4 v = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
+
+                    if (q0 + row < N)
+                        *(f32x4 *)((float *)d.O + obase + (long)(q0 + row) * d.ldo + 32 * half + 4 * c) = v;
+                }
+            }
+        }
+        else {
+            /* One pass: a row is 64 bf16 = 128 B; lane (l32, h) holds
+             * columns 8 g + 4 h .. +3, half h of logical chunk g. */
+            for (int g = 0; g < 8; g++) {
+                const f32x16 &o = g < 4 ? st.o0 : st.o1;
+                const int r = 4 * (g & 3);
+                const uint2 pk = {pack_bf16x2(o[r] * inv, o[r + 1] * inv),
+                                  pack_bf16x2(o[r + 2] * inv, o[r + 3] * inv)};
+
+                *(uint2 *)(stg + 128 * l32 + 16 * (g ^ (l32 & 7)) + 8 * h) = pk;
+            }
+            for (int j = 0; j < 4; j++) {
+                const int row = 8 * j + (l >> 3);
+                const u32x4 v = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
+
+                if (q0 + row < N)
+                    *(u32x4 *)((uint16_t *)d.O + obase + (long)(q0 + row) * d.ldo + 8 * c) = v;
+            }
+        }
+    }
+    else if (qi < N) {
+        const long orow = obase + (long)qi * d.ldo;
+
+        if (f32out) {
             for (int r = 0; r < 16; r++) {
                 const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 

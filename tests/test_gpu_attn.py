@@ -86,6 +86,31 @@ def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
     assert report("ragged N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
 
 
+@pytest.mark.parametrize("ooff,ldo", [(1, 131), (4, 132), (8, 136)])
+def test_output_offsets(hip, be, orc, ooff, ldo):
+    """Output rows at an offset and stride that break 16-byte alignment
+    (per-element stores) or keep it (rows transposed through LDS), with
+    the padding columns between rows left untouched."""
+    N, H, E = 150, 2, 128
+    m = hip.Model(be, embed=E, heads=H)
+    qkv = np.random.default_rng(ooff).standard_normal((N, 3 * E), np.float32)
+    dq = be.upload(qkv)
+    fill = np.full(ooff + N * ldo, 7.0, np.float32)
+    do = be.upload(fill)
+    hip.attn_fused(m, N, H, H, hip.bmat(dq, 0, 3 * E, 0, 64),
+                   hip.bmat(dq, E, 3 * E, 0, 64),
+                   hip.bmat(dq, 2 * E, 3 * E, 0, 64),
+                   hip.bmat(do, ooff, ldo, 0, 64), None, 1, 0.125)
+    raw = be.read(do)
+    got = raw[ooff:].reshape(N, ldo)
+    want = _oracle_units(orc, qkv, N, 1, H, E, None)
+    assert np.all(raw[:ooff] == 7.0) and np.all(got[:, E:] == 7.0)
+    assert report("offsets %d/%d %s" % (ooff, ldo, be.precision), got[:, :E],
+                  want) <= TOL[be.precision]
+    be.release(dq)
+    be.release(do)
+
+
 def test_attention_closed_forms(hip, be):
     """Zero queries give the mean of V; one token gives V itself."""
     E, H = 128, 2

@@ -386,6 +386,19 @@ __device__ __forceinline__ void g2lds16(const void *g, void *lds_base)
                  : "memory", "m0");
 }
 
+/* The same copy with a wave-uniform 64-bit base in SGPRs and a 32-bit
+ * per-lane byte offset (the saddr form): no per-lane address arithmetic
+ * when only the base moves from block to block. `lds` must be
+ * wave-uniform. */
+__device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsigned lds)
+{
+    asm volatile("s_mov_b32 m0, %0\n\t"
+                 "global_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
+
 /* Scores may run this far (log2 units) above or below the reference
  * point m before it must move: exp2 of them stays far inside the float
  * and bf16 ranges, and the accumulated O and l with it (5184 keys x 2^64
@@ -467,36 +480,64 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     /* Async copy of block kb into `slot`: wave w, pass j fills LDS rows
      * 8 (2 w + j) .. +7; lane i lands on row + i / 8, physical chunk
      * i % 8, so it fetches logical chunk (i % 8) ^ ((row >> 1) & 7). The
-     * per-lane element offsets do not depend on the block. */
-    int koff[2], voff[2];
+     * per-lane byte offsets do not depend on the block; the bases (block
+     * start in global memory, destination rows in LDS) are wave-uniform
+     * and live in SGPRs. */
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    unsigned koff[2], voff[2];
     for (int j = 0; j < 2; j++) {
         const int row = 8 * (2 * w + j) + (l >> 3);
         const int chunk = (l & 7) ^ ((row >> 1) & 7);
 
-        koff[j] = row * 64 + 8 * chunk;
-        voff[j] = row * Np + 8 * chunk;
+        koff[j] = 2u * (row * 64 + 8 * chunk);
+        voff[j] = 2u * (row * Np + 8 * chunk);
     }
+    const unsigned lds_k = (unsigned)(uintptr_t)&Ks[0][0][0] + 2048u * wu,
+                   lds_v = (unsigned)(uintptr_t)&Vt[0][0][0] + 2048u * wu;
     auto load_block = [&](int kb, int slot) {
         const uint16_t *kb_ = Ku + (long)kb * 64 * 64, *vb_ = Vu + kb * 64;
 
         for (int j = 0; j < 2; j++) {
-            g2lds16(kb_ + koff[j], &Ks[slot][8 * (2 * w + j)][0]);
-            g2lds16(vb_ + voff[j], &Vt[slot][8 * (2 * w + j)][0]);
+            g2lds16_s(kb_, koff[j], lds_k + 8192u * slot + 1024u * j);
+            g2lds16_s(vb_, voff[j], lds_v + 8192u * slot + 1024u * j);
         }
     };
+    /* Byte offsets of this lane's MFMA operand fragments within one slot:
+     * K rows 32 c + kperm(l32) (c adds 4096 B), V^T rows l32 and 32 + l32
+     * (+4096 B); the swizzle depends only on row bits 1..3, which c and
+     * the +32 leave alone. */
+    unsigned kro[4], vro[4];
+    for (int i = 0; i < 4; i++) {
+        kro[i] = 2u * (krow * 64 + swz(krow, 2 * i + h));
+        vro[i] = 2u * (l32 * 64 + swz(l32, 2 * i + h));
+    }
+    const char *Kb = (const char *)&Ks[0][0][0], *Vb = (const char *)&Vt[0][0][0];
+    float kn_next = kn[0];
 
     load_block(0, 0);
-    for (int kb = 0; kb < nblk; kb++) {
-        const int slot = kb & 1;
+    /* Unrolled by two so that the slot is a constant: the LDS fragment
+     * addresses are then one register plus an immediate offset. */
+    auto block = [&](int kb, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
         bf16x8 kf[8], vf[8], pb[4];
         f32x16 s0, s1;
         /* Can this block's scores exceed m + SAFE_SPAN for some lane? */
-        const bool check = __ballot(fresh || qn * kn[kb] - st.m > SAFE_SPAN) != 0;
+        const bool check = __ballot(fresh || qn * kn_next - st.m > SAFE_SPAN) != 0;
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        /* Next block's bound, loaded after the barrier so that its latency
+         * hides behind this block rather than in the barrier's wait. */
+        kn_next = kn[kb + 1 < nblk ? kb + 1 : kb];
         if (kb + 1 < nblk)
             load_block(kb + 1, slot ^ 1);
+        for (int c = 0; c < 2; c++)
+            for (int ds = 0; ds < 4; ds++)
+                kf[4 * c + ds] = *(const bf16x8 *)(Kb + 8192 * slot + 4096 * c + kro[ds]);
+        for (int t4 = 0; t4 < 4; t4++) {
+            vf[2 * t4] = *(const bf16x8 *)(Vb + 8192 * slot + vro[t4]);
+            vf[2 * t4 + 1] = *(const bf16x8 *)(Vb + 8192 * slot + 4096 + vro[t4]);
+        }
         /* Both 32-key halves at once: two independent Q K^T chains. */
         for (int c = 0; c < 2; c++) {
             const int row = 32 * c + krow;
@@ -570,6 +611,11 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 p2.y = pb[a][2 * e + 1];
                 st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
             }
+    };
+    for (int kb = 0; kb < nblk; kb += 2) {
+        block(kb, std::integral_constant<int, 0>());
+        if (kb + 1 < nblk)
+            block(kb + 1, std::integral_constant<int, 1>());
     }
 
     st.l += __shfl_xor(st.l, 32, 64);

@@ -38,7 +38,7 @@ COPY_BYTES = 256 << 20
 # (KiB per dispatch), each scaled by what the counter reads for the
 # runtime's 256 MiB copy in the same run (FETCH_SIZE 2.0, WRITE_SIZE 1.0).
 # Summary and commands: profiles/attn_bf16_global_5184.md.
-ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15618.0, 20736.0
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15641.0, 20736.0
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 
 

@@ -539,18 +539,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             vf[2 * t4 + 1] = *(const bf16x8 *)(Vb + 8192 * slot + 4096 + vro[t4]);
         }
         /* Both 32-key halves at once: two independent Q K^T chains. */
-        for (int c = 0; c < 2; c++) {
-            const int row = 32 * c + krow;
-
-            for (int ds = 0; ds < 4; ds++)
-                kf[4 * c + ds] = *(const bf16x8 *)&Ks[slot][row][swz(row, 2 * ds + h)];
-        }
-        for (int t4 = 0; t4 < 4; t4++) {
-            const int chunk = 2 * t4 + h;
-
-            vf[2 * t4] = *(const bf16x8 *)&Vt[slot][l32][swz(l32, chunk)];
-            vf[2 * t4 + 1] = *(const bf16x8 *)&Vt[slot][32 + l32][swz(32 + l32, chunk)];
-        }
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qb[0], zero16, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4], qb[0], zero16, 0, 0, 0);
         for (int ds = 1; ds < 4; ds++) {

@@ -52,7 +52,123 @@ __device__ __forceinline__ void nt_g2lds16(const void *g, void *lds_base)
                  : "memory", "m0");
 }
 
-template <int BM, int BN, int WM, int WN>
+/* Store of a 128 x 128 tile of a QKV projection as packed attention
+ * operands (gemm_desc pack_*), from the float tile E [128][132] in LDS:
+ * the tile's columns are two 64-wide heads of one third. Wave w takes
+ * head w / 2 and tile rows 64 (w % 2) .. +63, one 64-key block of one
+ * unit (pack_N and the row count are multiples of 64), in eight passes of
+ * eight rows: lane l handles 16-byte chunk l % 8 of row l / 8, so eight
+ * lanes write one whole 128-byte output row. q / k: RoPE on the chunk's
+ * four pairs (2j, 2j + 1), q times scale log2 e, bf16; for k the block's
+ * largest |k| over the bf16 values, rounded up by 2^-10. v (V^T rows of
+ * 64 keys): lane l takes channel 8 pass + l / 8 and keys 8 (l % 8) .. +7.
+ * The arithmetic is k_qkv_pack's, so the operands are the same bits. */
+__device__ __forceinline__ void nt_pack_rope(const gemm_desc &d, int m0, int n0, int t,
+                                             float2 (&rot)[8][4])
+{
+    const int third = n0 / d.pack_E, w = t >> 6, l = t & 63, mw = m0 + (w & 1) * 64;
+
+    if (third < 2 && d.pack_rope && mw < d.M)
+        for (int pass = 0; pass < 8; pass++) {
+            const int p = (mw + 8 * pass + (l >> 3)) % d.pack_N;
+            const float4 *src = (const float4 *)((const float2 *)d.pack_rope +
+                                                 (long)(p % d.pack_npos) * 32 + 4 * (l & 7));
+            const float4 r0 = src[0], r1 = src[1];
+
+            rot[pass][0] = make_float2(r0.x, r0.y);
+            rot[pass][1] = make_float2(r0.z, r0.w);
+            rot[pass][2] = make_float2(r1.x, r1.y);
+            rot[pass][3] = make_float2(r1.z, r1.w);
+        }
+}
+
+__device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0, int t,
+                              const float2 (&rot)[8][4])
+{
+    constexpr int LD = 132;
+    const int Np = d.pack_N, heads = d.pack_E / 64;
+    const int third = n0 / d.pack_E, head0 = (n0 - third * d.pack_E) / 64;
+    const int w = t >> 6, l = t & 63, hh = w >> 1, rbase = (w & 1) * 64;
+    const int mw = m0 + rbase, c8 = l & 7, r8 = l >> 3;
+
+    if (mw >= d.M)
+        return;
+    const int win = mw / Np, p0 = mw - win * Np;
+    const long unit = (long)win * heads + head0 + hh;
+
+    if (third < 2) {
+        uint16_t *dst = (uint16_t *)(third == 0 ? d.pack_q16 : d.pack_k16) +
+                        (unit * Np + p0) * 64 + 8 * c8;
+        float mx = 0.0f; /* largest row |k|^2 seen, of the bf16 values */
+
+        for (int pass = 0; pass < 8; pass++) {
+            const int row = 8 * pass + r8;
+            const float *src = E + (rbase + row) * LD + hh * 64 + 8 * c8;
+            const f32x4 x0 = *(const f32x4 *)src, x1 = *(const f32x4 *)(src + 4);
+            float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            float ps = 0.0f;
+            u32x4 pk;
+
+            if (d.pack_rope)
+                for (int j = 0; j < 4; j++) {
+                    const float2 r = rot[pass][j];
+                    const float a = v[2 * j], b = v[2 * j + 1];
+
+                    v[2 * j] = fmaf(a, r.x, -(b * r.y));
+                    v[2 * j + 1] = fmaf(a, r.y, b * r.x);
+                }
+            if (third == 0)
+                for (int e = 0; e < 8; e++)
+                    v[e] *= d.pack_scale * LOG2E_F;
+            for (int e = 0; e < 4; e++) {
+                pk[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+                if (third == 1) {
+                    /* Built element-wise: a bit-cast of pk[e] here was
+                     * compiled to reads of stale registers. */
+                    bf16x2 b2;
+
+                    b2.x = (__bf16)v[2 * e];
+                    b2.y = (__bf16)v[2 * e + 1];
+                    ps = __builtin_amdgcn_fdot2_f32_bf16(b2, b2, ps, false);
+                }
+            }
+            *(u32x4 *)(dst + (long)row * 64) = pk;
+            if (third == 1) {
+                /* The row's |k|^2: its 8 lanes' chunk sums. */
+                ps += __shfl_xor(ps, 1, 64);
+                ps += __shfl_xor(ps, 2, 64);
+                ps += __shfl_xor(ps, 4, 64);
+                mx = fmaxf(mx, ps);
+            }
+        }
+        if (third == 1) {
+            mx = wave_max(mx);
+            if (l == 0)
+                d.pack_knorm[unit * (Np / 64) + p0 / 64] = sqrtf(mx) * (1.0f + 0x1p-10f);
+        }
+    }
+    else {
+        for (int pass = 0; pass < 8; pass++) {
+            const int ch = 8 * pass + r8;
+            const float *src = E + (rbase + 8 * c8) * LD + hh * 64 + ch;
+            u32x4 pk;
+
+            for (int e = 0; e < 4; e++)
+                pk[e] = pack_bf16x2(src[(2 * e) * LD], src[(2 * e + 1) * LD]);
+            *(u32x4 *)((uint16_t *)d.pack_vt16 + (unit * 64 + ch) * Np + p0 + 8 * c8) = pk;
+        }
+    }
+}
+
+/* Wait until at most N of this wave's vector-memory operations are
+ * outstanding (they retire in issue order). */
+template <int N>
+__device__ __forceinline__ void nt_vm_wait()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int NSLOT>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt(gemm_desc d)
 {
@@ -64,10 +180,10 @@ k_gemm_nt(gemm_desc d)
     constexpr int NB = WN / 32;             /* 32-column blocks per wave */
     constexpr int ROWS = BM + BN;           /* LDS rows per stage */
     constexpr int LPW = ROWS / (8 * NW);    /* copies per wave per stage */
-    constexpr int LDS_BYTES = 2 * ROWS * NT_KS * 2 > EPI_BYTES
-                                  ? 2 * ROWS * NT_KS * 2
+    constexpr int LDS_BYTES = NSLOT * ROWS * NT_KS * 2 > EPI_BYTES
+                                  ? NSLOT * ROWS * NT_KS * 2
                                   : EPI_BYTES;
-    /* Two operand slots during the K loop, the output tile in the
+    /* NSLOT operand slots during the K loop, the output tile in the
      * epilogue (which may need a little more). */
     __shared__ __attribute__((aligned(16))) uint16_t S_raw[LDS_BYTES / 2];
     uint16_t(*S)[ROWS][NT_KS] = (uint16_t(*)[ROWS][NT_KS])S_raw;
@@ -124,14 +240,23 @@ k_gemm_nt(gemm_desc d)
         }
     };
 
-    load_stage(0, 0);
+    /* NSLOT - 1 stages in flight ahead of the one being multiplied. */
+    for (int ks = 0; ks < NSLOT - 1 && ks < nk; ks++)
+        load_stage(ks, ks);
     for (int ks = 0; ks < nk; ks++) {
-        const int slot = ks & 1;
+        const int slot = ks % NSLOT, ahead = min(NSLOT - 2, nk - 1 - ks);
 
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        /* Stage ks has landed once no more than the later stages' copies
+         * are outstanding. */
+        if (ahead >= 2)
+            nt_vm_wait<2 * LPW>();
+        else if (ahead == 1)
+            nt_vm_wait<LPW>();
+        else
+            nt_vm_wait<0>();
         __syncthreads();
-        if (ks + 1 < nk)
-            load_stage(ks + 1, slot ^ 1);
+        if (ks + NSLOT - 1 < nk)
+            load_stage(ks + NSLOT - 1, (ks + NSLOT - 1) % NSLOT);
 #pragma unroll
         for (int s = 0; s < NT_KS / 16; s++) {
             bf16x8 a[NA], b[NB];
@@ -168,6 +293,12 @@ k_gemm_nt(gemm_desc d)
     constexpr int CR = EPI_ROWS, LD = BN + 4, T = NW * 64, RPI = T * 4 / BN;
     float *E = (float *)S_raw;
     const bool vec = d.ldc % 4 == 0 && d.coff % 4 == 0 && d.roff % 4 == 0;
+    float2 rot[8][4];
+
+    if constexpr (BM == 128 && BN == 128) {
+        if (d.pack_N > 0)
+            nt_pack_rope(d, m0, n0, t, rot);
+    }
 
     __syncthreads();
 #pragma clang loop unroll(full)
@@ -191,6 +322,12 @@ k_gemm_nt(gemm_desc d)
             }
         }
         __syncthreads();
+        if constexpr (BM == 128 && BN == 128) {
+            if (d.pack_N > 0) {
+                nt_pack_store(d, E, m0, n0, t, rot);
+                return;
+            }
+        }
         for (int it = 0; it < CR / RPI; it++) {
             const int row = it * RPI + t / (BN / 4), col = (t % (BN / 4)) * 4;
             const int m = m0 + c * CR + row, n = n0 + col;
@@ -280,7 +417,11 @@ extern "C" int gemm_nt_ok(const gemm_desc *d)
     return d->mode == MODE_BF16 && d->adt == DT_BF16 && d->bdt == DT_BF16 &&
            d->transb && d->nb == 1 && d->K >= NT_KS && d->K % NT_KS == 0 &&
            d->lda % 8 == 0 && d->ldb % 8 == 0 && d->aoff % 8 == 0 &&
-           d->boff % 8 == 0 && d->M >= 1 && d->N >= 1;
+           d->boff % 8 == 0 && d->M >= 1 && d->N >= 1 &&
+           (d->pack_N == 0 ||
+            (d->pack_N % 64 == 0 && d->pack_E % 128 == 0 && d->N == 3 * d->pack_E &&
+             d->M % d->pack_N == 0 && d->alpha == 1.0f && d->act == ACT_NONE_K && !d->R &&
+             d->unpart_ws == 0 && d->pack_npos >= 1));
 }
 
 /* Returns -1 when the NT kernel does not apply, else a hipError_t. */
@@ -300,7 +441,8 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
      * 646 vs 691 TFLOP/s (N = 3072) and 460 vs 585 (N = 4096), K = 4096
      * at 1145 vs 1070 (N = 3072). */
     t256 = (long)((d->M + 255) / 256) * ((d->N + 255) / 256);
-    bm = t256 >= cu_count() * 9 / 10 && d->K >= 2048 ? 256 : 128;
+    /* The packed-operand store exists for 128 x 128 tiles only. */
+    bm = t256 >= cu_count() * 9 / 10 && d->K >= 2048 && d->pack_N == 0 ? 256 : 128;
     bn = bm;
     {
         const long tiles = (long)((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn);
@@ -309,10 +451,10 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
         if (grid > 0x7fffffffL)
             return hipErrorInvalidConfiguration;
         if (bm == 256)
-            hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64>),
+            hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64, 2>),
                                dim3((unsigned)grid), dim3(512), 0, s, *d);
         else
-            hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64>),
+            hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64, 2>),
                                dim3((unsigned)grid), dim3(256), 0, s, *d);
     }
     return hipGetLastError();

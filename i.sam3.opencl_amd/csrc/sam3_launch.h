@@ -54,6 +54,18 @@ struct gemm_desc {
      * are its grid token (padding rows are dropped): the projection's
      * window_unpartition_add fused into the store. */
     int unpart_H, unpart_ws, unpart_nwx;
+    /* NT kernel only: with pack_N > 0 the product is a QKV projection
+     * (N = 3 pack_E columns, q | k | v thirds of 64-wide heads; rows are
+     * units of pack_N tokens, pack_N % 64 == 0) and the store writes the
+     * attention operands of launch_qkv_pack instead of C: q16 / k16
+     * [unit][pack_N][64] bf16 with RoPE (pack_rope, pack_npos positions;
+     * q also scaled by pack_scale log2 e), vt16 [unit][64][pack_N], and
+     * knorm per 64-key block; unit = row / pack_N * heads + head. */
+    int pack_N, pack_E, pack_npos;
+    float pack_scale;
+    const float *pack_rope;
+    void *pack_q16, *pack_k16, *pack_vt16;
+    float *pack_knorm;
 };
 int launch_gemm(const struct gemm_desc *d, void *stream);
 /* The bf16 x bf16 "NT" kernel (A [M][K], B [N][K], K % 64 == 0,

@@ -559,6 +559,71 @@ static int head_chunk(const struct sam_model *m, const struct geom *g)
 
 /* The attention region of vit_attention with its output operand O
  * (rows of the block's window order, head h at column h * hd). */
+/* QKV projection of a block written straight as the packed attention
+ * operands (the NT GEMM's packed store: RoPE, scale, bf16, V^T and the
+ * key block norms in the GEMM epilogue, no fp32 qkv round trip). Returns
+ * 0 without queueing anything when the shape does not allow it (head
+ * width 64, E % 128 == 0 and N % 64 == 0 are needed), 1 when queued. */
+static int qkv_projection_packed(struct sam_model *m, const struct vit_block *blk,
+                                 long rows, int N, hipb_mem table, float scale)
+{
+    struct hipb_backend *b = m->hip;
+    const int E = m->embed;
+    const long nb = rows / (N > 0 ? N : 1) * m->heads;
+    struct gemm_desc d;
+    int err;
+
+    if (m->hd != 64 || E % 128 || N < 64 || N % 64 || rows % N ||
+        !blk->qkvw || blk->qkvw->dtype != HIPB_BF16 || !m->xn16 ||
+        (blk->qkvb && blk->qkvb->dtype != HIPB_F32))
+        return 0;
+    memset(&d, 0, sizeof(d));
+    d.M = (int)rows;
+    d.N = 3 * E;
+    d.K = E;
+    d.A = m->xn16->ptr;
+    d.lda = E;
+    d.adt = HIPB_BF16;
+    d.B = blk->qkvw->ptr;
+    d.ldb = E;
+    d.bdt = HIPB_BF16;
+    d.transb = 1;
+    d.cdt = HIPB_F32;
+    d.nb = d.nb1 = 1;
+    d.bias = blk->qkvb ? (const float *)blk->qkvb->ptr : NULL;
+    d.alpha = 1.0f;
+    d.act = ACT_NONE;
+    d.mode = MODE_BF16;
+    d.pack_N = N;
+    d.pack_E = E;
+    d.pack_npos = N;
+    d.pack_scale = scale;
+    d.pack_rope = (const float *)table->ptr;
+    if (!gemm_nt_ok(&d))
+        return 0;
+    if (!buf_ok("vit_attention", "normalized tokens", m->xn16, (size_t)rows * E,
+                HIPB_BF16) ||
+        !buf_ok("vit_attention", "qkv weight", blk->qkvw, (size_t)3 * E * E,
+                HIPB_BF16) ||
+        (blk->qkvb && !buf_ok("vit_attention", "qkv bias", blk->qkvb,
+                              (size_t)3 * E, HIPB_F32)) ||
+        !buf_ok("vit_attention", "rope", table, (size_t)N * 64, HIPB_F32) ||
+        !ensure_bf16(b, &m->q16, (size_t)nb * N * 64, "packed q") ||
+        !ensure_bf16(b, &m->k16, (size_t)nb * N * 64, "packed k") ||
+        !ensure_bf16(b, &m->vt16, (size_t)nb * N * 64, "packed v^T") ||
+        !ensure_typed(b, &m->knorm, (size_t)nb * (N / 64), HIPB_F32,
+                      "key block norms"))
+        return 0;
+    d.pack_q16 = m->q16->ptr;
+    d.pack_k16 = m->k16->ptr;
+    d.pack_vt16 = m->vt16->ptr;
+    d.pack_knorm = (float *)m->knorm->ptr;
+    hipb_run_begin(b);
+    err = launch_gemm_nt(&d, b->stream);
+    hipb_run_end(b, err, "gemm_nt_qkv_pack", 2.0 * rows * 3.0 * E * E);
+    return !hipb_failed();
+}
+
 static void attention_region(struct sam_model *m, const struct vit_block *blk,
                              int unfused, hipb_mem obuf)
 {
@@ -596,6 +661,13 @@ static void attention_region(struct sam_model *m, const struct vit_block *blk,
                 blk->window ? m->grid : 0, blk->window ? g.s : 0, g.nwx,
                 b->stream);
             hipb_run_end(b, err, "layernorm", 0.0);
+        }
+        if (hipb_failed())
+            return;
+        if (qkv_projection_packed(m, blk, rows, g.N, table, scale)) {
+            attn_packed(m, g.N, g.nwin * m->heads, m->heads,
+                        bmat(obuf, 0, E, (long)g.N * E, hd));
+            return;
         }
         if (hipb_failed())
             return;

@@ -6,9 +6,12 @@ Bars: rel-L2 <= 2e-5 for the fp32 path, <= 2e-2 for the bf16 path; the
 max-abs error is printed with every check.
 
 Full-size workloads (9 x 576 windows, 5184 global tokens) are checked on
-sampled (unit, head, query-row) sets: the QKV projection rows against the
-oracle's LayerNorm + linear, and the attention rows against the oracle's
-attention of the same rows computed from the device's qkv.
+sampled (unit, head, query-row) sets: on the fp32 path the QKV projection
+rows against the oracle's LayerNorm + linear and the attention rows
+against the oracle's attention computed from the device's qkv; on the
+bf16 path (whose projection packs the attention operands in its store and
+writes no fp32 qkv) the attention rows against the oracle's attention of
+the oracle's qkv.
 """
 import math
 
@@ -154,9 +157,13 @@ def _vit_small(hip, be, orc, grid, ws, unfused=False, E=128):
     return got, want
 
 
-@pytest.mark.parametrize("grid,ws", [(12, 6), (12, 0), (10, 4)])
+@pytest.mark.parametrize("grid,ws", [(12, 6), (12, 0), (10, 4), (16, 8), (16, 0),
+                                     (8, 0), (24, 8)])
 @pytest.mark.parametrize("unfused", [False, True])
 def test_vit_attention_small(hip, be, orc, grid, ws, unfused):
+    """Token counts per unit of 36, 144, 16 (packing kernel on the bf16
+    path) and 64, 256, 576 (operands packed by the projection's store;
+    grid 8 and 24 leave a partial 128-row tile)."""
     got, want = _vit_small(hip, be, orc, grid, ws, unfused)
     assert report("vit_attention grid=%d ws=%d unfused=%d %s" %
                   (grid, ws, unfused, be.precision), got, want) <= TOL[be.precision]
@@ -184,15 +191,20 @@ def test_vit_attention_full_size(hip, be, orc, ws):
     hip.vit_attention(m, blk)
     rows = grid * grid
     attn = be.read(m.m.attn, rows * E).reshape(rows, E)
-    qkv = be.read(m.m.qkv, rows * 3 * E).reshape(rows, 3 * E)
-
-    # QKV projection of sampled rows against LayerNorm + linear.
     xn = orc.layernorm(x, n1w, n1b)
     xw = orc.window_partition(xn, grid, grid, E, s) if ws else xn
-    pick = np.random.default_rng(0).choice(rows, 64, replace=False)
-    want_qkv = orc.linear(xw[pick], w, b, cpu=True)
-    assert report("qkv rows ws=%d %s" % (ws, be.precision), qkv[pick],
-                  want_qkv) <= TOL[be.precision]
+    if be.precision == "fp32":
+        # QKV projection of sampled rows against LayerNorm + linear; the
+        # attention below starts from the device's qkv.
+        qkv = be.read(m.m.qkv, rows * 3 * E).reshape(rows, 3 * E)
+        pick = np.random.default_rng(0).choice(rows, 64, replace=False)
+        want_qkv = orc.linear(xw[pick], w, b, cpu=True)
+        assert report("qkv rows ws=%d %s" % (ws, be.precision), qkv[pick],
+                      want_qkv) <= TOL[be.precision]
+    else:
+        # The bf16 path packs the operands in the projection's store and
+        # writes no fp32 qkv: the attention starts from the oracle's.
+        qkv = orc.linear(xw, w, b, cpu=True)
 
     # Attention of sampled (unit, head, rows) from the device's qkv.
     g = np.random.default_rng(1)
@@ -207,3 +219,46 @@ def test_vit_attention_full_size(hip, be, orc, ws):
     assert report("attention rows ws=%d %s" % (ws, be.precision),
                   np.concatenate(got), np.concatenate(want)) <= TOL[be.precision]
     m.free()
+
+
+@pytest.mark.parametrize("grid,ws", [(16, 8), (24, 8), (16, 0)])
+def test_packed_projection_matches_packing_kernel(hip, orc, grid, ws):
+    """bf16 path: the operands the QKV projection's store packs (RoPE,
+    scale, bf16, V^T, key block norms) are the packing kernel's, bit for
+    bit (norm bounds to 1e-6), on the same device projection."""
+    be = hip.Backend(precision="bf16")
+    E, H = 128, 2
+    x, n1w, n1b, w, b = block_inputs(grid + 3 * ws, grid, E)
+    s = ws if ws else grid
+    N = s * s
+    rows = (grid // s) ** 2 * N
+    nb = rows // N * H
+    table = orc.rope_table(s)
+    blk = hip.VitBlock()
+    blk.n1w, blk.n1b = be.upload(n1w), be.upload(n1b)
+    blk.qkvw, blk.qkvb = be.upload_weight(w), be.upload(b)
+    blk.window = ws
+    m = hip.Model(be, grid=grid, embed=E, heads=H, blocks=[blk])
+    tab = be.upload(table)
+    if ws:
+        m.m.rope_win = tab
+    else:
+        m.m.rope_glob = tab
+    be.write(m.m.x, 0, x)
+    hip.vit_attention(m, blk)
+    fused = [be.read(getattr(m.m, k), nb * N * 64) for k in ("q16", "k16", "vt16")]
+    kn_fused = be.read(m.m.knorm, nb * N // 64)
+    hip.linear(m, rows, E, 3 * E, m.m.xn16, 0, blk.qkvw, blk.qkvb, m.m.qkv, 0)
+    q = m.m.qkv
+    hip.attn_fused(m, N, nb, H, hip.bmat(q, 0, 3 * E, N * 3 * E, 64),
+                   hip.bmat(q, E, 3 * E, N * 3 * E, 64),
+                   hip.bmat(q, 2 * E, 3 * E, N * 3 * E, 64),
+                   hip.bmat(m.m.attn, 0, E, N * E, 64), tab, N, 0.125)
+    kernel = [be.read(getattr(m.m, k), nb * N * 64) for k in ("q16", "k16", "vt16")]
+    kn_kernel = be.read(m.m.knorm, nb * N // 64)
+    m.free()
+    be.free()
+    for name, a, c in zip(("q16", "k16", "vt16"), fused, kernel):
+        assert np.array_equal(a, c), name
+    assert np.all(kn_fused > 0)
+    assert rel_l2(kn_fused, kn_kernel) <= 1e-6

@@ -26,6 +26,8 @@
  */
 #include "k_common.h"
 
+#include <type_traits>
+
 #define NT_KS 64 /* K per stage */
 
 /* XCDs (L2 domains) of an MI355X. */
@@ -36,19 +38,18 @@ __device__ __forceinline__ int nt_swz(int row, int chunk)
     return 8 * (chunk ^ ((row >> 1) & 7));
 }
 
-/* Asynchronous 16-byte global -> LDS copy: lane i of the wave writes
- * lds_base + 16 i (lds_base wave-uniform, via M0). Inline assembly so the
- * compiler does not wait for it before unrelated LDS reads; the kernel
- * waits itself (s_waitcnt vmcnt(0)) before the barrier that publishes the
- * slot. */
-__device__ __forceinline__ void nt_g2lds16(const void *g, void *lds_base)
+/* Asynchronous 16-byte global -> LDS copy (global_load_lds_dwordx4, saddr
+ * form): lane i of the wave reads base + voff_i and writes lds + 16 i
+ * (base and lds wave-uniform, lds via M0). Inline assembly so the compiler
+ * does not wait for it before unrelated LDS reads; the kernel waits
+ * itself (s_waitcnt vmcnt(0)) before the barrier that publishes the slot.
+ */
+__device__ __forceinline__ void nt_g2lds16_s(const void *base, unsigned voff, unsigned lds)
 {
-    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds_base);
-
     asm volatile("s_mov_b32 m0, %0\n\t"
-                 "global_load_lds_dwordx4 %1, off"
+                 "global_load_lds_dwordx4 %1, %2"
                  :
-                 : "s"(lds), "v"(g)
+                 : "s"(lds), "v"(voff), "s"(base)
                  : "memory", "m0");
 }
 
@@ -160,15 +161,7 @@ __device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0
     }
 }
 
-/* Wait until at most N of this wave's vector-memory operations are
- * outstanding (they retire in issue order). */
-template <int N>
-__device__ __forceinline__ void nt_vm_wait()
-{
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-template <int BM, int BN, int WM, int WN, int NSLOT>
+template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt(gemm_desc d)
 {
@@ -179,14 +172,12 @@ k_gemm_nt(gemm_desc d)
     constexpr int NA = WM / 32;             /* 32-row blocks per wave */
     constexpr int NB = WN / 32;             /* 32-column blocks per wave */
     constexpr int ROWS = BM + BN;           /* LDS rows per stage */
+    constexpr int SLOT_BYTES = ROWS * NT_KS * 2;
     constexpr int LPW = ROWS / (8 * NW);    /* copies per wave per stage */
-    constexpr int LDS_BYTES = NSLOT * ROWS * NT_KS * 2 > EPI_BYTES
-                                  ? NSLOT * ROWS * NT_KS * 2
-                                  : EPI_BYTES;
-    /* NSLOT operand slots during the K loop, the output tile in the
+    constexpr int LDS_BYTES = 2 * SLOT_BYTES > EPI_BYTES ? 2 * SLOT_BYTES : EPI_BYTES;
+    /* Two operand slots during the K loop, the output tile in the
      * epilogue (which may need a little more). */
     __shared__ __attribute__((aligned(16))) uint16_t S_raw[LDS_BYTES / 2];
-    uint16_t(*S)[ROWS][NT_KS] = (uint16_t(*)[ROWS][NT_KS])S_raw;
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
     const int wm = w / (BN / WN), wn = w % (BN / WN);
@@ -200,11 +191,14 @@ k_gemm_nt(gemm_desc d)
     if (tile >= total)
         return;
     const int m0 = (int)(tile / tiles_n) * BM, n0 = (int)(tile % tiles_n) * BN;
-    const uint16_t *A = (const uint16_t *)d.A + d.aoff;
-    const uint16_t *B = (const uint16_t *)d.B + d.boff;
+    /* The tile's first A and B rows: wave-uniform bases (SGPRs) that the
+     * K loop advances by 128 bytes per stage. */
+    const char *Ab = (const char *)((const uint16_t *)d.A + d.aoff + (long)m0 * d.lda);
+    const char *Bb = (const char *)((const uint16_t *)d.B + d.boff + (long)n0 * d.ldb);
     const int nk = d.K / NT_KS;
+    const int wu = __builtin_amdgcn_readfirstlane(w);
     f32x16 acc[NA][NB];
-    long goff[LPW];
+    unsigned goff[LPW];
 
 #pragma unroll
     for (int i = 0; i < NA; i++)
@@ -215,64 +209,58 @@ k_gemm_nt(gemm_desc d)
     /* Copy j of wave w fills stage rows 8 (w LPW + j) .. +7; lane i lands
      * on row + i / 8, physical chunk i % 8 and so fetches logical chunk
      * (i % 8) ^ ((row >> 1) & 7). Rows past M or N read the last row
-     * (their products are never stored). */
+     * (their products are never stored). Byte offsets from the tile's
+     * first row of A or B. */
     for (int j = 0; j < LPW; j++) {
         const int row = 8 * (w * LPW + j) + (l >> 3);
         const int chunk = (l & 7) ^ ((row >> 1) & 7);
 
-        if (row < BM) {
-            const int gm = min(m0 + row, d.M - 1);
-
-            goff[j] = (long)gm * d.lda + 8 * chunk;
-        }
-        else {
-            const int gn = min(n0 + row - BM, d.N - 1);
-
-            goff[j] = (long)gn * d.ldb + 8 * chunk;
-        }
+        if (row < BM)
+            goff[j] = 2u * ((unsigned)(min(m0 + row, d.M - 1) - m0) * d.lda + 8 * chunk);
+        else
+            goff[j] = 2u * ((unsigned)(min(n0 + row - BM, d.N - 1) - n0) * d.ldb + 8 * chunk);
     }
+    const unsigned lds0 = (unsigned)(uintptr_t)S_raw + 1024u * LPW * wu;
     auto load_stage = [&](int ks, int slot) {
         for (int j = 0; j < LPW; j++) {
-            const int row0 = 8 * (w * LPW + j);
-            const uint16_t *base = row0 < BM ? A : B;
+            /* Whether copy j is of A or of B is the same for the wave. */
+            const bool isa = 8 * (wu * LPW + j) < BM;
 
-            nt_g2lds16(base + goff[j] + (long)ks * NT_KS, &S[slot][row0][0]);
+            nt_g2lds16_s((isa ? Ab : Bb) + 128L * ks, goff[j],
+                         lds0 + (unsigned)SLOT_BYTES * slot + 1024u * j);
         }
     };
+    /* Byte offsets of this lane's MFMA operand fragments in a slot, per
+     * 16-wide K step s: A rows wm WM + 32 i + l32 and B rows BM + wn WN +
+     * 32 j + l32 (i, j add 4096 B each); the swizzle depends only on row
+     * bits 1..3, which the 32-row blocks leave alone. */
+    unsigned aro[4], bro[4];
+    for (int s4 = 0; s4 < 4; s4++) {
+        const int ra = wm * WM + l32, rb = BM + wn * WN + l32;
 
-    /* NSLOT - 1 stages in flight ahead of the one being multiplied. */
-    for (int ks = 0; ks < NSLOT - 1 && ks < nk; ks++)
-        load_stage(ks, ks);
-    for (int ks = 0; ks < nk; ks++) {
-        const int slot = ks % NSLOT, ahead = min(NSLOT - 2, nk - 1 - ks);
+        aro[s4] = 2u * (ra * NT_KS + nt_swz(ra, 2 * s4 + h));
+        bro[s4] = 2u * (rb * NT_KS + nt_swz(rb, 2 * s4 + h));
+    }
+    const char *Sb = (const char *)S_raw;
+    /* One K stage from slot `slot` (a constant: the loop is unrolled by
+     * two, so every fragment address is a register plus an immediate). */
+    auto stage = [&](int ks, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
 
-        /* Stage ks has landed once no more than the later stages' copies
-         * are outstanding. */
-        if (ahead >= 2)
-            nt_vm_wait<2 * LPW>();
-        else if (ahead == 1)
-            nt_vm_wait<LPW>();
-        else
-            nt_vm_wait<0>();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (ks + NSLOT - 1 < nk)
-            load_stage(ks + NSLOT - 1, (ks + NSLOT - 1) % NSLOT);
+        if (ks + 1 < nk)
+            load_stage(ks + 1, slot ^ 1);
 #pragma unroll
-        for (int s = 0; s < NT_KS / 16; s++) {
+        for (int s4 = 0; s4 < NT_KS / 16; s4++) {
             bf16x8 a[NA], b[NB];
 
 #pragma unroll
-            for (int i = 0; i < NA; i++) {
-                const int row = wm * WM + 32 * i + l32;
-
-                a[i] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
-            }
+            for (int i = 0; i < NA; i++)
+                a[i] = *(const bf16x8 *)(Sb + SLOT_BYTES * slot + 4096 * i + aro[s4]);
 #pragma unroll
-            for (int j = 0; j < NB; j++) {
-                const int row = BM + wn * WN + 32 * j + l32;
-
-                b[j] = *(const bf16x8 *)&S[slot][row][nt_swz(row, 2 * s + h)];
-            }
+            for (int j = 0; j < NB; j++)
+                b[j] = *(const bf16x8 *)(Sb + SLOT_BYTES * slot + 4096 * j + bro[s4]);
 #pragma unroll
             for (int i = 0; i < NA; i++)
 #pragma unroll
@@ -280,7 +268,15 @@ k_gemm_nt(gemm_desc d)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         a[i], b[j], acc[i][j], 0, 0, 0);
         }
+    };
+
+    load_stage(0, 0);
+    for (int ks = 0; ks + 1 < nk; ks += 2) {
+        stage(ks, std::integral_constant<int, 0>());
+        stage(ks + 1, std::integral_constant<int, 1>());
     }
+    if (nk & 1)
+        stage(nk - 1, std::integral_constant<int, 0>());
 
     /* Epilogue (store_one, sam3_kernels.cl:306-319), through LDS: in
      * chunks of 64 rows, the waves owning the rows write alpha acc + bias
@@ -451,10 +447,10 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
         if (grid > 0x7fffffffL)
             return hipErrorInvalidConfiguration;
         if (bm == 256)
-            hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64, 2>),
+            hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64>),
                                dim3((unsigned)grid), dim3(512), 0, s, *d);
         else
-            hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64, 2>),
+            hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64>),
                                dim3((unsigned)grid), dim3(256), 0, s, *d);
     }
     return hipGetLastError();

@@ -156,7 +156,7 @@ def backbone_flops(grid=72, E=1024, mlp=4096, ps=14, depth=32, ws=24,
     return f
 
 
-def backbone(hip, steps, warmup):
+def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
     """Image encoder trunk, end to end (sam_encode_trunk): 1008 x 1008 x 3
     image ~ U(0, 1) normalised (x - 0.5) / 0.5, patch 14 -> 72 x 72 tokens
     of width 1024, 32 blocks (global attention at blocks 7, 15, 23, 31,
@@ -177,7 +177,7 @@ def backbone(hip, steps, warmup):
         b = 1.0 / math.sqrt(fan)
         return (g.random(n, dtype=np.float32) * (2 * b) - b)
 
-    bes = {p: hip.Backend(precision=p) for p in ("bf16", "fp32")}
+    bes = {p: hip.Backend(precision=p) for p in precisions}
     blocks = {p: [] for p in bes}
     ones, zeros = np.ones(E, np.float32), np.zeros(E, np.float32)
     for i in range(depth):
@@ -327,6 +327,8 @@ def main():
                     help="only the mask-decoder cross-attention (profiling)")
     ap.add_argument("--backbone-only", action="store_true",
                     help="only the image encoder trunk (profiling)")
+    ap.add_argument("--precision", choices=("bf16", "fp32"),
+                    help="with --backbone-only: that path alone")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; the attention path "
@@ -336,7 +338,9 @@ def main():
 
     hip = load_hip()
     if args.backbone_only:
-        print(json.dumps({"backbone": backbone(hip, args.steps, args.warmup)}))
+        prec = (args.precision,) if args.precision else ("bf16", "fp32")
+        print(json.dumps({"backbone": backbone(hip, args.steps, args.warmup,
+                                               prec)}))
         return
     if args.decoder_only:
         be32 = hip.Backend(precision="fp32")

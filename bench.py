@@ -213,6 +213,11 @@ def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
         m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(ones), be.upload(zeros)
         m.m.rope_win = be.upload(rope_table(24))
         m.m.rope_glob = be.upload(rope_table(grid))
+        ms_eager = timed(be, lambda: hip.sam_encode_trunk(m, img), steps,
+                         warmup)
+        # The same trunk replayed from a HIP graph (one launch per image
+        # after the image upload).
+        hip.sam_trunk_graph(m)
         ms = timed(be, lambda: hip.sam_encode_trunk(m, img), steps, warmup)
         # One profiled pass (per-operator events, the reference's
         # I_SAM3_OPENCL_PROFILE table) for the attention share.
@@ -225,7 +230,9 @@ def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
         tot = sum(r[1] for r in tab)
         att = sum(r[1] for r in tab if r[0] in ("attn_bf16", "qkv_pack",
                                                 "attn_f32"))
+        hip.sam_trunk_graph(m, False)
         out[p] = {"ms_per_img": round(ms, 3),
+                  "ms_per_img_kernel_by_kernel": round(ms_eager, 3),
                   "TFLOP/s": round(backbone_flops() / ms / 1e9, 1),
                   "attention_share": round(att / tot, 4),
                   "profile_ms": {r[0]: round(r[1], 3) for r in
@@ -392,7 +399,7 @@ def main():
     w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), sub_warm)
 
     dec = decoder(hip, be32, sub_steps, sub_warm)
-    bb = backbone(hip, 3, 1)
+    bb = backbone(hip, 5, 2)
 
     qkv_flops = 2.0 * 5184 * 1024 * 3072
     result = {

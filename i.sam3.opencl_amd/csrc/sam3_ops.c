@@ -15,6 +15,7 @@
 #include "hipb_internal.h"
 #include "sam3_launch.h"
 
+#include <hip/hip_runtime_api.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -386,6 +387,10 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
 
 /* Grow a model-owned staging buffer of element type dt to count
  * elements. */
+/* Bumped by every work-buffer (re)allocation: a captured trunk graph
+ * holds buffer addresses and is valid only while this has not moved. */
+static unsigned long work_gen;
+
 static int ensure_typed(struct hipb_backend *b, hipb_mem *buf, size_t count,
                         int dt, const char *what)
 {
@@ -396,6 +401,7 @@ static int ensure_typed(struct hipb_backend *b, hipb_mem *buf, size_t count,
         hipb_release(buf);
     }
     *buf = hipb_alloc_typed(b, count, dt, what);
+    work_gen++;
     return *buf != NULL;
 }
 
@@ -863,30 +869,35 @@ void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused)
     }
 }
 
-void sam_encode_trunk(struct sam_model *m, const float *img)
+/* Trunk preconditions and the image buffer; 1 when the trunk can run. */
+static int trunk_ready(struct sam_model *m, const char *who)
+{
+    const int G = m->grid, ps = m->patch, E = m->embed, K = 3 * ps * ps;
+    const long T = (long)G * G, side = (long)G * ps;
+
+    if (ps < 1 || !m->pe_w || !m->pos || !m->lnpw || !m->lnpb) {
+        hipb_fatal("%s: no patch size or trunk weights", who);
+        return 0;
+    }
+    if (!m->mlpbuf || hipb_count(m->mlpbuf) < (size_t)T * K) {
+        hipb_fatal("%s: work buffers hold fewer than %ld patch columns", who,
+                   T * K);
+        return 0;
+    }
+    return buf_ok(who, "pe_w", m->pe_w, (size_t)E * K, -1) &&
+           buf_ok(who, "pos", m->pos, (size_t)T * E, HIPB_F32) &&
+           ensure_typed(m->hip, &m->img, (size_t)3 * side * side, HIPB_F32,
+                        "image");
+}
+
+/* Everything of the trunk after the image upload. */
+static void trunk_kernels(struct sam_model *m)
 {
     struct hipb_backend *b = m->hip;
     const int G = m->grid, ps = m->patch, E = m->embed, K = 3 * ps * ps;
     const long T = (long)G * G, side = (long)G * ps;
     int i, err;
 
-    if (ps < 1 || !img || !m->pe_w || !m->pos || !m->lnpw || !m->lnpb) {
-        hipb_fatal("sam_encode_trunk: no image, patch size or trunk weights");
-        return;
-    }
-    if (!m->mlpbuf || hipb_count(m->mlpbuf) < (size_t)T * K) {
-        hipb_fatal("sam_encode_trunk: work buffers hold fewer than %ld patch "
-                   "columns",
-                   T * K);
-        return;
-    }
-    if (!buf_ok("sam_encode_trunk", "pe_w", m->pe_w, (size_t)E * K, -1) ||
-        !buf_ok("sam_encode_trunk", "pos", m->pos, (size_t)T * E, HIPB_F32) ||
-        !ensure_typed(b, &m->img, (size_t)3 * side * side, HIPB_F32, "image"))
-        return;
-    hipb_write(b, m->img, 0, img, (size_t)3 * side * side * sizeof(float));
-    if (hipb_failed())
-        return;
     /* Patch embedding (no bias), tiled position embedding, ln_pre
      * (sam3_model.c:1119-1130). */
     hipb_run_begin(b);
@@ -901,6 +912,96 @@ void sam_encode_trunk(struct sam_model *m, const float *img)
     layernorm(m, T, E, m->x, m->x, m->lnpw, m->lnpb, ENC_EPS, ACT_NONE);
     for (i = 0; i < m->depth && !hipb_failed(); i++)
         vit_block(m, &m->blocks[i], 0);
+}
+
+static void trunk_graph_drop(struct sam_model *m)
+{
+    if (m->trunk_exec)
+        hipGraphExecDestroy((hipGraphExec_t)m->trunk_exec);
+    if (m->trunk_graph)
+        hipGraphDestroy((hipGraph_t)m->trunk_graph);
+    m->trunk_exec = NULL;
+    m->trunk_graph = NULL;
+}
+
+void sam_encode_trunk(struct sam_model *m, const float *img)
+{
+    struct hipb_backend *b = m->hip;
+    const long side = (long)m->grid * m->patch;
+    int err;
+
+    if (!img) {
+        hipb_fatal("sam_encode_trunk: no image");
+        return;
+    }
+    if (!trunk_ready(m, "sam_encode_trunk"))
+        return;
+    hipb_write(b, m->img, 0, img, (size_t)3 * side * side * sizeof(float));
+    if (hipb_failed())
+        return;
+    if (m->trunk_exec && !b->profile) {
+        if (m->trunk_gen == work_gen) {
+            err = hipGraphLaunch((hipGraphExec_t)m->trunk_exec,
+                                 (hipStream_t)b->stream);
+            hipb_run_end(b, err, "trunk_graph", 0.0);
+            return;
+        }
+        trunk_graph_drop(m); /* a work buffer moved since the capture */
+    }
+    trunk_kernels(m);
+}
+
+void sam_trunk_graph(struct sam_model *m, int enable)
+{
+    struct hipb_backend *b = m->hip;
+    hipGraph_t g = NULL;
+    hipGraphExec_t x = NULL;
+    unsigned long gen;
+    int err, err2;
+
+    if (b)
+        hipb_finish(b);
+    trunk_graph_drop(m);
+    if (!enable)
+        return;
+    if (b->profile) {
+        hipb_fatal("sam_trunk_graph: profiling runs the kernels one by one");
+        return;
+    }
+    if (!trunk_ready(m, "sam_trunk_graph"))
+        return;
+    trunk_kernels(m); /* allocates whatever is still missing */
+    hipb_finish(b);
+    if (hipb_failed())
+        return;
+    gen = work_gen;
+    err = hipStreamBeginCapture((hipStream_t)b->stream,
+                                hipStreamCaptureModeRelaxed);
+    if (err != hipSuccess) {
+        hipb_fatal("sam_trunk_graph: hipStreamBeginCapture: %s (%d)",
+                   hipb_errstr(err), err);
+        return;
+    }
+    trunk_kernels(m);
+    err = hipStreamEndCapture((hipStream_t)b->stream, &g);
+    if (hipb_failed() || err != hipSuccess || !g || work_gen != gen) {
+        if (g)
+            hipGraphDestroy(g);
+        if (!hipb_failed())
+            hipb_fatal("sam_trunk_graph: capture failed: %s (%d)",
+                       hipb_errstr(err), err);
+        return;
+    }
+    err2 = hipGraphInstantiate(&x, g, NULL, NULL, 0);
+    if (err2 != hipSuccess) {
+        hipGraphDestroy(g);
+        hipb_fatal("sam_trunk_graph: hipGraphInstantiate: %s (%d)",
+                   hipb_errstr(err2), err2);
+        return;
+    }
+    m->trunk_graph = g;
+    m->trunk_exec = x;
+    m->trunk_gen = gen;
 }
 
 /* ------------------------------------------------------------ setup */
@@ -965,6 +1066,7 @@ void sam_path_free(struct sam_model *m)
 {
     if (m->hip)
         hipb_finish(m->hip);
+    trunk_graph_drop(m);
     hipb_release(&m->x);
     hipb_release(&m->xn);
     hipb_release(&m->xw);

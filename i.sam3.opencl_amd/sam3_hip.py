@@ -34,6 +34,7 @@ EXPORTS = [
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
     "window_partition", "window_unpartition_add", "mha", "attn_fused",
     "attn_packed", "vit_attention", "vit_block", "sam_encode_trunk",
+    "sam_trunk_graph",
 ]
 
 
@@ -84,7 +85,9 @@ class SamModel(ctypes.Structure):
                             "q16", "k16", "vt16", "knorm")] + \
         [("patch", ctypes.c_int)] + \
         [(n, Mem) for n in ("pe_w", "pos", "lnpw", "lnpb", "img", "tmp",
-                            "mlpbuf", "mlp16")]
+                            "mlpbuf", "mlp16")] + \
+        [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
+         ("trunk_gen", ctypes.c_ulong)]
 
 
 _lib = None
@@ -162,6 +165,7 @@ def lib():
     L.vit_attention.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
     L.vit_block.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
     L.sam_encode_trunk.argtypes = [MP, ctypes.c_void_p]
+    L.sam_trunk_graph.argtypes = [MP, c_int]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
     return L
@@ -393,6 +397,12 @@ def sam_encode_trunk(m, img):
     """img: float32 [3, side, side] host array."""
     img = np.ascontiguousarray(img, np.float32)
     _call(_lib.sam_encode_trunk, m.ptr, img.ctypes.data)
+
+
+def sam_trunk_graph(m, enable=True):
+    """Capture the trunk's kernels into a HIP graph that later
+    sam_encode_trunk calls replay (enable=False drops it)."""
+    _call(_lib.sam_trunk_graph, m.ptr, int(bool(enable)))
 
 
 def prof_table():

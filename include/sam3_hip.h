@@ -199,6 +199,10 @@ struct sam_model {
      * [3][grid patch]^2, projection output [rows][E], MLP hidden /
      * patch columns; mlp16 the bf16 MLP hidden of precision=bf16. */
     hipb_mem img, tmp, mlpbuf, mlp16;
+    /* HIP graph of the trunk's kernels (sam_trunk_graph): hipGraph_t,
+     * hipGraphExec_t, and the work-buffer generation it was captured at. */
+    void *trunk_graph, *trunk_exec;
+    unsigned long trunk_gen;
 };
 
 /* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =
@@ -301,6 +305,17 @@ void vit_block(struct sam_model *m, const struct vit_block *blk, int unfused);
  * embedding + ln_pre give m->x, then the m->depth blocks run in order.
  * The result stays in m->x; the caller synchronises (hipb_finish). */
 void sam_encode_trunk(struct sam_model *m, const float *img);
+
+/* HIP-graph replay of the trunk. With enable != 0: run the trunk's
+ * kernels once (so that every work buffer exists), capture them on the
+ * backend's stream, and let later sam_encode_trunk calls replay the graph
+ * after the image upload (one launch instead of ~200). enable = 0 drops
+ * the graph. Weights, rope tables and work buffers are captured by
+ * address: re-enable after changing weights; a work-buffer reallocation by
+ * any later call drops the graph (later calls run the kernels one by
+ * one). Profiling (profile=1) always runs the kernels one by one. No
+ * counterpart in the reference (whose OpenCL queue has no graphs). */
+void sam_trunk_graph(struct sam_model *m, int enable);
 
 #ifdef __cplusplus
 }

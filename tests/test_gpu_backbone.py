@@ -118,3 +118,59 @@ def test_trunk_prologue_full_size(hip, be, orc):
     got, want = trunk(hip, be, orc, 72, 14, 1024, 16, 4096, [], 91)
     assert report("trunk prologue full %s" % be.precision, got,
                   want) <= TOL[be.precision]
+
+
+def test_trunk_graph_replay(hip, be, orc):
+    """HIP-graph replay of the trunk (sam_trunk_graph): every replay, with
+    alternating images and eager work plus synchronisations between
+    replays, equals the kernel-by-kernel run bit for bit; a later
+    work-buffer reallocation drops the graph and the trunk still computes
+    the same result; dropping the graph returns to the eager path."""
+    grid, ps, E, heads, mlp, windows = 16, 4, 128, 2, 256, [8, 0, 8]
+    img1, pe_w, pos, lnpw, lnpb, blocks = bc.trunk_case(95, grid, ps, E, mlp,
+                                                        windows)
+    img2 = bc.trunk_case(96, grid, ps, E, mlp, windows)[0]
+    blks = [upload_block(hip, be, w) for w in blocks]
+    m = hip.Model(be, grid=grid, embed=E, heads=heads, blocks=blks, mlp=mlp)
+    m.m.patch = ps
+    m.m.pe_w = be.upload_weight(pe_w)
+    m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(lnpw), be.upload(lnpb)
+    m.m.rope_win = be.upload(orc.rope_table(8))
+    m.m.rope_glob = be.upload(orc.rope_table(grid))
+    print("trunk graph grid=%d %s" % (grid, be.precision), flush=True)
+
+    def run(img):
+        hip.sam_encode_trunk(m, img)
+        be.finish()
+        return be.read(m.m.x, grid * grid * E)
+
+    eager = [run(img1), run(img2)]
+    assert not np.array_equal(eager[0], eager[1])
+    hip.sam_trunk_graph(m)
+    assert m.m.trunk_exec
+    other = be.upload(np.ones(4096, np.float32))
+    for rep in range(4):
+        got = run(img1 if rep % 2 == 0 else img2)
+        assert np.array_equal(got, eager[rep % 2]), rep
+        hip.add_bcast(m, other, other, other, 4096, 4096)
+        be.finish()
+    assert m.m.trunk_exec
+    # Larger packed attention operands (bf16 path) reallocate work buffers.
+    N = 1000
+    qkv = be.upload(np.random.default_rng(1).standard_normal((N, 3 * E),
+                                                             np.float32))
+    out = be.alloc(N * E * 4)
+    hip.attn_fused(m, N, heads, heads, hip.bmat(qkv, 0, 3 * E, 0, 64),
+                   hip.bmat(qkv, E, 3 * E, 0, 64),
+                   hip.bmat(qkv, 2 * E, 3 * E, 0, 64),
+                   hip.bmat(out, 0, E, 0, 64), None, 1, 0.125)
+    assert np.array_equal(run(img1), eager[0])
+    if be.precision == "bf16":
+        assert not m.m.trunk_exec
+    hip.sam_trunk_graph(m, False)
+    assert not m.m.trunk_exec
+    assert np.array_equal(run(img2), eager[1])
+    be.release(qkv)
+    be.release(out)
+    be.release(other)
+    m.free()

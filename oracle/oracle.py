@@ -44,6 +44,10 @@ def lib():
         L.or_gemm.argtypes = [_i] + gemm_args
         L.or_gemm_dispatch.argtypes = [_i] + gemm_args
         L.or_softmax_rows.argtypes = [_p, _l, _i]
+        L.or_softmax_ext.argtypes = [_p, _l, _i, _i, _i, _i, _p, _p, _i, _i]
+        L.or_attend.argtypes = [_i, _i, _i, _i, _i, _p, _i, _p, _i, _p, _i, _p,
+                                _i, _i, _p, _p, _i, _l]
+        L.or_attend.restype = _i
         L.or_layernorm.argtypes = [_p, _p, _l, _i, _p, _p, _f, _i]
         L.or_rope_apply.argtypes = [_p, _l, _i, _i, _i, _p]
         L.or_window_partition.argtypes = [_p, _p, _i, _i, _i, _i, _i]
@@ -124,6 +128,37 @@ def softmax_rows(S):
     L = S.shape[-1]
     lib().or_softmax_rows(_ptr(S), S.size // L, L)
     return S
+
+
+def softmax_ext(S, Nq, h0=0, causal=False, dy=None, dx=None, W=0, nh=1):
+    """softmax_ext over the rows of S [rows, L] (row = head * Nq + query,
+    heads from h0); dy [Nq, L / W, nh] and dx [Nq, W, nh] the box bias."""
+    S = _f32(S).copy()
+    L = S.shape[-1]
+    dy = None if dy is None else _f32(dy)
+    dx = None if dx is None else _f32(dx)
+    lib().or_softmax_ext(_ptr(S), S.size // L, L, Nq, h0, int(bool(causal)),
+                         _ptr(dy), _ptr(dx), W, nh)
+    return S
+
+
+def attend(Q, K, V, heads, hd, causal=False, dy=None, dx=None, W=0,
+           score_cap=(512 << 20) // 4, cpu=False, O=None):
+    """attend() of sam3_text.c:305-343 on row-major Q [Nq, ldq], K / V
+    [Nk, ld]; returns O [Nq, heads * hd] (or updates the given O)."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    Nq, Nk = Q.shape[0], K.shape[0]
+    if O is None:
+        O = np.zeros((Nq, heads * hd), np.float32)
+    dy = None if dy is None else _f32(dy)
+    dx = None if dx is None else _f32(dx)
+    hc = lib().or_attend(int(cpu), Nq, Nk, heads, hd, _ptr(Q), Q.shape[1],
+                         _ptr(K), K.shape[1], _ptr(V), V.shape[1], _ptr(O),
+                         O.shape[1], int(bool(causal)), _ptr(dy), _ptr(dx), W,
+                         score_cap)
+    if hc < 1:
+        raise ValueError("score buffer cannot hold one head")
+    return O
 
 
 def layernorm(X, g, b, eps=1e-5, act=ACT_NONE):

@@ -12,7 +12,7 @@
  * sam3_model.c:314-330, softmax_rows() sam3_model.c:332-341,
  * window_partition() / window_unpartition_add() sam3_model.c:360-392,
  * mha() sam3_model.c:413-451, rope_apply() sam3_model.c:965-978,
- * run1d() sam3_model.c:209-214.
+ * run1d() sam3_model.c:209-214, softmax_ext in attend() sam3_text.c:320-335.
  */
 #define CL_TARGET_OPENCL_VERSION 120
 #define CL_USE_DEPRECATED_OPENCL_1_2_APIS
@@ -255,6 +255,51 @@ int ref_softmax_rows(float *S, long rows, int L)
                                   NULL, NULL),
               "read S");
     clReleaseMemObject(d);
+    clReleaseKernel(k);
+    return rc;
+}
+
+/* softmax_ext as attend() launches it (sam3_text.c:320-335): one
+ * work-group of 256 (L >= 256) or 64 items per row; dy / dx may be NULL
+ * (a NULL cl_mem argument, as the reference passes for no bias). */
+int ref_softmax_ext(float *S, long rows, int L, int Nq, int h0, int causal,
+                    const float *dy, long ndy, const float *dx, long ndx, int W,
+                    int nh)
+{
+    cl_int err, cL = L, cNq = Nq, ch0 = h0, cc = causal, cW = W, cnh = nh;
+    cl_mem d, ddy = NULL, ddx = NULL;
+    cl_kernel k = clCreateKernel(prog, "softmax_ext", &err);
+    size_t ls = L >= 256 ? 256 : 64, gs = rows * ls;
+    int rc;
+
+    CHECK(err, "clCreateKernel");
+    d = buf_in(S, (size_t)rows * L * 4, &err);
+    CHECK(err, "S");
+    if (dy) {
+        ddy = buf_in(dy, (size_t)ndy * 4, &err);
+        CHECK(err, "dy");
+        ddx = buf_in(dx, (size_t)ndx * 4, &err);
+        CHECK(err, "dx");
+    }
+    ARG(k, 0, d);
+    ARG(k, 1, cL);
+    ARG(k, 2, cNq);
+    ARG(k, 3, ch0);
+    ARG(k, 4, cc);
+    ARG(k, 5, ddy);
+    ARG(k, 6, ddx);
+    ARG(k, 7, cW);
+    ARG(k, 8, cnh);
+    rc = launch(k, 1, &gs, &ls, "softmax_ext");
+    if (rc == 0)
+        CHECK(clEnqueueReadBuffer(q, d, CL_TRUE, 0, (size_t)rows * L * 4, S, 0,
+                                  NULL, NULL),
+              "read S");
+    clReleaseMemObject(d);
+    if (ddy) {
+        clReleaseMemObject(ddy);
+        clReleaseMemObject(ddx);
+    }
     clReleaseKernel(k);
     return rc;
 }

@@ -36,6 +36,7 @@ def lib():
         L.ref_gemm.argtypes = [i, i, i, i, p, l, l, i, l, l, p, l, l, i, l, l,
                                i, p, l, l, i, l, l, i, i, p, i, l, f, i]
         L.ref_softmax_rows.argtypes = [p, l, i]
+        L.ref_softmax_ext.argtypes = [p, l, i, i, i, i, p, l, p, l, i, i]
         L.ref_layernorm.argtypes = [p, p, l, i, p, p, f, i]
         L.ref_rope_apply.argtypes = [p, l, i, i, i, p]
         L.ref_window_partition.argtypes = [p, p, i, i, i, i]
@@ -77,6 +78,20 @@ def softmax_rows(S):
     S = _c(S).copy()
     _ok(lib().ref_softmax_rows(S.ctypes.data, S.size // S.shape[-1],
                                S.shape[-1]))
+    return S
+
+
+def softmax_ext(S, Nq, h0=0, causal=False, dy=None, dx=None, W=0, nh=1):
+    S = _c(S).copy()
+    L = S.shape[-1]
+    dy = None if dy is None else _c(dy)
+    dx = None if dx is None else _c(dx)
+    _ok(lib().ref_softmax_ext(S.ctypes.data, S.size // L, L, Nq, h0,
+                              int(bool(causal)),
+                              None if dy is None else dy.ctypes.data,
+                              0 if dy is None else dy.size,
+                              None if dx is None else dx.ctypes.data,
+                              0 if dx is None else dx.size, W, nh))
     return S
 
 

@@ -14,6 +14,11 @@
  *   or_gemm (both kinds)        exact small-integer products, fp64 matmul,
  *                                batch/stride/alias/epilogue cases
  *   or_softmax_rows             fp64 softmax, shift invariance, row sums
+ *   or_softmax_ext / or_attend  softmax_rows without terms (bit for bit),
+ *                                fp64 masked / biased softmax and SDPA with
+ *                                the bias built by broadcasting, causal
+ *                                row 0 = V[0], per-row bias shifts, head
+ *                                chunking
  *   or_layernorm                fp64 textbook LayerNorm
  *   or_rope_apply               identity table, pair norms, relative
  *                                position property of the rotation
@@ -273,6 +278,92 @@ void or_softmax_rows(float *S, long rows, int L)
         for (j = 0; j < L; j++)
             s[j] *= inv;
     }
+}
+
+/* softmax_ext (sam3_kernels.cl:885-921): softmax_rows' reduction
+ * order with the causal mask or box bias added in the first pass, which
+ * stores the biased scores back (so the exp pass reads them). */
+void or_softmax_ext(float *S, long rows, int L, int Nq, int h0, int causal,
+                    const float *dy, const float *dx, int W, int nh)
+{
+    const int ls = L >= 256 ? 256 : 64, H = W > 0 ? L / W : 0;
+    long r;
+
+#pragma omp parallel for schedule(static)
+    for (r = 0; r < rows; r++) {
+        const int i = (int)(r % Nq), h = h0 + (int)(r / Nq);
+        float *s = S + r * L;
+        float part[256], m, inv;
+        int t, j;
+
+        for (t = 0; t < ls; t++) {
+            float mx = -INFINITY;
+
+            for (j = t; j < L; j += ls) {
+                float v = s[j];
+
+                if (causal && j > i)
+                    v = -INFINITY;
+                else if (dy)
+                    v += dy[((long)i * H + j / W) * nh + h] +
+                         dx[((long)i * W + j % W) * nh + h];
+                s[j] = v;
+                mx = fmaxf(mx, v);
+            }
+            part[t] = mx;
+        }
+        m = tree_max(part, ls);
+        for (t = 0; t < ls; t++) {
+            float sum = 0.0f;
+
+            for (j = t; j < L; j += ls) {
+                const float v = expf(s[j] - m);
+
+                s[j] = v;
+                sum += v;
+            }
+            part[t] = sum;
+        }
+        inv = 1.0f / tree_sum(part, ls);
+        for (j = 0; j < L; j++)
+            s[j] *= inv;
+    }
+}
+
+/* attend() (sam3_text.c:305-343): the head chunking, the two GEMMs of
+ * each chunk (alpha 1 / sqrtf(hd), heads as the batch with stride hd) and
+ * softmax_ext between them. */
+int or_attend(int cpu, int Nq, int Nk, int heads, int hd, const float *Q,
+              int ldq, const float *K, int ldk, const float *V, int ldv,
+              float *O, int ldo, int causal, const float *dy, const float *dx,
+              int W, long score_cap)
+{
+    const long plane = (long)Nq * Nk;
+    const long hcl = score_cap / plane;
+    const int hc = hcl > heads ? heads : (int)hcl;
+    float *scores;
+    int h0;
+
+    if (hc < 1)
+        return -1;
+    scores = malloc((size_t)hc * plane * sizeof(float));
+    if (!scores)
+        return -1;
+    for (h0 = 0; h0 < heads; h0 += hc) {
+        const int hcc = heads - h0 < hc ? heads - h0 : hc;
+
+        or_gemm_dispatch(cpu, Nq, Nk, hd, Q, (long)h0 * hd, ldq, 0, hd, K,
+                         (long)h0 * hd, ldk, 0, hd, 1, scores, 0, Nk, 0, plane,
+                         hcc, hcc, NULL, NULL, 0, 1.0f / sqrtf((float)hd),
+                         OR_ACT_NONE);
+        or_softmax_ext(scores, (long)hcc * Nq, Nk, Nq, h0, causal, dy, dx, W,
+                       heads);
+        or_gemm_dispatch(cpu, Nq, hd, Nk, scores, 0, Nk, 0, plane, V,
+                         (long)h0 * hd, ldv, 0, hd, 0, O, (long)h0 * hd, ldo, 0,
+                         hd, hcc, hcc, NULL, NULL, 0, 1.0f, OR_ACT_NONE);
+    }
+    free(scores);
+    return hc;
 }
 
 /* layernorm (sam3_kernels.cl:489-514), ls = 256 for C >= 1024 else 64

@@ -53,6 +53,27 @@ void or_gemm_dispatch(int cpu, int M, int N, int K, const float *A, long aoff,
  * (sam3_kernels.cl:637-656, host sam3_model.c:332-341). */
 void or_softmax_rows(float *S, long rows, int L);
 
+/* softmax_ext (sam3_kernels.cl:885-921) as attend() launches it
+ * (sam3_text.c:320-335, ls = L >= 256 ? 256 : 64 items per row): in
+ * place over `rows` rows of L scores, row = head * Nq + query with heads
+ * counted from h0. Each score first gets the causal mask (key j > query i
+ * becomes -inf) or else, when dy is given, SAM 3's box relative position
+ * bias dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h] with H = L / W;
+ * then the strided max / exp / sum of softmax_rows. */
+void or_softmax_ext(float *S, long rows, int L, int Nq, int h0, int causal,
+                    const float *dy, const float *dx, int W, int nh);
+
+/* attend() (sam3_text.c:305-343): `heads` heads of width hd at columns
+ * h hd of Q [Nq][ldq], K [Nk][ldk], V [Nk][ldv], O [Nq][ldo]; per chunk of
+ * hc = min(heads, score_cap / (Nq Nk)) heads: scores = Q K^T / sqrt(hd)
+ * (gemm dispatch, cpu as in or_gemm_dispatch), softmax_ext with the mask or
+ * bias (nh = heads), O = P V. Returns hc, or -1 if one head's scores do
+ * not fit (the reference's fatal error). */
+int or_attend(int cpu, int Nq, int Nk, int heads, int hd, const float *Q,
+              int ldq, const float *K, int ldk, const float *V, int ldv,
+              float *O, int ldo, int causal, const float *dy, const float *dx,
+              int W, long score_cap);
+
 /* Row LayerNorm, Y may alias X (sam3_kernels.cl:489-514, host
  * sam3_model.c:314-330). */
 void or_layernorm(const float *X, float *Y, long rows, int C, const float *g,

@@ -3,7 +3,7 @@ kernels: sam3_kernels.cl compiled unchanged for gfx950 (oracle/ref.mk) and
 launched through the ROCm OpenCL runtime the way sam3_model.c launches
 them (oracle/ref_harness.c). Run on a machine with an OpenCL GPU device:
 
-    python tests/golden/gen_golden.py OUTDIR
+    python tests/golden/gen_golden.py OUTDIR [CASE ...]
 
 Each case is one .npz: the reference outputs (full, or sampled rows for
 large cases, with the sample indices), plus the SHA-1 of the inputs. The
@@ -31,10 +31,12 @@ def sha(*arrays):
     return h.hexdigest()
 
 
-def main(out):
+def main(out, names=None):
     os.makedirs(out, exist_ok=True)
     print("reference device:", refk.device(), flush=True)
     for name, make in gc.CASES.items():
+        if names and name not in names:
+            continue
         case = make()
         res = gc.run_reference(name, case, refk)
         rows = case.get("sample_rows")
@@ -50,4 +52,4 @@ def main(out):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1])
+    main(sys.argv[1], sys.argv[2:])

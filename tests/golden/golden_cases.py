@@ -112,6 +112,33 @@ def _vit_case(seed):
             "inputs": [x, n1w, n1b, w, b, rope_table(ws)]}
 
 
+def _softmax_ext_case(Nq, H, W, nh, h0, hc, causal, seed):
+    """softmax_ext rows (row = head * Nq + query, heads from h0) of L = H W
+    scores, the causal mask or the box bias dy [Nq, H, nh], dx [Nq, W, nh]."""
+    g = rng(seed)
+    L = H * W
+    S = (3 * g.standard_normal((hc * Nq, L))).astype(np.float32)
+    inputs = [S]
+    if not causal:
+        inputs += [g.standard_normal((Nq, H, nh)).astype(np.float32),
+                   g.standard_normal((Nq, W, nh)).astype(np.float32)]
+    return {"kind": "softmax_ext", "Nq": Nq, "W": W, "nh": nh, "h0": h0,
+            "causal": causal, "inputs": inputs}
+
+
+def _attend_case(Nq, Nk, heads, hd, mode, seed, W=0):
+    """attend() (sam3_text.c:305-343) on Q [Nq, D], K / V [Nk, D],
+    D = heads hd: mode "box" (bias, Nk = H W), "causal" or "plain"."""
+    g = rng(seed)
+    D = heads * hd
+    inputs = [g.standard_normal((n, D)).astype(np.float32) for n in (Nq, Nk, Nk)]
+    if mode == "box":
+        inputs += [g.standard_normal((Nq, Nk // W, heads)).astype(np.float32),
+                   g.standard_normal((Nq, W, heads)).astype(np.float32)]
+    return {"kind": "attend", "Nq": Nq, "Nk": Nk, "heads": heads, "hd": hd,
+            "mode": mode, "W": W, "inputs": inputs}
+
+
 CASES = {
     "gemm_t": lambda: _gemm_case(GEMM, 1, 1),
     "gemm_n": lambda: _gemm_case(GEMM, 0, 2),
@@ -134,6 +161,12 @@ CASES = {
     "attn_window_gpu": lambda: _attn_case(576, 1024, 16, False, True, 18),
     "attn_global_rope_head": lambda: _attn_case(5184, 64, 1, True, False, 19),
     "vit_window_region": lambda: _vit_case(20),
+    "softmax_ext_causal": lambda: _softmax_ext_case(40, 1, 40, 2, 0, 2, True, 21),
+    "softmax_ext_box": lambda: _softmax_ext_case(7, 10, 12, 4, 1, 2, False, 22),
+    "softmax_ext_box_L5184": lambda: _softmax_ext_case(3, 72, 72, 8, 5, 3, False, 23),
+    "attend_box_hd32": lambda: _attend_case(21, 144, 8, 32, "box", 24, W=12),
+    "attend_causal_hd64": lambda: _attend_case(33, 33, 4, 64, "causal", 25),
+    "attend_self_hd32": lambda: _attend_case(200, 200, 8, 32, "plain", 26),
 }
 
 
@@ -205,7 +238,42 @@ def run_reference(name, case, impl):
                               False)
             out[u * N:(u + 1) * N] = o
         return {"qkv": qkv, "O": out}
+    if k == "softmax_ext":
+        dy, dx = (x[1], x[2]) if len(x) > 1 else (None, None)
+        return {"S": impl.softmax_ext(x[0], case["Nq"], case["h0"],
+                                      case["causal"], dy, dx, case["W"],
+                                      case["nh"])}
+    if k == "attend":
+        return {"O": _attend(impl, case)}
     raise ValueError(k)
+
+
+def _gpu_kernel(M, N, K, lda, ldb):
+    """The GPU dispatcher's kernel (sam3_model.c:240-255): gemm_big when
+    M >= 128, N >= 64 and the rows are 16-byte aligned, else gemm."""
+    big = M >= 128 and N >= 64 and K % 4 == 0 and lda % 4 == 0 and ldb % 4 == 0
+    return GEMM_BIG if big else GEMM
+
+
+def _attend(impl, case):
+    """attend()'s sequence with impl's kernels, all heads in one chunk:
+    Q K^T (alpha 1 / sqrtf(hd)), softmax_ext, P V, each GEMM on the kernel
+    the GPU dispatcher picks."""
+    Q, K, V = case["inputs"][:3]
+    dy, dx = (case["inputs"][3], case["inputs"][4]) if case["mode"] == "box" \
+        else (None, None)
+    Nq, Nk, H, hd = case["Nq"], case["Nk"], case["heads"], case["hd"]
+    D = H * hd
+    alpha = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    S = np.zeros(H * Nq * Nk, np.float32)
+    S = impl.gemm(_gpu_kernel(Nq, Nk, hd, D, D), Nq, Nk, hd, Q, 0, D, 0, hd, K,
+                  0, D, 0, hd, 1, S, 0, Nk, 0, Nq * Nk, H, H, alpha=alpha)
+    P = impl.softmax_ext(S.reshape(H * Nq, Nk), Nq, 0, case["mode"] == "causal",
+                         dy, dx, case["W"], H)
+    O = np.zeros((Nq, D), np.float32)
+    return impl.gemm(_gpu_kernel(Nq, hd, Nk, Nk, D), Nq, hd, Nk, P, 0, Nk, 0,
+                     Nq * Nk, V, 0, D, 0, hd, 0, O, 0, D, 0, hd, H,
+                     H).reshape(Nq, D)
 
 
 class OracleImpl:
@@ -231,6 +299,9 @@ class OracleImpl:
 
     def softmax_rows(self, S):
         return self.o.softmax_rows(S)
+
+    def softmax_ext(self, S, Nq, h0, causal, dy, dx, W, nh):
+        return self.o.softmax_ext(S, Nq, h0, causal, dy, dx, W, nh)
 
     def layernorm(self, X, g, b, eps=1e-5, act=0):
         return self.o.layernorm(X, g, b, eps, act)

@@ -134,3 +134,30 @@ def encode_trunk(img, grid, ps, E, heads, hd, mlp, pe_w, pos, lnpw, lnpb,
         x = vit_block(x, grid, E, heads, hd, mlp, w,
                       rope_win if w["window"] else rope_glob)
     return x
+
+
+def box_bias(dy, dx):
+    """SAM 3's box relative position bias by broadcasting: dy [Nq, H, nh],
+    dx [Nq, W, nh] -> [Nq, H * W, nh], key j = y * W + x gets
+    dy[i, y] + dx[i, x]."""
+    Nq, H, nh = dy.shape
+    W = dx.shape[1]
+    b = dy.astype(np.float64)[:, :, None, :] + dx.astype(np.float64)[:, None, :, :]
+    return b.reshape(Nq, H * W, nh)
+
+
+def attend(Q, K, V, heads, hd, causal=False, bias=None):
+    """softmax(Q_h K_h^T / sqrt(hd) + bias_h (or the causal mask)) V_h per
+    head, heads at columns h hd."""
+    Q, K, V = (a.astype(np.float64) for a in (Q, K, V))
+    Nq, Nk = Q.shape[0], K.shape[0]
+    out = np.zeros((Nq, heads * hd))
+    for h in range(heads):
+        c = slice(h * hd, (h + 1) * hd)
+        s = Q[:, c] @ K[:, c].T / math.sqrt(hd)
+        if causal:
+            s = np.where(np.arange(Nk)[None, :] > np.arange(Nq)[:, None], -np.inf, s)
+        elif bias is not None:
+            s = s + bias[:, :, h]
+        out[:, c] = softmax(s) @ V[:, c]
+    return out

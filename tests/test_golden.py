@@ -53,3 +53,17 @@ def test_oracle_matches_reference_kernels(orc, name):
 def test_every_case_has_vectors():
     have = {f[:-4] for f in os.listdir(VEC) if f.endswith(".npz")}
     assert have == set(gc.CASES)
+
+
+@pytest.mark.parametrize("name", [n for n in gc.CASES if n.startswith("attend_")])
+def test_oracle_attend_matches_reference(orc, name):
+    """or_attend (the composed attend() of the oracle, with its own head
+    chunking and GEMM dispatch) against the reference kernels' sequence."""
+    case, gold = load(name)
+    Q, K, V = case["inputs"][:3]
+    kw = {}
+    if case["mode"] == "box":
+        kw = dict(dy=case["inputs"][3], dx=case["inputs"][4], W=case["W"])
+    O = orc.attend(Q, K, V, case["heads"], case["hd"],
+                   causal=case["mode"] == "causal", **kw)
+    compare(name, {"O": O}, gold, 1e-6)

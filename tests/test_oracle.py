@@ -156,6 +156,108 @@ def test_softmax_rows(orc, L):
     assert ref64.rel_l2(P2, P) < 2e-6
 
 
+# ------------------------------------------------ text-path attention
+
+
+@pytest.mark.parametrize("L", [40, 576])
+def test_softmax_ext_without_terms_is_softmax_rows(orc, L):
+    S = (3 * rng(L + 1).standard_normal((18, L))).astype(np.float32)
+    assert np.array_equal(orc.softmax_ext(S, 6, h0=2), orc.softmax_rows(S))
+
+
+def test_softmax_ext_causal(orc):
+    Nq = L = 50
+    S = (3 * rng(3).standard_normal((2 * Nq, L))).astype(np.float32)
+    P = orc.softmax_ext(S, Nq, causal=True)
+    mask = np.arange(L)[None, :] > np.arange(Nq)[:, None]
+    want = np.concatenate([ref64.softmax(np.where(mask, -np.inf, S[h * Nq:(h + 1) * Nq]))
+                           for h in range(2)])
+    assert ref64.rel_l2(P, want) < 1e-6
+    assert np.all(P.reshape(2, Nq, L)[:, mask] == 0.0)
+    assert np.all(P[::Nq, 0] == 1.0)            # query 0 sees key 0 only
+
+
+def _box_terms(seed, Nq, H, W, nh):
+    g = rng(seed)
+    dy = g.standard_normal((Nq, H, nh)).astype(np.float32)
+    dx = g.standard_normal((Nq, W, nh)).astype(np.float32)
+    return dy, dx
+
+
+@pytest.mark.parametrize("Nq,H,W,nh,h0", [(7, 5, 7, 4, 1), (3, 72, 72, 8, 5)])
+def test_softmax_ext_box_bias(orc, Nq, H, W, nh, h0):
+    """Against softmax of the scores plus the bias built by broadcasting
+    (H != W catches a swapped row / column index); heads from h0 pick
+    their own bias columns."""
+    L, hc = H * W, 2
+    S = (2 * rng(Nq + L).standard_normal((hc * Nq, L))).astype(np.float32)
+    dy, dx = _box_terms(Nq, Nq, H, W, nh)
+    P = orc.softmax_ext(S, Nq, h0=h0, dy=dy, dx=dx, W=W, nh=nh)
+    bias = ref64.box_bias(dy, dx)
+    want = np.concatenate([ref64.softmax(S[k * Nq:(k + 1) * Nq] + bias[:, :, h0 + k])
+                           for k in range(hc)])
+    assert ref64.rel_l2(P, want) < 1e-6
+    if H != W:
+        # Teeth: the bias with the key index read x major (j = x H + y)
+        # is a different function, which the check above would reject.
+        bad = (dx.astype(np.float64)[:, :, None, :] +
+               dy.astype(np.float64)[:, None, :, :]).reshape(Nq, L, nh)
+        wrong = np.concatenate([ref64.softmax(S[k * Nq:(k + 1) * Nq] + bad[:, :, h0 + k])
+                                for k in range(hc)])
+        assert ref64.rel_l2(P, wrong) > 1e-2
+    # A constant added to one query's dy row shifts its scores uniformly.
+    dy2 = dy.copy()
+    dy2[1] += np.float32(3.0)
+    P2 = orc.softmax_ext(S, Nq, h0=h0, dy=dy2, dx=dx, W=W, nh=nh)
+    assert ref64.rel_l2(P2, P) < 2e-6
+
+
+@pytest.mark.parametrize("cpu", [False, True])
+@pytest.mark.parametrize("case", ["bias_hd32", "causal_hd64", "plain_hd32"])
+def test_attend_vs_float64(orc, cpu, case):
+    g = rng(len(case))
+    if case == "bias_hd32":
+        Nq, heads, hd, H, W = 21, 8, 32, 5, 7
+        Nk = H * W
+    elif case == "causal_hd64":
+        Nq, Nk, heads, hd = 33, 33, 4, 64
+    else:
+        Nq, Nk, heads, hd = 60, 60, 8, 32
+    D = heads * hd
+    Q = g.standard_normal((Nq, D + 8)).astype(np.float32)
+    K = g.standard_normal((Nk, D)).astype(np.float32)
+    V = g.standard_normal((Nk, D + 4)).astype(np.float32)
+    kw = {}
+    bias = None
+    if case == "bias_hd32":
+        dy, dx = _box_terms(5, Nq, H, W, heads)
+        kw = dict(dy=dy, dx=dx, W=W)
+        bias = ref64.box_bias(dy, dx)
+    O = orc.attend(Q, K, V, heads, hd, causal=case == "causal_hd64", cpu=cpu, **kw)
+    want = ref64.attend(Q[:, :D], K, V[:, :D], heads, hd,
+                        causal=case == "causal_hd64", bias=bias)
+    assert ref64.rel_l2(O, want) < 1e-5
+
+
+def test_attend_head_chunks_and_causal_first_row(orc):
+    """One head per score chunk gives the same bits as all heads at once
+    (the chunk offset reaches the bias and the operand columns); with the
+    causal mask query 0's output is V's row 0 exactly."""
+    g = rng(9)
+    Nq, heads, hd, H, W = 12, 4, 32, 3, 4
+    Nk, D = H * W, heads * hd
+    Q, K, V = (g.standard_normal((n, D)).astype(np.float32) for n in (Nq, Nk, Nk))
+    dy, dx = _box_terms(10, Nq, H, W, heads)
+    a = orc.attend(Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    b = orc.attend(Q, K, V, heads, hd, dy=dy, dx=dx, W=W, score_cap=Nq * Nk)
+    assert np.array_equal(a, b)
+    Kc, Vc = Q.copy(), g.standard_normal((Nq, D)).astype(np.float32)
+    O = orc.attend(Q, Kc, Vc, heads, hd, causal=True)
+    assert np.array_equal(O[0], Vc[0])
+    with pytest.raises(ValueError):
+        orc.attend(Q, K, V, heads, hd, score_cap=Nq * Nk - 1)
+
+
 @pytest.mark.parametrize("C", [1024, 256, 100])
 def test_layernorm(orc, C):
     g = rng(C)

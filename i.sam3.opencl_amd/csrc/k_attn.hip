@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
     const float2 *cs = (const float2 *)d.rope;
     float q[16], k[16], v[16];
 
-    if (i < d.N) {
+    if (i < d.N && ds < d.hd) {
         const float *qr = (const float *)d.Q + d.qoff + b0 * d.sq0 +
                           b1 * d.sq1 + (long)i * d.ldq + ds;
         const float *kr = (const float *)d.K + d.koff + b0 * d.sk0 +
@@ -625,8 +625,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         const int q0 = qi - l32, c = l & 7;
 
         if (f32out) {
-            /* Two passes of 32 columns (128 B per row). */
-            for (int half = 0; half < 2; half++) {
+            /* Two passes of 32 columns (128 B per row); one for hd 32. */
+            for (int half = 0; half < d.hd / 32; half++) {
                 const f32x16 &o = half ? st.o1 : st.o0;
 
                 for (int g = 0; g < 4; g++) {
@@ -659,7 +659,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 const int row = 8 * j + (l >> 3);
                 const u32x4 v = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
-                if (q0 + row < N)
+                if (q0 + row < N && 8 * c < d.hd)
                     *(u32x4 *)((uint16_t *)d.O + obase + (long)(q0 + row) * d.ldo + 8 * c) = v;
             }
         }
@@ -667,12 +667,15 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     else if (qi < N) {
         const long orow = obase + (long)qi * d.ldo;
 
+        const bool wide = d.hd > 32;
+
         if (f32out) {
             for (int r = 0; r < 16; r++) {
                 const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
                 ((float *)d.O)[orow + dd] = st.o0[r] * inv;
-                ((float *)d.O)[orow + 32 + dd] = st.o1[r] * inv;
+                if (wide)
+                    ((float *)d.O)[orow + 32 + dd] = st.o1[r] * inv;
             }
         }
         else {
@@ -680,7 +683,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
                 ((uint16_t *)d.O)[orow + dd] = f2bf(st.o0[r] * inv);
-                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
+                if (wide)
+                    ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
             }
         }
     }

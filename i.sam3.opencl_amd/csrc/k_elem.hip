@@ -235,6 +235,59 @@ extern "C" int launch_softmax_rows(float *S, long rows, int L, void *stream)
     return hipGetLastError();
 }
 
+/* softmax_ext (sam3_kernels.cl:885-921): row = head * Nq + query (heads
+ * from h0); each score first gets the causal mask (key j > query i:
+ * -inf) or else, with dy, the box relative position bias
+ * dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h] (H = L / W), stored
+ * back; then the softmax of k_softmax_rows. */
+__global__ __launch_bounds__(256) void k_softmax_ext(
+    float *__restrict__ S, int L, int Nq, int h0, int causal,
+    const float *__restrict__ dy, const float *__restrict__ dx, int W, int nh)
+{
+    __shared__ float red[4];
+    const int row = blockIdx.x, i = row % Nq, h = h0 + row / Nq;
+    const int H = W > 0 ? L / W : 0;
+    float *s = S + (long)row * L;
+    const int t = threadIdx.x, w = t >> 6, l = t & 63;
+    float m = -INFINITY, sum = 0.0f, inv;
+    int j;
+
+    for (j = t; j < L; j += 256) {
+        float v = s[j];
+
+        if (causal && j > i)
+            v = -INFINITY;
+        else if (dy)
+            v += dy[((long)i * H + j / W) * nh + h] + dx[((long)i * W + j % W) * nh + h];
+        s[j] = v;
+        m = fmaxf(m, v);
+    }
+    m = wave_max(m);
+    __syncthreads();
+    if (l == 0)
+        red[w] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (j = t; j < L; j += 256) {
+        const float v = expf(s[j] - m);
+
+        s[j] = v;
+        sum += v;
+    }
+    inv = 1.0f / block_sum256(sum, red);
+    for (j = t; j < L; j += 256)
+        s[j] *= inv;
+}
+
+extern "C" int launch_softmax_ext(float *S, long rows, int L, int Nq, int h0,
+                                  int causal, const float *dy, const float *dx,
+                                  int W, int nh, void *stream)
+{
+    hipLaunchKernelGGL(k_softmax_ext, dim3(rows), dim3(256), 0,
+                       (hipStream_t)stream, S, L, Nq, h0, causal, dy, dx, W, nh);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------ RoPE */
 
 /* One thread per (row, q/k, pair): the rotation of rope_apply

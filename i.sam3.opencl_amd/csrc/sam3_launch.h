@@ -81,6 +81,11 @@ int launch_layernorm(const float *X, void *Y, int ydt, const float *g,
                      int H, int ws, int nwx, void *stream);
 
 int launch_softmax_rows(float *S, long rows, int L, void *stream);
+/* softmax_ext: causal mask or box bias, then the row softmax; rows =
+ * heads x Nq, heads from h0 (dy / dx NULL for no bias). */
+int launch_softmax_ext(float *S, long rows, int L, int Nq, int h0, int causal,
+                       const float *dy, const float *dx, int W, int nh,
+                       void *stream);
 int launch_rope_apply(float *qkv, long rows, int E, int hd, int npos,
                       const float *cs, void *stream);
 int launch_window_partition(const float *X, float *out, int H, int W, int C,
@@ -117,6 +122,9 @@ struct attn_desc {
     const float *rope; /* (cos, sin) x 32 per position, or NULL */
     int npos;
     float scale;
+    /* Head width: 64, or 32 on the bf16 path (packed with zero channels
+     * 32..63, so the 64-wide kernel applies; 32 output columns stored). */
+    int hd;
 };
 
 /* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads. */

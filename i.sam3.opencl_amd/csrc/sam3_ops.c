@@ -256,6 +256,34 @@ void softmax_rows(struct sam_model *m, hipb_mem S, long rows, int L)
     hipb_run_end(be, err, "softmax_rows", 0.0);
 }
 
+void softmax_ext(struct sam_model *m, hipb_mem S, long rows, int L, int Nq,
+                 int h0, int causal, hipb_mem dy, hipb_mem dx, int W, int nh)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (rows < 0 || L < 1 || Nq < 1 || h0 < 0 || (dy && !dx) || (dx && !dy) ||
+        (dy && (W < 1 || L % W || nh < 1 || h0 + (rows + Nq - 1) / Nq > nh))) {
+        hipb_fatal("softmax_ext: invalid shape rows=%ld L=%d Nq=%d h0=%d W=%d "
+                   "nh=%d",
+                   rows, L, Nq, h0, W, nh);
+        return;
+    }
+    if (!buf_ok("softmax_ext", "S", S, (size_t)rows * L, HIPB_F32) ||
+        (dy && (!buf_ok("softmax_ext", "dy", dy, (size_t)Nq * (L / W) * nh,
+                        HIPB_F32) ||
+                !buf_ok("softmax_ext", "dx", dx, (size_t)Nq * W * nh,
+                        HIPB_F32))))
+        return;
+    if (rows == 0)
+        return;
+    hipb_run_begin(be);
+    err = launch_softmax_ext(S->ptr, rows, L, Nq, h0, causal != 0,
+                             dy ? dy->ptr : NULL, dx ? dx->ptr : NULL, W, nh,
+                             be->stream);
+    hipb_run_end(be, err, "softmax_ext", 0.0);
+}
+
 void rope_apply(struct sam_model *m, hipb_mem table, long rows, int npos)
 {
     struct hipb_backend *be = m->hip;
@@ -411,38 +439,39 @@ static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
     return ensure_typed(b, buf, count, HIPB_BF16, what);
 }
 
-void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
-                struct opnd K, struct opnd V, struct opnd O, hipb_mem rope,
-                int npos, float scale)
+/* The fused attention of attn_fused at head width hd: 64 on both paths,
+ * 32 on the bf16 path (operands packed with zero channels 32..63). */
+static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
+                          int nb, int nb1, struct opnd Q, struct opnd K,
+                          struct opnd V, struct opnd O, hipb_mem rope,
+                          int npos, float scale)
 {
     struct hipb_backend *b = m->hip;
-    const int hd = 64;
     struct attn_desc d;
     int err;
 
     if (N < 0 || nb < 1 || nb1 < 1 || (rope && npos < 1)) {
-        hipb_fatal("attn_fused: invalid shape N=%d nb=%d nb1=%d npos=%d", N,
-                   nb, nb1, npos);
+        hipb_fatal("%s: invalid shape N=%d nb=%d nb1=%d npos=%d", who, N, nb,
+                   nb1, npos);
         return;
     }
-    if (m->hd != 0 && m->hd != hd) {
-        hipb_fatal("attn_fused: unsupported head width %d", m->hd);
+    if (!(hd == 64 || (hd == 32 && b->bf16 && !rope))) {
+        hipb_fatal("%s: unsupported head width %d", who, hd);
         return;
     }
     if (N == 0)
         return;
-    if (!opnd_ok("attn_fused", "Q", Q, N, hd, nb, nb1) ||
-        !opnd_ok("attn_fused", "K", K, N, hd, nb, nb1) ||
-        !opnd_ok("attn_fused", "V", V, N, hd, nb, nb1) ||
-        !opnd_ok("attn_fused", "O", O, N, hd, nb, nb1))
+    if (!opnd_ok(who, "Q", Q, N, hd, nb, nb1) ||
+        !opnd_ok(who, "K", K, N, hd, nb, nb1) ||
+        !opnd_ok(who, "V", V, N, hd, nb, nb1) ||
+        !opnd_ok(who, "O", O, N, hd, nb, nb1))
         return;
     if (Q.buf->dtype != HIPB_F32 || K.buf->dtype != HIPB_F32 ||
         V.buf->dtype != HIPB_F32 || O.buf->dtype == HIPB_F16) {
-        hipb_fatal("attn_fused: Q, K, V must be float; O float or bf16");
+        hipb_fatal("%s: Q, K, V must be float; O float or bf16", who);
         return;
     }
-    if (rope && !buf_ok("attn_fused", "rope", rope, (size_t)npos * hd,
-                        HIPB_F32))
+    if (rope && !buf_ok(who, "rope", rope, (size_t)npos * hd, HIPB_F32))
         return;
     d.N = N;
     d.nb = nb;
@@ -471,9 +500,10 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
     d.rope = rope ? (const float *)rope->ptr : NULL;
     d.npos = rope ? npos : 1;
     d.scale = scale;
+    d.hd = hd;
     if (b->bf16) {
         const size_t np = ((size_t)N + 63) / 64 * 64;
-        const size_t cnt = (size_t)nb * np * hd;
+        const size_t cnt = (size_t)nb * np * 64;
 
         if (!ensure_bf16(b, &m->q16, cnt, "packed q") ||
             !ensure_bf16(b, &m->k16, cnt, "packed k") ||
@@ -496,6 +526,18 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
     hipb_run_begin(b);
     err = launch_attn_f32(&d, b->stream);
     hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)N * hd * nb);
+}
+
+void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
+                struct opnd K, struct opnd V, struct opnd O, hipb_mem rope,
+                int npos, float scale)
+{
+    if (m->hd != 0 && m->hd != 64) {
+        hipb_fatal("attn_fused: unsupported head width %d", m->hd);
+        return;
+    }
+    attn_fused_hd(m, "attn_fused", 64, N, nb, nb1, Q, K, V, O, rope, npos,
+                  scale);
 }
 
 void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
@@ -525,6 +567,7 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.N = N;
     d.nb = nb;
     d.nb1 = nb1;
+    d.hd = 64;
     d.O = O.buf->ptr;
     d.ooff = O.off;
     d.ldo = O.ld;
@@ -535,6 +578,62 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
                            (const float *)m->knorm->ptr, b->stream);
     hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
+}
+
+void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
+            int ldq, hipb_mem K, int ldk, hipb_mem V, int ldv, hipb_mem O,
+            int ldo, int causal, hipb_mem dy, hipb_mem dx, int W)
+{
+    struct hipb_backend *b = m->hip;
+    const long plane = (long)Nq * Nk;
+    const float scale = 1.0f / sqrtf((float)hd);
+    long hcl;
+    int hc, h0;
+
+    if (Nq < 0 || Nk < 0 || heads < 1 || hd < 1) {
+        hipb_fatal("attend: invalid shape Nq=%d Nk=%d heads=%d hd=%d", Nq, Nk,
+                   heads, hd);
+        return;
+    }
+    if (Nq == 0 || Nk == 0)
+        return;
+    /* Fused: no mask or bias, self-attention shape, and a head width the
+     * fused kernels take (64; 32 on the bf16 path). Heads are the units,
+     * head h at column h hd of every operand. */
+    if (!causal && !dy && Nq == Nk &&
+        (hd == 64 || (hd == 32 && b->bf16))) {
+        attn_fused_hd(m, "attend", hd, Nq, heads, heads, bmat(Q, 0, ldq, 0, hd),
+                      bmat(K, 0, ldk, 0, hd), bmat(V, 0, ldv, 0, hd),
+                      bmat(O, 0, ldo, 0, hd), NULL, 1, scale);
+        return;
+    }
+    /* The reference's sequence (sam3_text.c:305-343): per chunk of heads
+     * whose scores fit the score buffer, Q K^T / sqrt(hd), softmax_ext,
+     * P V. */
+    hcl = m->score_cap / plane;
+    hc = hcl > heads ? heads : (int)hcl;
+    if (hc < 1) {
+        hipb_fatal("attend: device cannot hold %d x %d attention scores", Nq,
+                   Nk);
+        return;
+    }
+    if (!ensure_typed(b, &m->scores, (size_t)hc * plane, HIPB_F32,
+                      "attention scores"))
+        return;
+    for (h0 = 0; h0 < heads && !hipb_failed(); h0 += hc) {
+        const int hcc = heads - h0 < hc ? heads - h0 : hc;
+
+        gemm(m, Nq, Nk, hd, bmat(Q, (long)h0 * hd, ldq, 0, hd),
+             bmat(K, (long)h0 * hd, ldk, 0, hd), 1,
+             bmat(m->scores, 0, Nk, 0, plane), hcc, hcc, NULL, NULL, 0, scale,
+             ACT_NONE);
+        softmax_ext(m, m->scores, (long)hcc * Nq, Nk, Nq, h0, causal, dy, dx, W,
+                    heads);
+        gemm(m, Nq, hd, Nk, bmat(m->scores, 0, Nk, 0, plane),
+             bmat(V, (long)h0 * hd, ldv, 0, hd), 0,
+             bmat(O, (long)h0 * hd, ldo, 0, hd), hcc, hcc, NULL, NULL, 0, 1.0f,
+             ACT_NONE);
+    }
 }
 
 /* Attention geometry of a block (block_geom, sam3_model.c:777-791). */

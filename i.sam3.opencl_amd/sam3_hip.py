@@ -34,7 +34,7 @@ EXPORTS = [
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
     "window_partition", "window_unpartition_add", "mha", "attn_fused",
     "attn_packed", "vit_attention", "vit_block", "sam_encode_trunk",
-    "sam_trunk_graph",
+    "sam_trunk_graph", "softmax_ext", "attend",
 ]
 
 
@@ -153,6 +153,10 @@ def lib():
                             c_int]
     L.add_bcast.argtypes = [MP, Mem, Mem, Mem, c_long, c_long]
     L.softmax_rows.argtypes = [MP, Mem, c_long, c_int]
+    L.softmax_ext.argtypes = [MP, Mem, c_long, c_int, c_int, c_int, c_int, Mem,
+                              Mem, c_int, c_int]
+    L.attend.argtypes = [MP, c_int, c_int, c_int, c_int, Mem, c_int, Mem, c_int,
+                         Mem, c_int, Mem, c_int, c_int, Mem, Mem, c_int]
     L.rope_apply.argtypes = [MP, Mem, c_long, c_int]
     L.window_partition.argtypes = [MP, Mem, Mem, c_int, c_int, c_int, c_int]
     L.window_unpartition_add.argtypes = [MP, Mem, Mem, c_int, c_int, c_int,
@@ -315,6 +319,8 @@ class Model:
         else:
             self.m.hip = ctypes.pointer(backend._b)
             self.m.embed, self.m.heads, self.m.hd = embed, heads, hd
+            # Score buffer capacity as sam_path_init sizes it (floats).
+            self.m.score_cap = min(backend._b.max_alloc, 512 << 20) // 4
 
     @property
     def ptr(self):
@@ -359,6 +365,19 @@ def add_bcast(m, out, a, b, n, bmod):
 
 def softmax_rows(m, S, rows, L):
     _call(_lib.softmax_rows, m.ptr, S, rows, L)
+
+
+def softmax_ext(m, S, rows, L, Nq, h0=0, causal=False, dy=None, dx=None, W=0,
+                nh=1):
+    _call(_lib.softmax_ext, m.ptr, S, rows, L, Nq, h0, int(bool(causal)), dy,
+          dx, W, nh)
+
+
+def attend(m, Nq, Nk, heads, hd, Q, ldq, K, ldk, V, ldv, O, ldo, causal=False,
+           dy=None, dx=None, W=0):
+    """attend() of the text path (sam3_text.c:305-343) on device buffers."""
+    _call(_lib.attend, m.ptr, Nq, Nk, heads, hd, Q, ldq, K, ldk, V, ldv, O, ldo,
+          int(bool(causal)), dy, dx, W)
 
 
 def rope_apply(m, table, rows, npos):

@@ -245,6 +245,27 @@ void add_bcast(struct sam_model *m, hipb_mem out, hipb_mem a, hipb_mem b,
 /* In-place softmax of rows of L floats (sam3_model.c:332-341). */
 void softmax_rows(struct sam_model *m, hipb_mem S, long rows, int L);
 
+/* softmax_ext over rows = heads x Nq rows of L scores (heads from h0),
+ * sam3_kernels.cl:885-921: the causal mask (key j > query i excluded) or,
+ * with dy / dx, SAM 3's box relative position bias dy[(i H + j / W) nh +
+ * h] + dx[(i W + j % W) nh + h], H = L / W, added before the softmax. The
+ * reference's kernel has no host wrapper; attend() launches it. */
+void softmax_ext(struct sam_model *m, hipb_mem S, long rows, int L, int Nq,
+                 int h0, int causal, hipb_mem dy, hipb_mem dx, int W, int nh);
+
+/* Multi-head attention of the text path, attend() of sam3_text.c:305-343
+ * (the reference's static helper, taking the model instead of struct
+ * sam3_text): heads of width hd at columns h hd of Q [Nq][ldq], K [Nk][ldk],
+ * V [Nk][ldv], O [Nq][ldo]; scale 1 / sqrt(hd); optional causal mask or
+ * box bias (dy [Nq][Nk / W][heads], dx [Nq][W][heads]). Without mask or
+ * bias, with Nq == Nk and hd 64 (or 32 on the bf16 path) the fused
+ * attention runs; otherwise the reference's sequence per score-buffer
+ * chunk of heads: gemm Q K^T, softmax_ext, gemm P V. Fatal, like the
+ * reference, when one head's Nq x Nk scores exceed the score buffer. */
+void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
+            int ldq, hipb_mem K, int ldk, hipb_mem V, int ldv, hipb_mem O,
+            int ldo, int causal, hipb_mem dy, hipb_mem dx, int W);
+
 /* In-place RoPE of the q and k thirds of m->qkv rows at position
  * r % npos (sam3_model.c:965-978). */
 void rope_apply(struct sam_model *m, hipb_mem table, long rows, int npos);

@@ -2,9 +2,9 @@
 kernels (same seeded inputs, outputs of sam3_kernels.cl run unchanged).
 
 Two routes per case: the reference's operator sequence replayed with this
-library's operators (gemm, softmax_rows, layernorm, rope_apply, window
-ops, mha), and for the attention cases the fused attn_fused / vit_attention
-entry points. Bars: bit-exact for data movement and RoPE, rel-L2 <= 2e-5
+library's operators (gemm, softmax_rows, softmax_ext, layernorm,
+rope_apply, window ops, mha), and for the attention cases the fused
+attn_fused / vit_attention / attend entry points. Bars: bit-exact for data movement and RoPE, rel-L2 <= 2e-5
 on the fp32 path, <= 2e-2 on the bf16 path; max-abs printed."""
 import os
 import sys
@@ -72,6 +72,18 @@ class HipImpl:
         self.hip.softmax_rows(self.m, d, S.size // S.shape[-1], S.shape[-1])
         out = self.be.read(d).reshape(S.shape)
         self.be.release(d)
+        return out
+
+    def softmax_ext(self, S, Nq, h0, causal, dy, dx, W, nh):
+        d = self._up(S)
+        ddy = self._up(dy) if dy is not None else None
+        ddx = self._up(dx) if dx is not None else None
+        self.hip.softmax_ext(self.m, d, S.size // S.shape[-1], S.shape[-1], Nq,
+                             h0, causal, ddy, ddx, W, nh)
+        out = self.be.read(d).reshape(S.shape)
+        for x in (d, ddy, ddx):
+            if x is not None:
+                self.be.release(x)
         return out
 
     def layernorm(self, X, g, b, eps=1e-5, act=0):
@@ -163,4 +175,29 @@ def test_vit_region(hip, be, be16, precision, unfused):
     tol = 2e-5 if precision == "fp32" else 2e-2
     assert report("vit region %s unfused=%d" % (precision, unfused), got,
                   gold["O"]) <= tol
+    m.free()
+
+
+@pytest.mark.parametrize("name", [n for n in gc.CASES if n.startswith("attend_")])
+@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+def test_attend_entry_point(hip, be, be16, name, precision):
+    """attend() through the C-ABI: fused for the unmasked self-attention
+    (head width 32 packed to 64 on the bf16 path), the reference's
+    gemm / softmax_ext / gemm sequence for the causal and box-bias cases."""
+    case, gold = load(name)
+    b = be if precision == "fp32" else be16
+    Q, K, V = case["inputs"][:3]
+    Nq, Nk, H, hd = case["Nq"], case["Nk"], case["heads"], case["hd"]
+    D = H * hd
+    m = hip.Model(b, embed=128, heads=2)
+    dq, dk, dv = b.upload(Q), b.upload(K), b.upload(V)
+    do = b.alloc(Nq * D * 4)
+    dy = dx = None
+    if case["mode"] == "box":
+        dy, dx = b.upload(case["inputs"][3]), b.upload(case["inputs"][4])
+    hip.attend(m, Nq, Nk, H, hd, dq, D, dk, D, dv, D, do, D,
+               case["mode"] == "causal", dy, dx, case["W"])
+    got = b.read(do).reshape(Nq, D)
+    tol = 2e-5 if precision == "fp32" else 2e-2
+    assert report("attend %s %s" % (name, precision), got, gold["O"]) <= tol
     m.free()

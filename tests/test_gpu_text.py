@@ -1,0 +1,120 @@
+"""GPU parity of the text path's attention, attend() (sam3_text.c:305-343),
+against the oracle's restatement (or_attend: gemm Q K^T / sqrt(hd),
+softmax_ext with the causal mask or the box relative position bias, gemm
+P V), at the shapes the text path runs:
+
+- fusion encoder self-attention: 5184 image tokens, 8 heads x 32
+  (sam3_text.c:797); fused on the bf16 path, the reference's sequence
+  (two score chunks) on the fp32 path; sampled query rows;
+- decoder cross-attention to the image: 201 queries over 5184 keys with
+  the box bias dy / dx (sam3_text.c:860-861);
+- text encoder self-attention: 32 tokens, 16 heads x 64, causal
+  (sam3_text.c:489-490).
+
+Bars: rel-L2 <= 2e-5 (fp32), <= 2e-2 (bf16); max-abs printed.
+"""
+import numpy as np
+import pytest
+
+from gpu_common import report
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 2e-5, "bf16": 2e-2}
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import sam3_hip
+    return sam3_hip
+
+
+@pytest.fixture(scope="module", params=["fp32", "bf16"])
+def be(hip, request):
+    b = hip.Backend(precision=request.param)
+    b.precision = request.param
+    yield b
+    b.free()
+
+
+def _run(hip, be, Q, K, V, heads, hd, causal=False, dy=None, dx=None, W=0,
+         score_cap=None):
+    Nq, Nk, D = Q.shape[0], K.shape[0], heads * hd
+    m = hip.Model(be, embed=128, heads=2)
+    if score_cap is not None:
+        m.m.score_cap = score_cap
+    dq, dk, dv = be.upload(Q), be.upload(K), be.upload(V)
+    do = be.alloc(Nq * D * 4)
+    ddy = be.upload(dy) if dy is not None else None
+    ddx = be.upload(dx) if dx is not None else None
+    try:
+        hip.attend(m, Nq, Nk, heads, hd, dq, Q.shape[1], dk, K.shape[1], dv,
+                   V.shape[1], do, D, causal, ddy, ddx, W)
+        return be.read(do).reshape(Nq, D)
+    finally:
+        for x in (dq, dk, dv, do, ddy, ddx):
+            if x is not None:
+                be.release(x)
+        m.free()
+
+
+def test_fusion_encoder_self_attention(hip, be, orc):
+    """5184 tokens (72 x 72), 8 heads x 32, no mask or bias."""
+    N, heads, hd = 5184, 8, 32
+    g = np.random.default_rng(31)
+    Q, K, V = (g.standard_normal((N, heads * hd)).astype(np.float32)
+               for _ in range(3))
+    print("attend fusion self N=%d %s" % (N, be.precision), flush=True)
+    got = _run(hip, be, Q, K, V, heads, hd)
+    rows = np.sort(g.choice(N, 96, replace=False))
+    want = orc.attend(Q[rows], K, V, heads, hd)
+    assert report("fusion self %s" % be.precision, got[rows], want) <= TOL[be.precision]
+
+
+def test_decoder_image_cross_attention_box_bias(hip, be, orc):
+    """201 queries (presence + 200) over the 72 x 72 image tokens, 8 heads
+    x 32, box relative position bias dy [201, 72, 8] + dx [201, 72, 8]."""
+    Nq, W, heads, hd = 201, 72, 8, 32
+    Nk = W * W
+    g = np.random.default_rng(32)
+    Q = g.standard_normal((Nq, heads * hd)).astype(np.float32)
+    K, V = (g.standard_normal((Nk, heads * hd)).astype(np.float32) for _ in range(2))
+    dy = (2 * g.standard_normal((Nq, W, heads))).astype(np.float32)
+    dx = (2 * g.standard_normal((Nq, W, heads))).astype(np.float32)
+    print("attend decoder box Nq=%d Nk=%d %s" % (Nq, Nk, be.precision), flush=True)
+    got = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    want = orc.attend(Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    assert report("decoder box %s" % be.precision, got, want) <= TOL[be.precision]
+
+
+def test_text_encoder_causal(hip, be, orc):
+    """32 text tokens of width 1024: 16 heads x 64, causal mask; query 0
+    attends to key 0 alone."""
+    n, heads, hd = 32, 16, 64
+    g = np.random.default_rng(33)
+    Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
+               for _ in range(3))
+    got = _run(hip, be, Q, K, V, heads, hd, causal=True)
+    want = orc.attend(Q, K, V, heads, hd, causal=True)
+    assert report("text causal %s" % be.precision, got, want) <= TOL[be.precision]
+    if be.precision == "fp32":
+        assert np.array_equal(got[0], V[0])
+
+
+def test_score_chunks_and_capacity(hip, be):
+    """One head per score chunk gives the result of all heads at once (the
+    chunk offset reaches the bias and the operand columns); a buffer that
+    cannot hold one head's scores is the reference's fatal error."""
+    Nq, W, heads, hd = 30, 6, 4, 32
+    Nk = W * 5
+    g = np.random.default_rng(34)
+    Q = g.standard_normal((Nq, heads * hd + 8)).astype(np.float32)
+    K, V = (g.standard_normal((Nk, heads * hd)).astype(np.float32) for _ in range(2))
+    dy = g.standard_normal((Nq, 5, heads)).astype(np.float32)
+    dx = g.standard_normal((Nq, W, heads)).astype(np.float32)
+    a = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    b = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W, score_cap=Nq * Nk)
+    assert np.array_equal(a, b)
+    with pytest.raises(hip.Sam3HipError):
+        _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
+             score_cap=Nq * Nk - 1)

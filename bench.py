@@ -243,6 +243,47 @@ def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
     return out
 
 
+def text_attention(hip, steps, warmup):
+    """The text path's attend() (sam3_text.c:305-343) at its two large
+    shapes, random N(0, 1) operands: the fusion encoder's self-attention
+    over the 72 x 72 image tokens (8 heads x 32, no mask: the fused kernel
+    on bf16, the reference's chunked gemm / softmax_ext / gemm on fp32) and
+    the decoder's cross-attention of 201 queries to the image with the box
+    relative position bias (gemm / softmax_ext / gemm). TFLOP/s counts
+    4 Nq Nk hd per head."""
+    out = {}
+    g = np.random.default_rng(41)
+    heads, hd, N, W, Nq = 8, 32, 5184, 72, 201
+    D = heads * hd
+    for p in ("bf16", "fp32"):
+        be = hip.Backend(precision=p)
+        m = hip.Model(be, embed=128, heads=2)
+        q, k, v = (be.upload(g.standard_normal((N, D), dtype=np.float32))
+                   for _ in range(3))
+        o = be.alloc(N * D * 4)
+        dy = be.upload(g.standard_normal((Nq, W, heads), dtype=np.float32))
+        dx = be.upload(g.standard_normal((Nq, W, heads), dtype=np.float32))
+        st, wu = (steps, warmup) if p == "bf16" else (max(2, steps // 20), 1)
+        ms = timed(be, lambda: hip.attend(m, N, N, heads, hd, q, D, k, D, v, D,
+                                          o, D), st, wu)
+        ms_box = timed(be, lambda: hip.attend(m, Nq, N, heads, hd, q, D, k, D,
+                                              v, D, o, D, False, dy, dx, W),
+                       max(2, steps // 10), max(1, warmup // 10))
+        out["fusion_self_" + p] = {
+            "workload": "5184 tokens, 8 heads x 32, no mask",
+            "ms": round(ms, 4),
+            "TFLOP/s": round(4.0 * N * N * hd * heads / ms / 1e9, 1)}
+        out["decoder_box_" + p] = {
+            "workload": "201 queries x 5184 keys, 8 heads x 32, box bias",
+            "ms": round(ms_box, 4),
+            "TFLOP/s": round(4.0 * Nq * N * hd * heads / ms_box / 1e9, 2)}
+        for d in (q, k, v, o, dy, dx):
+            be.release(d)
+        m.free()
+        be.free()
+    return out
+
+
 def cpu_baseline(steps=3):
     """The oracle's restatement of the reference's profile=cpu attention of
     the global block (gemm_cpu_t Q K^T with alpha 1/8 -> softmax_rows ->
@@ -334,6 +375,8 @@ def main():
                     help="only the mask-decoder cross-attention (profiling)")
     ap.add_argument("--backbone-only", action="store_true",
                     help="only the image encoder trunk (profiling)")
+    ap.add_argument("--text-only", action="store_true",
+                    help="only the text path's attend() shapes (profiling)")
     ap.add_argument("--precision", choices=("bf16", "fp32"),
                     help="with --backbone-only: that path alone")
     args = ap.parse_args()
@@ -348,6 +391,10 @@ def main():
         prec = (args.precision,) if args.precision else ("bf16", "fp32")
         print(json.dumps({"backbone": backbone(hip, args.steps, args.warmup,
                                                prec)}))
+        return
+    if args.text_only:
+        print(json.dumps({"text_attention": text_attention(
+            hip, args.steps, min(args.warmup, 20))}))
         return
     if args.decoder_only:
         be32 = hip.Backend(precision="fp32")
@@ -400,6 +447,7 @@ def main():
 
     dec = decoder(hip, be32, sub_steps, sub_warm)
     bb = backbone(hip, 5, 2)
+    text = text_attention(hip, sub_steps, sub_warm)
 
     qkv_flops = 2.0 * 5184 * 1024 * 3072
     result = {
@@ -440,6 +488,7 @@ def main():
             "windowed_TFLOP/s": round(win.flops() / w32_ms / 1e9, 2)},
         "decoder_fp32": dec,
         "backbone": bb,
+        "text_attention": text,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16, 4),

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
                                                   uint16_t *__restrict__ k16,
                                                   uint16_t *__restrict__ vt16,
                                                   float *__restrict__ knorm,
-                                                  int Np)
+                                                  int Npq, int Npk)
 {
     __shared__ uint16_t Vl[64][66];
     __shared__ float kred[4];
@@ -219,61 +219,74 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
     const int unit = blockIdx.y, i = blockIdx.x * 64 + row;
     const long b0 = unit / d.nb1, b1 = unit % d.nb1;
     const float2 *cs = (const float2 *)d.rope;
+    /* Row blocks past one side's padded length write nothing of it. */
+    const bool qblk = blockIdx.x * 64 < Npq, kblk = blockIdx.x * 64 < Npk;
+    const bool qrow = i < d.N && ds < d.hd, krow = i < d.Nk && ds < d.hd;
     float q[16], k[16], v[16];
 
-    if (i < d.N && ds < d.hd) {
+    for (int e = 0; e < 16; e++) {
+        q[e] = 0.0f;
+        k[e] = 0.0f;
+        v[e] = 0.0f;
+    }
+    if (qrow) {
         const float *qr = (const float *)d.Q + d.qoff + b0 * d.sq0 +
                           b1 * d.sq1 + (long)i * d.ldq + ds;
+
+        for (int e = 0; e < 16; e++)
+            q[e] = qr[e];
+    }
+    if (krow) {
         const float *kr = (const float *)d.K + d.koff + b0 * d.sk0 +
                           b1 * d.sk1 + (long)i * d.ldk + ds;
         const float *vr = (const float *)d.V + d.voff + b0 * d.sv0 +
                           b1 * d.sv1 + (long)i * d.ldv + ds;
 
         for (int e = 0; e < 16; e++) {
-            q[e] = qr[e];
             k[e] = kr[e];
             v[e] = vr[e];
         }
-        if (cs) {
-            const float2 *rot = cs + (long)(i % d.npos) * 32 + ds / 2;
-
-            for (int j = 0; j < 8; j++) {
-                const float2 r = rot[j];
-                float a = q[2 * j], b = q[2 * j + 1];
-
-                q[2 * j] = fmaf(a, r.x, -(b * r.y));
-                q[2 * j + 1] = fmaf(a, r.y, b * r.x);
-                a = k[2 * j];
-                b = k[2 * j + 1];
-                k[2 * j] = fmaf(a, r.x, -(b * r.y));
-                k[2 * j + 1] = fmaf(a, r.y, b * r.x);
-            }
-        }
-        for (int e = 0; e < 16; e++)
-            q[e] *= d.scale * LOG2E_F;
     }
-    else
-        for (int e = 0; e < 16; e++) {
-            q[e] = 0.0f;
-            k[e] = 0.0f;
-            v[e] = 0.0f;
+    if (cs && (qrow || krow)) {
+        const float2 *rot = cs + (long)(i % d.npos) * 32 + ds / 2;
+
+        for (int j = 0; j < 8; j++) {
+            const float2 r = rot[j];
+            float a = q[2 * j], b = q[2 * j + 1];
+
+            q[2 * j] = fmaf(a, r.x, -(b * r.y));
+            q[2 * j + 1] = fmaf(a, r.y, b * r.x);
+            a = k[2 * j];
+            b = k[2 * j + 1];
+            k[2 * j] = fmaf(a, r.x, -(b * r.y));
+            k[2 * j + 1] = fmaf(a, r.y, b * r.x);
         }
+    }
+    for (int e = 0; e < 16; e++)
+        q[e] *= d.scale * LOG2E_F;
     {
-        const long o = ((long)unit * Np + i) * 64 + ds;
         u32x4 a, b;
 
-        for (int e = 0; e < 4; e++) {
-            a[e] = pack_bf16x2(q[2 * e], q[2 * e + 1]);
-            b[e] = pack_bf16x2(q[8 + 2 * e], q[8 + 2 * e + 1]);
+        if (qblk) {
+            const long o = ((long)unit * Npq + i) * 64 + ds;
+
+            for (int e = 0; e < 4; e++) {
+                a[e] = pack_bf16x2(q[2 * e], q[2 * e + 1]);
+                b[e] = pack_bf16x2(q[8 + 2 * e], q[8 + 2 * e + 1]);
+            }
+            *(u32x4 *)(q16 + o) = a;
+            *(u32x4 *)(q16 + o + 8) = b;
         }
-        *(u32x4 *)(q16 + o) = a;
-        *(u32x4 *)(q16 + o + 8) = b;
-        for (int e = 0; e < 4; e++) {
-            a[e] = pack_bf16x2(k[2 * e], k[2 * e + 1]);
-            b[e] = pack_bf16x2(k[8 + 2 * e], k[8 + 2 * e + 1]);
+        if (kblk) {
+            const long o = ((long)unit * Npk + i) * 64 + ds;
+
+            for (int e = 0; e < 4; e++) {
+                a[e] = pack_bf16x2(k[2 * e], k[2 * e + 1]);
+                b[e] = pack_bf16x2(k[8 + 2 * e], k[8 + 2 * e + 1]);
+            }
+            *(u32x4 *)(k16 + o) = a;
+            *(u32x4 *)(k16 + o + 8) = b;
         }
-        *(u32x4 *)(k16 + o) = a;
-        *(u32x4 *)(k16 + o + 8) = b;
     }
     {
         /* Largest |k| of this 64-key block, over the bf16 values the
@@ -295,33 +308,73 @@ __global__ __launch_bounds__(256) void k_qkv_pack(attn_desc d,
     for (int e = 0; e < 16; e++)
         Vl[ds + e][row] = f2bf(v[e]);
     __syncthreads();
-    {
+    if (kblk) {
         /* Thread t writes channel t / 4, keys 16 (t % 4) .. +15. */
         const int dd = t >> 2, k0 = (t & 3) * 16;
-        uint16_t *dst = vt16 + ((long)unit * 64 + dd) * Np + blockIdx.x * 64 + k0;
+        uint16_t *dst = vt16 + ((long)unit * 64 + dd) * Npk + blockIdx.x * 64 + k0;
 
         for (int e = 0; e < 16; e++)
             dst[e] = Vl[dd][k0 + e];
-    }
-    if (t == 0) {
-        const float m2 = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
+        if (t == 0) {
+            const float m2 = fmaxf(fmaxf(kred[0], kred[1]), fmaxf(kred[2], kred[3]));
 
-        /* Rounded up by 2^-10 relative: covers the square root's and the
-         * sum's roundings. */
-        knorm[(long)unit * (Np / 64) + blockIdx.x] = sqrtf(m2) * (1.0f + 0x1p-10f);
+            /* Rounded up by 2^-10 relative: covers the square root's and
+             * the sum's roundings. */
+            knorm[(long)unit * (Npk / 64) + blockIdx.x] = sqrtf(m2) * (1.0f + 0x1p-10f);
+        }
     }
 }
 
 extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
                                void *vt16, float *knorm, void *stream)
 {
-    const int Np = (d->N + 63) / 64 * 64;
+    const int Npq = (d->N + 63) / 64 * 64, Npk = (d->Nk + 63) / 64 * 64;
+    const int Np = Npq > Npk ? Npq : Npk;
 
-    if (d->nb > 65535)
+    if (d->nb > 65535 || d->Nk < 1)
         return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_qkv_pack, dim3(Np / 64, d->nb), dim3(256), 0,
                        (hipStream_t)stream, *d, (uint16_t *)q16,
-                       (uint16_t *)k16, (uint16_t *)vt16, knorm, Np);
+                       (uint16_t *)k16, (uint16_t *)vt16, knorm, Npq, Npk);
+    return hipGetLastError();
+}
+
+/* Additive bias of the bf16 attention in its exp2 domain,
+ * out[unit][i][j] = log2(e) (dy[(i H + j / W) nh + h] + dx[(i W + j % W)
+ * nh + h]) for keys j < Nk and -inf for the padding up to Npk (unit = head
+ * h, H = Nk / W): the box relative position bias of softmax_ext
+ * (sam3_kernels.cl:904-906) for every (head, query, key). */
+__global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
+                                                  const float *__restrict__ dy,
+                                                  const float *__restrict__ dx,
+                                                  int heads, int Nq, int Nk, int Npk,
+                                                  int W, int nh)
+{
+    const long total = (long)heads * Nq * Npk;
+    const long e = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (e >= total)
+        return;
+    const int j = (int)(e % Npk);
+    const long r = e / Npk;
+    const int i = (int)(r % Nq), h = (int)(r / Nq), H = Nk / W;
+
+    out[e] = j < Nk ? (dy[((long)i * H + j / W) * nh + h] +
+                       dx[((long)i * W + j % W) * nh + h]) * LOG2E_F
+                    : -INFINITY;
+}
+
+extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
+                               int heads, int Nq, int Nk, int W, int nh,
+                               void *stream)
+{
+    const int Npk = (Nk + 63) / 64 * 64;
+    const long total = (long)heads * Nq * Npk;
+
+    if (total == 0)
+        return hipSuccess;
+    hipLaunchKernelGGL(k_box_bias, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh);
     return hipGetLastError();
 }
 
@@ -424,6 +477,7 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * block (which also guards against a row whose scores all lie far below
  * 0), take the exact block max with its cross-lane exchange. While every
  * m of the wave is 0 the scores feed exp2 directly. */
+template <bool EXT>
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
@@ -434,7 +488,9 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][64];
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
-    const int N = d.N, Np = (N + 63) / 64 * 64, nblk = Np / 64;
+    /* N queries and Nk keys per unit, each padded to a multiple of 64. */
+    const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64,
+              Npk = (Nk + 63) / 64 * 64, nblk = Npk / 64;
     const int ntiles = (N + 127) / 128;
     const long total = (long)d.nb * ntiles, per_xcd = (total + NXCD - 1) / NXCD;
     /* XCD-aware order: workgroups are dispatched to the XCDs round-robin,
@@ -446,10 +502,15 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         return;
     const long unit = item / ntiles;
     const uint16_t *Qu = q16 + unit * Np * 64;
-    const uint16_t *Ku = k16 + unit * Np * 64;
-    const uint16_t *Vu = vt16 + unit * 64 * Np;
+    const uint16_t *Ku = k16 + unit * Npk * 64;
+    const uint16_t *Vu = vt16 + unit * 64 * Npk;
     const float *kn = knorm + unit * nblk;
     const int qi = (int)(item % ntiles) * 128 + w * 32 + l32;
+    /* This lane's row of the additive bias table (exp2 domain, -inf past
+     * Nk), if any; queries past N read the last row (never stored). */
+    const float *brow = EXT && d.bias
+                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * Npk
+                            : nullptr;
     const int krow = kperm(l32);
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     const f32x16 zero16 = {};
@@ -490,7 +551,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         const int chunk = (l & 7) ^ ((row >> 1) & 7);
 
         koff[j] = 2u * (row * 64 + 8 * chunk);
-        voff[j] = 2u * (row * Np + 8 * chunk);
+        voff[j] = 2u * (row * Npk + 8 * chunk);
     }
     const unsigned lds_k = (unsigned)(uintptr_t)&Ks[0][0][0] + 2048u * wu,
                    lds_v = (unsigned)(uintptr_t)&Vt[0][0][0] + 2048u * wu;
@@ -522,7 +583,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         bf16x8 kf[8], vf[8], pb[4];
         f32x16 s0, s1;
         /* Can this block's scores exceed m + SAFE_SPAN for some lane? */
-        const bool check = __ballot(fresh || qn * kn_next - st.m > SAFE_SPAN) != 0;
+        const bool check =
+            __ballot(fresh || brow || qn * kn_next - st.m > SAFE_SPAN) != 0;
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -550,19 +612,49 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 s0[r] -= st.m;
                 s1[r] -= st.m;
             }
-        if (kb * 64 + 64 > N)
+        if (kb * 64 + 64 > Nk)
             for (int r = 0; r < 16; r++) {
                 const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
 
-                s0[r] += key < N ? 0.0f : -INFINITY;
-                s1[r] += key + 32 < N ? 0.0f : -INFINITY;
+                s0[r] += key < Nk ? 0.0f : -INFINITY;
+                s1[r] += key + 32 < Nk ? 0.0f : -INFINITY;
+            }
+        if (EXT && brow) {
+            /* Additive bias (no bound on it: every such block takes the
+             * exact max below). Registers 8a .. 8a + 7 of s0 are keys
+             * 16 a + 8 h .. +7 of the block, s1's 32 further. */
+            const float *bk = brow + kb * 64 + 8 * h;
+
+            for (int a = 0; a < 2; a++) {
+                const f32x4 b0 = *(const f32x4 *)(bk + 16 * a);
+                const f32x4 b1 = *(const f32x4 *)(bk + 16 * a + 4);
+                const f32x4 b2 = *(const f32x4 *)(bk + 32 + 16 * a);
+                const f32x4 b3 = *(const f32x4 *)(bk + 32 + 16 * a + 4);
+
+                for (int e = 0; e < 4; e++) {
+                    s0[8 * a + e] += b0[e];
+                    s0[8 * a + 4 + e] += b1[e];
+                    s1[8 * a + e] += b2[e];
+                    s1[8 * a + 4 + e] += b3[e];
+                }
+            }
+        }
+        if (EXT && d.causal)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
+
+                s0[r] += key > qi ? -INFINITY : 0.0f;
+                s1[r] += key + 32 > qi ? -INFINITY : 0.0f;
             }
         if (check) {
             /* Exact block max relative to m; move m (rescaling O, l and
-             * this block's scores) if it leaves the safe span. */
+             * this block's scores) if it leaves the safe span. A lane
+             * whose keys are all masked in this block stays put. */
             float mx = max16(s1, max16(s0, -INFINITY));
 
             mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            if (mx == -INFINITY)
+                mx = 0.0f;
             if (__ballot(mx > SAFE_SPAN || (fresh && mx < -SAFE_SPAN)) != 0) {
                 const float corr = __builtin_amdgcn_exp2f(-mx);
 
@@ -697,11 +789,17 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     const long total = (long)d->nb * ((d->N + 127) / 128);
     const long grid = (total + NXCD - 1) / NXCD * NXCD;
 
-    if (grid > 0x7fffffffL)
+    if (grid > 0x7fffffffL || d->Nk < 1)
         return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(k_attn_bf16, dim3((unsigned)grid), dim3(256), 0,
-                       (hipStream_t)stream, *d,
-                       (const uint16_t *)q16, (const uint16_t *)k16,
-                       (const uint16_t *)vt16, knorm);
+    if (d->bias || d->causal)
+        hipLaunchKernelGGL(k_attn_bf16<true>, dim3((unsigned)grid), dim3(256), 0,
+                           (hipStream_t)stream, *d,
+                           (const uint16_t *)q16, (const uint16_t *)k16,
+                           (const uint16_t *)vt16, knorm);
+    else
+        hipLaunchKernelGGL(k_attn_bf16<false>, dim3((unsigned)grid), dim3(256), 0,
+                           (hipStream_t)stream, *d,
+                           (const uint16_t *)q16, (const uint16_t *)k16,
+                           (const uint16_t *)vt16, knorm);
     return hipGetLastError();
 }

@@ -125,6 +125,13 @@ struct attn_desc {
     /* Head width: 64, or 32 on the bf16 path (packed with zero channels
      * 32..63, so the 64-wide kernel applies; 32 output columns stored). */
     int hd;
+    /* Keys per unit (N queries, Nk keys; K and V rows count Nk). bf16
+     * path only beyond Nk == N: the additive bias table [unit][N][Nk
+     * padded to 64] in the exp2 domain (-inf in the padding) or NULL, and
+     * the causal mask (key j > query i excluded). */
+    int Nk;
+    const float *bias;
+    int causal;
 };
 
 /* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads. */
@@ -141,6 +148,13 @@ int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
 int launch_attn_bf16(const struct attn_desc *d, const void *q16,
                      const void *k16, const void *vt16, const float *knorm,
                      void *stream);
+
+/* Additive bias table of the bf16 attention from the box relative
+ * position bias of softmax_ext: out [heads][Nq][Nk padded to 64] =
+ * log2(e) (dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h]), -inf in
+ * the padding (H = Nk / W). */
+int launch_box_bias(float *out, const float *dy, const float *dx, int heads,
+                    int Nq, int Nk, int W, int nh, void *stream);
 
 /* Decoder attention (8 heads, head width c = dint / 8). */
 int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,

@@ -442,28 +442,32 @@ static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
 /* The fused attention of attn_fused at head width hd: 64 on both paths,
  * 32 on the bf16 path (operands packed with zero channels 32..63). */
 static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
-                          int nb, int nb1, struct opnd Q, struct opnd K,
+                          int Nk, int nb, int nb1, struct opnd Q, struct opnd K,
                           struct opnd V, struct opnd O, hipb_mem rope,
-                          int npos, float scale)
+                          int npos, float scale, int causal, hipb_mem bias)
 {
     struct hipb_backend *b = m->hip;
     struct attn_desc d;
     int err;
 
-    if (N < 0 || nb < 1 || nb1 < 1 || (rope && npos < 1)) {
-        hipb_fatal("%s: invalid shape N=%d nb=%d nb1=%d npos=%d", who, N, nb,
-                   nb1, npos);
+    if (N < 0 || Nk < 0 || nb < 1 || nb1 < 1 || (rope && npos < 1)) {
+        hipb_fatal("%s: invalid shape N=%d Nk=%d nb=%d nb1=%d npos=%d", who, N,
+                   Nk, nb, nb1, npos);
         return;
     }
     if (!(hd == 64 || (hd == 32 && b->bf16 && !rope))) {
         hipb_fatal("%s: unsupported head width %d", who, hd);
         return;
     }
-    if (N == 0)
+    if (!b->bf16 && (Nk != N || causal || bias)) {
+        hipb_fatal("%s: key count, mask and bias need the bf16 path", who);
+        return;
+    }
+    if (N == 0 || Nk == 0)
         return;
     if (!opnd_ok(who, "Q", Q, N, hd, nb, nb1) ||
-        !opnd_ok(who, "K", K, N, hd, nb, nb1) ||
-        !opnd_ok(who, "V", V, N, hd, nb, nb1) ||
+        !opnd_ok(who, "K", K, Nk, hd, nb, nb1) ||
+        !opnd_ok(who, "V", V, Nk, hd, nb, nb1) ||
         !opnd_ok(who, "O", O, N, hd, nb, nb1))
         return;
     if (Q.buf->dtype != HIPB_F32 || K.buf->dtype != HIPB_F32 ||
@@ -501,14 +505,19 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
     d.npos = rope ? npos : 1;
     d.scale = scale;
     d.hd = hd;
+    d.Nk = Nk;
+    d.causal = causal != 0;
+    d.bias = bias ? (const float *)bias->ptr : NULL;
     if (b->bf16) {
         const size_t np = ((size_t)N + 63) / 64 * 64;
-        const size_t cnt = (size_t)nb * np * 64;
+        const size_t npk = ((size_t)Nk + 63) / 64 * 64;
 
-        if (!ensure_bf16(b, &m->q16, cnt, "packed q") ||
-            !ensure_bf16(b, &m->k16, cnt, "packed k") ||
-            !ensure_bf16(b, &m->vt16, cnt, "packed v^T") ||
-            !ensure_typed(b, &m->knorm, (size_t)nb * (np / 64), HIPB_F32,
+        if ((bias && !buf_ok(who, "bias table", bias, (size_t)nb * N * npk,
+                             HIPB_F32)) ||
+            !ensure_bf16(b, &m->q16, (size_t)nb * np * 64, "packed q") ||
+            !ensure_bf16(b, &m->k16, (size_t)nb * npk * 64, "packed k") ||
+            !ensure_bf16(b, &m->vt16, (size_t)nb * npk * 64, "packed v^T") ||
+            !ensure_typed(b, &m->knorm, (size_t)nb * (npk / 64), HIPB_F32,
                           "key block norms"))
             return;
         hipb_run_begin(b);
@@ -520,7 +529,7 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         hipb_run_begin(b);
         err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
                                (const float *)m->knorm->ptr, b->stream);
-        hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * hd * nb);
+        hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)Nk * hd * nb);
         return;
     }
     hipb_run_begin(b);
@@ -536,8 +545,8 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
         hipb_fatal("attn_fused: unsupported head width %d", m->hd);
         return;
     }
-    attn_fused_hd(m, "attn_fused", 64, N, nb, nb1, Q, K, V, O, rope, npos,
-                  scale);
+    attn_fused_hd(m, "attn_fused", 64, N, N, nb, nb1, Q, K, V, O, rope, npos,
+                  scale, 0, NULL);
 }
 
 void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
@@ -568,6 +577,7 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.nb = nb;
     d.nb1 = nb1;
     d.hd = 64;
+    d.Nk = N;
     d.O = O.buf->ptr;
     d.ooff = O.off;
     d.ldo = O.ld;
@@ -597,14 +607,39 @@ void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
     }
     if (Nq == 0 || Nk == 0)
         return;
-    /* Fused: no mask or bias, self-attention shape, and a head width the
-     * fused kernels take (64; 32 on the bf16 path). Heads are the units,
-     * head h at column h hd of every operand. */
-    if (!causal && !dy && Nq == Nk &&
-        (hd == 64 || (hd == 32 && b->bf16))) {
-        attn_fused_hd(m, "attend", hd, Nq, heads, heads, bmat(Q, 0, ldq, 0, hd),
-                      bmat(K, 0, ldk, 0, hd), bmat(V, 0, ldv, 0, hd),
-                      bmat(O, 0, ldo, 0, hd), NULL, 1, scale);
+    if (dy && (!dx || W < 1 || Nk % W ||
+               !buf_ok("attend", "dy", dy, (size_t)Nq * (Nk / W) * heads,
+                       HIPB_F32) ||
+               !buf_ok("attend", "dx", dx, (size_t)Nq * W * heads, HIPB_F32))) {
+        if (!hipb_failed())
+            hipb_fatal("attend: box bias needs dy, dx and W dividing Nk");
+        return;
+    }
+    /* Fused: the bf16 path for head width 64 or 32 with any mask or bias
+     * (the bias as a table in the kernel's exp2 domain), the fp32 path
+     * for head width 64 self-attention without either. Heads are the
+     * units, head h at column h hd of every operand. */
+    if ((b->bf16 && (hd == 64 || hd == 32)) ||
+        (hd == 64 && Nq == Nk && !causal && !dy)) {
+        if (dy) {
+            const size_t npk = ((size_t)Nk + 63) / 64 * 64;
+            int err;
+
+            if (!ensure_typed(b, &m->abias, (size_t)heads * Nq * npk, HIPB_F32,
+                              "attention bias table"))
+                return;
+            hipb_run_begin(b);
+            err = launch_box_bias((float *)m->abias->ptr, (const float *)dy->ptr,
+                                  (const float *)dx->ptr, heads, Nq, Nk, W,
+                                  heads, b->stream);
+            hipb_run_end(b, err, "box_bias", 0.0);
+            if (hipb_failed())
+                return;
+        }
+        attn_fused_hd(m, "attend", hd, Nq, Nk, heads, heads,
+                      bmat(Q, 0, ldq, 0, hd), bmat(K, 0, ldk, 0, hd),
+                      bmat(V, 0, ldv, 0, hd), bmat(O, 0, ldo, 0, hd), NULL, 1,
+                      scale, causal, dy ? m->abias : NULL);
         return;
     }
     /* The reference's sequence (sam3_text.c:305-343): per chunk of heads
@@ -1181,4 +1216,5 @@ void sam_path_free(struct sam_model *m)
     hipb_release(&m->tmp);
     hipb_release(&m->mlpbuf);
     hipb_release(&m->mlp16);
+    hipb_release(&m->abias);
 }

@@ -87,7 +87,7 @@ class SamModel(ctypes.Structure):
         [(n, Mem) for n in ("pe_w", "pos", "lnpw", "lnpb", "img", "tmp",
                             "mlpbuf", "mlp16")] + \
         [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
-         ("trunk_gen", ctypes.c_ulong)]
+         ("trunk_gen", ctypes.c_ulong), ("abias", Mem)]
 
 
 _lib = None

@@ -203,6 +203,9 @@ struct sam_model {
      * hipGraphExec_t, and the work-buffer generation it was captured at. */
     void *trunk_graph, *trunk_exec;
     unsigned long trunk_gen;
+    /* attend(): the box bias as the bf16 kernel's additive table
+     * [heads][Nq][Nk padded to 64] (exp2 domain). */
+    hipb_mem abias;
 };
 
 /* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =
@@ -257,11 +260,12 @@ void softmax_ext(struct sam_model *m, hipb_mem S, long rows, int L, int Nq,
  * (the reference's static helper, taking the model instead of struct
  * sam3_text): heads of width hd at columns h hd of Q [Nq][ldq], K [Nk][ldk],
  * V [Nk][ldv], O [Nq][ldo]; scale 1 / sqrt(hd); optional causal mask or
- * box bias (dy [Nq][Nk / W][heads], dx [Nq][W][heads]). Without mask or
- * bias, with Nq == Nk and hd 64 (or 32 on the bf16 path) the fused
- * attention runs; otherwise the reference's sequence per score-buffer
- * chunk of heads: gemm Q K^T, softmax_ext, gemm P V. Fatal, like the
- * reference, when one head's Nq x Nk scores exceed the score buffer. */
+ * box bias (dy [Nq][Nk / W][heads], dx [Nq][W][heads]). The fused
+ * attention runs on the bf16 path for hd 64 or 32 (with the mask or the
+ * bias) and on the fp32 path for hd 64 self-attention without either;
+ * otherwise the reference's sequence per score-buffer chunk of heads:
+ * gemm Q K^T, softmax_ext, gemm P V (fatal, like the reference, when one
+ * head's Nq x Nk scores exceed the score buffer). */
 void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
             int ldq, hipb_mem K, int ldk, hipb_mem V, int ldv, hipb_mem O,
             int ldo, int causal, hipb_mem dy, hipb_mem dx, int W);

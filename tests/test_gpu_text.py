@@ -4,12 +4,16 @@ softmax_ext with the causal mask or the box relative position bias, gemm
 P V), at the shapes the text path runs:
 
 - fusion encoder self-attention: 5184 image tokens, 8 heads x 32
-  (sam3_text.c:797); fused on the bf16 path, the reference's sequence
-  (two score chunks) on the fp32 path; sampled query rows;
+  (sam3_text.c:797); sampled query rows;
 - decoder cross-attention to the image: 201 queries over 5184 keys with
   the box bias dy / dx (sam3_text.c:860-861);
 - text encoder self-attention: 32 tokens, 16 heads x 64, causal
   (sam3_text.c:489-490).
+
+The bf16 path runs all three in the fused kernel (bias as an additive
+table, causal mask, head width 32 packed to 64); the fp32 path runs the
+reference's chunked gemm / softmax_ext / gemm for all three (head width
+32, the mask and the bias are outside its fused kernel).
 
 Bars: rel-L2 <= 2e-5 (fp32), <= 2e-2 (bf16); max-abs printed.
 """
@@ -103,8 +107,10 @@ def test_text_encoder_causal(hip, be, orc):
 
 def test_score_chunks_and_capacity(hip, be):
     """One head per score chunk gives the result of all heads at once (the
-    chunk offset reaches the bias and the operand columns); a buffer that
-    cannot hold one head's scores is the reference's fatal error."""
+    chunk offset reaches the bias and the operand columns); on the fp32
+    path, which runs the reference's chunked sequence for biased
+    attention, a buffer that cannot hold one head's scores is the
+    reference's fatal error (the bf16 path's fused kernel needs none)."""
     Nq, W, heads, hd = 30, 6, 4, 32
     Nk = W * 5
     g = np.random.default_rng(34)
@@ -115,6 +121,8 @@ def test_score_chunks_and_capacity(hip, be):
     a = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
     b = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W, score_cap=Nq * Nk)
     assert np.array_equal(a, b)
+    if be.precision != "fp32":
+        return
     with pytest.raises(hip.Sam3HipError):
         _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
              score_cap=Nq * Nk - 1)

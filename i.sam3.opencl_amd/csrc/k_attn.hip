@@ -482,7 +482,9 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
                                                       const uint16_t *__restrict__ vt16,
-                                                      const float *__restrict__ knorm)
+                                                      const float *__restrict__ knorm,
+                                                      float *__restrict__ part,
+                                                      int nsplit)
 {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][64];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][64];
@@ -492,20 +494,29 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64,
               Npk = (Nk + 63) / 64 * 64, nblk = Npk / 64;
     const int ntiles = (N + 127) / 128;
-    const long total = (long)d.nb * ntiles, per_xcd = (total + NXCD - 1) / NXCD;
+    /* 32-bit item arithmetic (the launcher keeps the grid below 2^31). */
+    const unsigned total = (unsigned)d.nb * ntiles * nsplit,
+                   per_xcd = (total + NXCD - 1) / NXCD;
     /* XCD-aware order: workgroups are dispatched to the XCDs round-robin,
      * so workgroup g runs on XCD g % NXCD; give each XCD a contiguous run
      * of (unit, tile) items, i.e. whole units, whose K / V then stay in
      * that XCD's L2 instead of every XCD streaming every unit. */
-    const long item = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
+    const unsigned item = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
     if (item >= total)
         return;
-    const long unit = item / ntiles;
+    /* Item = (unit, query tile, key split); split sp takes key blocks
+     * [kb0, kb1) and, with nsplit > 1, leaves partial (O, m, l) records
+     * in `part` for k_attn_merge. */
+    const unsigned us = nsplit > 1 ? item / (unsigned)nsplit : item;
+    const int sp = (int)(item - us * (unsigned)nsplit);
+    const long unit = us / (unsigned)ntiles;
+    const int tile = (int)(us - (unsigned)unit * (unsigned)ntiles);
+    const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
     const uint16_t *Qu = q16 + unit * Np * 64;
     const uint16_t *Ku = k16 + unit * Npk * 64;
     const uint16_t *Vu = vt16 + unit * 64 * Npk;
     const float *kn = knorm + unit * nblk;
-    const int qi = (int)(item % ntiles) * 128 + w * 32 + l32;
+    const int qi = tile * 128 + w * 32 + l32;
     /* This lane's row of the additive bias table (exp2 domain, -inf past
      * Nk), if any; queries past N read the last row (never stored). */
     const float *brow = EXT && d.bias
@@ -573,9 +584,9 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         vro[i] = 2u * (l32 * 64 + swz(l32, 2 * i + h));
     }
     const char *Kb = (const char *)&Ks[0][0][0], *Vb = (const char *)&Vt[0][0][0];
-    float kn_next = kn[0];
+    float kn_next = kn[kb0];
 
-    load_block(0, 0);
+    load_block(kb0, 0);
     /* Unrolled by two so that the slot is a constant: the LDS fragment
      * addresses are then one register plus an immediate offset. */
     auto block = [&](int kb, auto slot_c) {
@@ -590,8 +601,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         __syncthreads();
         /* Next block's bound, loaded after the barrier so that its latency
          * hides behind this block rather than in the barrier's wait. */
-        kn_next = kn[kb + 1 < nblk ? kb + 1 : kb];
-        if (kb + 1 < nblk)
+        kn_next = kn[kb + 1 < kb1 ? kb + 1 : kb];
+        if (kb + 1 < kb1)
             load_block(kb + 1, slot ^ 1);
         for (int c = 0; c < 2; c++)
             for (int ds = 0; ds < 4; ds++)
@@ -692,33 +703,46 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
             }
     };
-    for (int kb = 0; kb < nblk; kb += 2) {
+    for (int kb = kb0; kb < kb1; kb += 2) {
         block(kb, std::integral_constant<int, 0>());
-        if (kb + 1 < nblk)
+        if (kb + 1 < kb1)
             block(kb + 1, std::integral_constant<int, 1>());
     }
 
     st.l += __shfl_xor(st.l, 32, 64);
-    const float inv = 1.0f / st.l;
+    /* Final O / l, or with key splits the unnormalised O of this split
+     * (fp32 rows of 64 at part [unit][split][Np][64]) and its (m, l) pair
+     * (part's tail, [unit][split][Np][2]). */
+    const bool partial = nsplit > 1;
+    const float inv = partial ? 1.0f : 1.0f / st.l;
     const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-    const long obase = d.ooff + b0 * d.so0 + b1 * d.so1;
-    const bool f32out = d.odt == DT_F32;
+    const long pidx = (unit * nsplit + sp) * (long)Np;
+    void *const Obuf = partial ? (void *)part : d.O;
+    const long obase = partial ? pidx * 64 : d.ooff + b0 * d.so0 + b1 * d.so1;
+    const int ldo = partial ? 64 : d.ldo, ocols = partial ? 64 : d.hd;
+    const bool f32out = partial || d.odt == DT_F32;
 
-    if ((((obase | (long)d.ldo) & (f32out ? 3 : 7)) | ((uintptr_t)d.O & 15)) == 0) {
+    if (partial && h == 0 && qi < N) {
+        float *ml = part + (long)d.nb * nsplit * Np * 64 + (pidx + qi) * 2;
+
+        ml[0] = st.m;
+        ml[1] = st.l;
+    }
+    if ((((obase | (long)ldo) & (f32out ? 3 : 7)) | ((uintptr_t)Obuf & 15)) == 0) {
         /* Output rows 16-byte aligned: transpose the wave's O^T through
          * LDS so that 8 lanes write one 128-byte line of one query row.
-         * The slot of block nblk - 2 (or the unused one) is free: every
+         * The slot of block kb1 - 2 (or the unused one) is free: every
          * wave passed the last barrier after its final reads of it. Each
          * wave takes 4 KB; 16-byte chunk c of staging row r sits at chunk
          * c ^ (r & 7), which keeps both the writes (8 rows, one chunk)
          * and the reads (one row, 8 chunks) free of bank conflicts. */
-        const int fs = nblk & 1;
+        const int fs = (kb1 - kb0) & 1;
         char *stg = w < 2 ? (char *)&Ks[fs][32 * w][0] : (char *)&Vt[fs][32 * (w - 2)][0];
         const int q0 = qi - l32, c = l & 7;
 
         if (f32out) {
             /* Two passes of 32 columns (128 B per row); one for hd 32. */
-            for (int half = 0; half < d.hd / 32; half++) {
+            for (int half = 0; half < ocols / 32; half++) {
                 const f32x16 &o = half ? st.o1 : st.o0;
 
                 for (int g = 0; g < 4; g++) {
@@ -732,7 +756,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                     const f32x4 v = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
                     if (q0 + row < N)
-                        *(f32x4 *)((float *)d.O + obase + (long)(q0 + row) * d.ldo + 32 * half + 4 * c) = v;
+                        *(f32x4 *)((float *)Obuf + obase + (long)(q0 + row) * ldo + 32 * half + 4 * c) = v;
                 }
             }
         }
@@ -751,55 +775,113 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 const int row = 8 * j + (l >> 3);
                 const u32x4 v = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
-                if (q0 + row < N && 8 * c < d.hd)
-                    *(u32x4 *)((uint16_t *)d.O + obase + (long)(q0 + row) * d.ldo + 8 * c) = v;
+                if (q0 + row < N && 8 * c < ocols)
+                    *(u32x4 *)((uint16_t *)Obuf + obase + (long)(q0 + row) * ldo + 8 * c) = v;
             }
         }
     }
     else if (qi < N) {
-        const long orow = obase + (long)qi * d.ldo;
-
-        const bool wide = d.hd > 32;
+        const long orow = obase + (long)qi * ldo;
+        const bool wide = ocols > 32;
 
         if (f32out) {
             for (int r = 0; r < 16; r++) {
                 const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
-                ((float *)d.O)[orow + dd] = st.o0[r] * inv;
+                ((float *)Obuf)[orow + dd] = st.o0[r] * inv;
                 if (wide)
-                    ((float *)d.O)[orow + 32 + dd] = st.o1[r] * inv;
+                    ((float *)Obuf)[orow + 32 + dd] = st.o1[r] * inv;
             }
         }
         else {
             for (int r = 0; r < 16; r++) {
                 const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
-                ((uint16_t *)d.O)[orow + dd] = f2bf(st.o0[r] * inv);
+                ((uint16_t *)Obuf)[orow + dd] = f2bf(st.o0[r] * inv);
                 if (wide)
-                    ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
+                    ((uint16_t *)Obuf)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
             }
         }
     }
 }
 
+/* Merge of key-split partials (k_attn_bf16 with nsplit > 1): for each
+ * (unit, query), M = the largest m_s over splits that saw a key, weights
+ * w_s = 2^(m_s - M), O = sum_s w_s o_s / sum_s w_s l_s, stored like the
+ * kernel's own epilogue (hd columns, fp32 or bf16). 16 threads per query,
+ * four channels each. */
+__global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__restrict__ part,
+                                                    int nsplit, int Np)
+{
+    const long g = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int c4 = (threadIdx.x & 15) * 4;
+
+    if (g >= (long)d.nb * d.N || c4 >= d.hd)
+        return;
+    const long unit = g / d.N;
+    const int q = (int)(g % d.N);
+    const float *ml = part + (long)d.nb * nsplit * Np * 64;
+    float M = -INFINITY, L = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int sp = 0; sp < nsplit; sp++) {
+        const float *p = ml + ((unit * nsplit + sp) * Np + q) * 2;
+
+        if (p[1] > 0.0f)
+            M = fmaxf(M, p[0]);
+    }
+    for (int sp = 0; sp < nsplit; sp++) {
+        const long r = (unit * nsplit + sp) * Np + q;
+        const float *p = ml + r * 2;
+
+        if (p[1] > 0.0f) {
+            const float wt = __builtin_amdgcn_exp2f(p[0] - M);
+            const f32x4 o = *(const f32x4 *)(part + r * 64 + c4);
+
+            L = fmaf(wt, p[1], L);
+            acc += wt * o;
+        }
+    }
+    const float inv = 1.0f / L;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+    const long o = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + c4;
+
+    for (int e = 0; e < 4; e++) {
+        if (d.odt == DT_F32)
+            ((float *)d.O)[o + e] = acc[e] * inv;
+        else
+            ((uint16_t *)d.O)[o + e] = f2bf(acc[e] * inv);
+    }
+}
+
 extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 const void *k16, const void *vt16,
-                                const float *knorm, void *stream)
+                                const float *knorm, float *part, int nsplit,
+                                void *stream)
 {
-    const long total = (long)d->nb * ((d->N + 127) / 128);
+    const int Np = (d->N + 63) / 64 * 64, nblk = (d->Nk + 63) / 64;
+    const long total = (long)d->nb * ((d->N + 127) / 128) * nsplit;
     const long grid = (total + NXCD - 1) / NXCD * NXCD;
+    int err;
 
-    if (grid > 0x7fffffffL || d->Nk < 1)
+    if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk ||
+        (nsplit > 1 && !part))
         return hipErrorInvalidConfiguration;
     if (d->bias || d->causal)
         hipLaunchKernelGGL(k_attn_bf16<true>, dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
-                           (const uint16_t *)vt16, knorm);
+                           (const uint16_t *)vt16, knorm, part, nsplit);
     else
         hipLaunchKernelGGL(k_attn_bf16<false>, dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
-                           (const uint16_t *)vt16, knorm);
+                           (const uint16_t *)vt16, knorm, part, nsplit);
+    err = hipGetLastError();
+    if (err != hipSuccess || nsplit == 1)
+        return err;
+    hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
+                       dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
+                       nsplit, Np);
     return hipGetLastError();
 }

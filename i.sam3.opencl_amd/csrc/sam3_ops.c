@@ -439,6 +439,34 @@ static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
     return ensure_typed(b, buf, count, HIPB_BF16, what);
 }
 
+/* Key splits of the bf16 attention: enough (unit, query tile, split)
+ * workgroups to fill one round of three per CU when the units and query
+ * tiles alone leave CUs idle, each split keeping at least two 64-key
+ * blocks. The ViT shapes (656 and 720 workgroups) stay at one. */
+static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
+{
+    const long items = (long)nb * ((N + 127) / 128);
+    const int nblk = (Nk + 63) / 64, cus = b->cu_count > 0 ? b->cu_count : 256;
+    long ns = 3L * cus / (items > 0 ? items : 1);
+
+    if (ns > nblk / 2)
+        ns = nblk / 2;
+    return ns > 1 ? (int)ns : 1;
+}
+
+/* Partial records for nsplit key splits: nb nsplit Np (64 + 2) floats. */
+static float *attn_part(struct sam_model *m, int N, int nb, int nsplit)
+{
+    const size_t np = ((size_t)N + 63) / 64 * 64;
+
+    if (nsplit <= 1)
+        return NULL;
+    if (!ensure_typed(m->hip, &m->apart, (size_t)nb * nsplit * np * 66,
+                      HIPB_F32, "attention split partials"))
+        return NULL;
+    return (float *)m->apart->ptr;
+}
+
 /* The fused attention of attn_fused at head width hd: 64 on both paths,
  * 32 on the bf16 path (operands packed with zero channels 32..63). */
 static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
@@ -526,10 +554,18 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         hipb_run_end(b, err, "qkv_pack", 0.0);
         if (hipb_failed())
             return;
-        hipb_run_begin(b);
-        err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                               (const float *)m->knorm->ptr, b->stream);
-        hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)Nk * hd * nb);
+        {
+            const int ns = attn_splits(b, N, Nk, nb);
+            float *part = attn_part(m, N, nb, ns);
+
+            if (ns > 1 && !part)
+                return;
+            hipb_run_begin(b);
+            err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                                   (const float *)m->knorm->ptr, part, ns,
+                                   b->stream);
+            hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)Nk * hd * nb);
+        }
         return;
     }
     hipb_run_begin(b);
@@ -554,7 +590,8 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     struct hipb_backend *b = m->hip;
     const size_t np = ((size_t)N + 63) / 64 * 64;
     struct attn_desc d;
-    int err;
+    float *part;
+    int err, ns;
 
     if (N < 1 || nb < 1 || nb1 < 1) {
         hipb_fatal("attn_packed: invalid shape N=%d nb=%d nb1=%d", N, nb, nb1);
@@ -584,9 +621,13 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.so0 = O.s0;
     d.so1 = O.s1;
     d.odt = O.buf->dtype;
+    ns = attn_splits(b, N, N, nb);
+    part = attn_part(m, N, nb, ns);
+    if (ns > 1 && !part)
+        return;
     hipb_run_begin(b);
     err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                           (const float *)m->knorm->ptr, b->stream);
+                           (const float *)m->knorm->ptr, part, ns, b->stream);
     hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
 }
 
@@ -1217,4 +1258,5 @@ void sam_path_free(struct sam_model *m)
     hipb_release(&m->mlpbuf);
     hipb_release(&m->mlp16);
     hipb_release(&m->abias);
+    hipb_release(&m->apart);
 }

@@ -87,7 +87,8 @@ class SamModel(ctypes.Structure):
         [(n, Mem) for n in ("pe_w", "pos", "lnpw", "lnpb", "img", "tmp",
                             "mlpbuf", "mlp16")] + \
         [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
-         ("trunk_gen", ctypes.c_ulong), ("abias", Mem)]
+         ("trunk_gen", ctypes.c_ulong), ("abias", Mem),
+         ("apart", Mem)]
 
 
 _lib = None

@@ -206,6 +206,9 @@ struct sam_model {
     /* attend(): the box bias as the bf16 kernel's additive table
      * [heads][Nq][Nk padded to 64] (exp2 domain). */
     hipb_mem abias;
+    /* Key-split partial records of the bf16 attention ([unit][split][Np]
+     * rows of 64 O values, then their (m, l) pairs). */
+    hipb_mem apart;
 };
 
 /* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =

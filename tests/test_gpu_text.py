@@ -126,3 +126,16 @@ def test_score_chunks_and_capacity(hip, be):
     with pytest.raises(hip.Sam3HipError):
         _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
              score_cap=Nq * Nk - 1)
+
+
+def test_long_causal_split_keys(hip, be, orc):
+    """600 tokens, 2 heads x 64, causal: on the bf16 path the keys split
+    five ways, and splits past a query's position see no key at all
+    (their partials carry l = 0 and drop out of the merge)."""
+    n, heads, hd = 600, 2, 64
+    g = np.random.default_rng(35)
+    Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
+               for _ in range(3))
+    got = _run(hip, be, Q, K, V, heads, hd, causal=True)
+    want = orc.attend(Q, K, V, heads, hd, causal=True)
+    assert report("long causal %s" % be.precision, got, want) <= TOL[be.precision]

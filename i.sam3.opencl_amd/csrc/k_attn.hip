@@ -350,18 +350,25 @@ __global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
                                                   int heads, int Nq, int Nk, int Npk,
                                                   int W, int nh)
 {
-    const long total = (long)heads * Nq * Npk;
-    const long e = (long)blockIdx.x * 256 + threadIdx.x;
+    /* Thread: four consecutive keys of one (head, query) row; 32-bit
+     * index arithmetic (the launcher keeps heads Nq Npk below 2^31). */
+    const unsigned rowlen = (unsigned)Npk / 4, total = (unsigned)heads * Nq * rowlen;
+    const unsigned e = blockIdx.x * 256u + threadIdx.x;
 
     if (e >= total)
         return;
-    const int j = (int)(e % Npk);
-    const long r = e / Npk;
-    const int i = (int)(r % Nq), h = (int)(r / Nq), H = Nk / W;
+    const unsigned r = e / rowlen, j0 = (e - r * rowlen) * 4;
+    const unsigned h = r / (unsigned)Nq, i = r - h * (unsigned)Nq, H = (unsigned)(Nk / W);
+    f32x4 v;
 
-    out[e] = j < Nk ? (dy[((long)i * H + j / W) * nh + h] +
-                       dx[((long)i * W + j % W) * nh + h]) * LOG2E_F
-                    : -INFINITY;
+    for (int k = 0; k < 4; k++) {
+        const unsigned j = j0 + k, y = j / (unsigned)W;
+
+        v[k] = j < (unsigned)Nk ? (dy[(i * H + y) * nh + h] +
+                                   dx[(i * (unsigned)W + (j - y * W)) * nh + h]) * LOG2E_F
+                                : -INFINITY;
+    }
+    *(f32x4 *)(out + (long)r * Npk + j0) = v;
 }
 
 extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
@@ -369,10 +376,12 @@ extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
                                void *stream)
 {
     const int Npk = (Nk + 63) / 64 * 64;
-    const long total = (long)heads * Nq * Npk;
+    const long total = (long)heads * Nq * (Npk / 4);
 
     if (total == 0)
         return hipSuccess;
+    if ((long)heads * Nq * Npk >= 0x7fffffffL)
+        return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_box_bias, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh);
     return hipGetLastError();

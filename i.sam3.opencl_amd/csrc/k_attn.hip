@@ -350,25 +350,28 @@ __global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
                                                   int heads, int Nq, int Nk, int Npk,
                                                   int W, int nh)
 {
-    /* Thread: four consecutive keys of one (head, query) row; 32-bit
-     * index arithmetic (the launcher keeps heads Nq Npk below 2^31). */
-    const unsigned rowlen = (unsigned)Npk / 4, total = (unsigned)heads * Nq * rowlen;
-    const unsigned e = blockIdx.x * 256u + threadIdx.x;
+    /* Workgroup: one (head, query) row; its H dy and W dx values go to
+     * LDS once, then the row is written as 16-byte runs of four keys. */
+    extern __shared__ float sxy[];
+    const int r = blockIdx.x, h = r / Nq, i = r - h * Nq, H = Nk / W;
+    float *sy = sxy, *sx = sxy + H;
+    float *orow = out + (long)r * Npk;
 
-    if (e >= total)
-        return;
-    const unsigned r = e / rowlen, j0 = (e - r * rowlen) * 4;
-    const unsigned h = r / (unsigned)Nq, i = r - h * (unsigned)Nq, H = (unsigned)(Nk / W);
-    f32x4 v;
+    for (int t = threadIdx.x; t < H; t += 256)
+        sy[t] = dy[((long)i * H + t) * nh + h];
+    for (int t = threadIdx.x; t < W; t += 256)
+        sx[t] = dx[((long)i * W + t) * nh + h];
+    __syncthreads();
+    for (int j0 = 4 * threadIdx.x; j0 < Npk; j0 += 1024) {
+        f32x4 v;
 
-    for (int k = 0; k < 4; k++) {
-        const unsigned j = j0 + k, y = j / (unsigned)W;
+        for (int k = 0; k < 4; k++) {
+            const unsigned j = j0 + k, y = j / (unsigned)W;
 
-        v[k] = j < (unsigned)Nk ? (dy[(i * H + y) * nh + h] +
-                                   dx[(i * (unsigned)W + (j - y * W)) * nh + h]) * LOG2E_F
-                                : -INFINITY;
+            v[k] = j < (unsigned)Nk ? (sy[y] + sx[j - y * W]) * LOG2E_F : -INFINITY;
+        }
+        *(f32x4 *)(orow + j0) = v;
     }
-    *(f32x4 *)(out + (long)r * Npk + j0) = v;
 }
 
 extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
@@ -376,13 +379,14 @@ extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
                                void *stream)
 {
     const int Npk = (Nk + 63) / 64 * 64;
-    const long total = (long)heads * Nq * (Npk / 4);
+    const long rows = (long)heads * Nq;
+    const size_t lds = ((size_t)Nk / W + W) * sizeof(float);
 
-    if (total == 0)
+    if (rows == 0)
         return hipSuccess;
-    if ((long)heads * Nq * Npk >= 0x7fffffffL)
+    if (rows > 0x7fffffffL || W < 1 || lds > 65536)
         return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(k_box_bias, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(k_box_bias, dim3((unsigned)rows), dim3(256), lds,
                        (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh);
     return hipGetLastError();
 }
@@ -814,13 +818,13 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     }
 }
 
-/* Merge of key-split partials (k_attn_bf16 with nsplit > 1): for each
- * (unit, query), M = the largest m_s over splits that saw a key, weights
- * w_s = 2^(m_s - M), O = sum_s w_s o_s / sum_s w_s l_s, stored like the
- * kernel's own epilogue (hd columns, fp32 or bf16). 16 threads per query,
- * four channels each. */
-__global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__restrict__ part,
-                                                    int nsplit, int Np)
+/* Merge of a few key-split partials (nsplit <= 8): 16 threads per
+ * (unit, query), four channels each, looping over the splits: M = the
+ * largest m_s over splits that saw a key, O = sum w_s o_s / sum w_s l_s
+ * with w_s = 2^(m_s - M), stored like the kernel's own epilogue. */
+__global__ __launch_bounds__(256) void k_attn_merge_few(attn_desc d,
+                                                        const float *__restrict__ part,
+                                                        int nsplit, int Np)
 {
     const long g = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
     const int c4 = (threadIdx.x & 15) * 4;
@@ -863,6 +867,51 @@ __global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__
     }
 }
 
+/* Merge of key-split partials (k_attn_bf16 with 8 < nsplit <= 64): a
+ * wave per (unit, query). Lane s holds split s's (m, l): M = the largest m
+ * over splits that saw a key, weights w_s = 2^(m_s - M), L = sum w_s l_s
+ * (wave reductions); then lane c sums w_s o_s[c] over the splits (each
+ * split's 64 channels one coalesced 256-byte read) and stores O = that / L
+ * like the kernel's own epilogue (hd columns, fp32 or bf16). */
+__global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__restrict__ part,
+                                                    int nsplit, int Np)
+{
+    const int l = threadIdx.x & 63;
+    const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+
+    if (g >= (long)d.nb * d.N)
+        return;
+    const long unit = g / d.N;
+    const int q = (int)(g % d.N);
+    const float *ml = part + (long)d.nb * nsplit * Np * 64;
+    float ms = -INFINITY, ls = 0.0f;
+
+    if (l < nsplit) {
+        const float *p = ml + ((unit * nsplit + l) * Np + q) * 2;
+
+        ms = p[0];
+        ls = p[1];
+    }
+    const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
+    const float wt = ls > 0.0f ? __builtin_amdgcn_exp2f(ms - M) : 0.0f;
+    const float L = wave_sum(wt * ls);
+    const float *o = part + ((unit * nsplit) * Np + q) * 64 + l;
+    float acc = 0.0f;
+
+#pragma unroll 8
+    for (int sp = 0; sp < nsplit; sp++)
+        acc = fmaf(__shfl(wt, sp, 64), o[(long)sp * Np * 64], acc);
+    if (l < d.hd) {
+        const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+        const long oi = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + l;
+
+        if (d.odt == DT_F32)
+            ((float *)d.O)[oi] = acc / L;
+        else
+            ((uint16_t *)d.O)[oi] = f2bf(acc / L);
+    }
+}
+
 extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 const void *k16, const void *vt16,
                                 const float *knorm, float *part, int nsplit,
@@ -873,7 +922,7 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     const long grid = (total + NXCD - 1) / NXCD * NXCD;
     int err;
 
-    if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk ||
+    if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk || nsplit > 64 ||
         (nsplit > 1 && !part))
         return hipErrorInvalidConfiguration;
     if (d->bias || d->causal)
@@ -889,8 +938,13 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     err = hipGetLastError();
     if (err != hipSuccess || nsplit == 1)
         return err;
-    hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
-                       dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
-                       nsplit, Np);
+    if (nsplit <= 8)
+        hipLaunchKernelGGL(k_attn_merge_few, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
+                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
+                           nsplit, Np);
+    else
+        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 3) / 4)),
+                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
+                           nsplit, Np);
     return hipGetLastError();
 }

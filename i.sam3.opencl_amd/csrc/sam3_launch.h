@@ -145,7 +145,7 @@ int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
                     void *vt16, float *knorm, void *stream);
 
 /* bf16 MFMA attention on the packed operands; O addressed as in d. With
- * nsplit > 1 the key blocks are split nsplit ways and `part` (nb nsplit
+ * 1 < nsplit <= 64 the key blocks are split nsplit ways and `part` (nb nsplit
  * Np 66 floats, Np = N rounded up to 64) holds the partials that a merge
  * kernel combines into O. */
 int launch_attn_bf16(const struct attn_desc *d, const void *q16,

@@ -442,7 +442,8 @@ static int ensure_bf16(struct hipb_backend *b, hipb_mem *buf, size_t count,
 /* Key splits of the bf16 attention: enough (unit, query tile, split)
  * workgroups to fill one round of three per CU when the units and query
  * tiles alone leave CUs idle, each split keeping at least two 64-key
- * blocks. The ViT shapes (656 and 720 workgroups) stay at one. */
+ * blocks, at most 64 splits. The ViT shapes (656 and 720 workgroups)
+ * stay at one. */
 static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
 {
     const long items = (long)nb * ((N + 127) / 128);
@@ -451,6 +452,8 @@ static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
 
     if (ns > nblk / 2)
         ns = nblk / 2;
+    if (ns > 64) /* the merge takes a split per lane */
+        ns = 64;
     return ns > 1 ? (int)ns : 1;
 }
 

@@ -139,3 +139,17 @@ def test_long_causal_split_keys(hip, be, orc):
     got = _run(hip, be, Q, K, V, heads, hd, causal=True)
     want = orc.attend(Q, K, V, heads, hd, causal=True)
     assert report("long causal %s" % be.precision, got, want) <= TOL[be.precision]
+
+
+def test_one_head_many_key_splits(hip, be, orc):
+    """2000 tokens, one head of 64: on the bf16 path 16 query tiles leave
+    the GPU idle, so the keys split 15 ways and the wave-per-query merge
+    combines them (the bias case above takes 40 splits)."""
+    n, heads, hd = 2000, 1, 64
+    g = np.random.default_rng(36)
+    Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
+               for _ in range(3))
+    got = _run(hip, be, Q, K, V, heads, hd)
+    rows = np.sort(g.choice(n, 128, replace=False))
+    want = orc.attend(Q[rows], K, V, heads, hd)
+    assert report("many splits %s" % be.precision, got[rows], want) <= TOL[be.precision]

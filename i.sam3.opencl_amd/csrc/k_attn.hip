@@ -530,6 +530,11 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     const uint16_t *Vu = vt16 + unit * 64 * Npk;
     const float *kn = knorm + unit * nblk;
     const int qi = tile * 128 + w * 32 + l32;
+    /* A wave whose 32 queries all lie past N (the second half of a
+     * 64-query tail tile) still fills its share of the K / V staging and
+     * meets every barrier, but issues no MFMA or softmax work, leaving its
+     * SIMD to the co-resident waves. */
+    const bool idle = tile * 128 + __builtin_amdgcn_readfirstlane(w) * 32 >= N;
     /* This lane's row of the additive bias table (exp2 domain, -inf past
      * Nk), if any; queries past N read the last row (never stored). */
     const float *brow = EXT && d.bias
@@ -542,25 +547,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     SoftState st;
     float qn; /* |q| of this lane's query, rounded up */
     bool fresh = true, shifted = false; /* shifted: some lane's m != 0 */
-
-    for (int s = 0; s < 4; s++) {
-        if (qi < Np)
-            qb[s] = *(const bf16x8 *)(Qu + (long)qi * 64 + 16 * s + 8 * h);
-        else
-            for (int e = 0; e < 8; e++)
-                qb[s][e] = (__bf16)0.0f;
-    }
-    qn = 0.0f;
-    for (int s = 0; s < 4; s++)
-        for (int e = 0; e < 8; e++)
-            qn = fmaf((float)qb[s][e], (float)qb[s][e], qn);
-    qn = sqrtf(qn + __shfl_xor(qn, 32, 64)) * (1.0f + 0x1p-10f);
-    for (int r = 0; r < 16; r++) {
-        st.o0[r] = 0.0f;
-        st.o1[r] = 0.0f;
-    }
-    st.m = 0.0f;
-    st.l = 0.0f;
 
     /* Async copy of block kb into `slot`: wave w, pass j fills LDS rows
      * 8 (2 w + j) .. +7; lane i lands on row + i / 8, physical chunk
@@ -600,6 +586,25 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     float kn_next = kn[kb0];
 
     load_block(kb0, 0);
+    for (int s = 0; s < 4; s++) {
+        if (qi < Np)
+            qb[s] = *(const bf16x8 *)(Qu + (long)qi * 64 + 16 * s + 8 * h);
+        else
+            for (int e = 0; e < 8; e++)
+                qb[s][e] = (__bf16)0.0f;
+    }
+    qn = 0.0f;
+    for (int s = 0; s < 4; s++)
+        for (int e = 0; e < 8; e++)
+            qn = fmaf((float)qb[s][e], (float)qb[s][e], qn);
+    qn = sqrtf(qn + __shfl_xor(qn, 32, 64)) * (1.0f + 0x1p-10f);
+    for (int r = 0; r < 16; r++) {
+        st.o0[r] = 0.0f;
+        st.o1[r] = 0.0f;
+    }
+    st.m = 0.0f;
+    st.l = 0.0f;
+
     /* Unrolled by two so that the slot is a constant: the LDS fragment
      * addresses are then one register plus an immediate offset. */
     auto block = [&](int kb, auto slot_c) {
@@ -617,6 +622,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         kn_next = kn[kb + 1 < kb1 ? kb + 1 : kb];
         if (kb + 1 < kb1)
             load_block(kb + 1, slot ^ 1);
+        if (idle)
+            return;
         for (int c = 0; c < 2; c++)
             for (int ds = 0; ds < 4; ds++)
                 kf[4 * c + ds] = *(const bf16x8 *)(Kb + 8192 * slot + 4096 * c + kro[ds]);
@@ -769,7 +776,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                     const f32x4 v = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
                     if (q0 + row < N)
-                        *(f32x4 *)((float *)Obuf + obase + (long)(q0 + row) * ldo + 32 * half + 4 * c) = v;
+                        __builtin_nontemporal_store(
+                            v, (f32x4 *)((float *)Obuf + obase + (long)(q0 + row) * ldo + 32 * half + 4 * c));
                 }
             }
         }

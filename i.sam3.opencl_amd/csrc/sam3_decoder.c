@@ -1,0 +1,553 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * sam3_decoder.c - the point-prompt mask decoder on HIP: prompt tokens,
+ * the two-way transformer (self attention, token -> image and image ->
+ * token attention, token MLP), the output upscaling, the hypernetwork
+ * and IoU heads, the low-resolution logits and the postprocessing
+ * (sam3_model.c:1212-1530), over the operators of sam3_ops.c.
+ *
+ * The host-side parts (prompt encoding, the small MLP heads, hole
+ * filling) are plain C as in the reference; the tensor work is queued on
+ * the backend's stream.
+ */
+#include "hipb_internal.h"
+#include "sam3_launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define NTOK 8         /* prompt tokens per prompt (sam3_model.c:35) */
+#define DEC_EPS 1e-5f  /* decoder LayerNorm eps (sam3_model.c:31) */
+#define LN2D_EPS 1e-6f /* LayerNorm2d of the upscaling (sam3_model.c:32) */
+
+/* PositionEmbeddingRandom of normalized (x, y) in [0, 1]
+ * (sam3_model.c:760-773). */
+static void pe_encode(const struct sam_decoder *d, float x, float y,
+                      float *out)
+{
+    int i;
+
+    x = 2.0f * x - 1.0f;
+    y = 2.0f * y - 1.0f;
+    for (i = 0; i < SAM_DIM / 2; i++) {
+        float v = x * d->gauss[i] + y * d->gauss[SAM_DIM / 2 + i];
+
+        v *= 2.0f * (float)M_PI;
+        out[i] = sinf(v);
+        out[SAM_DIM / 2 + i] = cosf(v);
+    }
+}
+
+/* y = W x + b with double accumulation, optional ReLU
+ * (host_linear, sam3_model.c:1185-1198). */
+static void host_linear(const float *W, const float *b, const float *x,
+                        int nin, int nout, int relu, float *y)
+{
+    int o, i;
+
+    for (o = 0; o < nout; o++) {
+        const float *w = W + (long)o * nin;
+        double acc = b[o];
+
+        for (i = 0; i < nin; i++)
+            acc += (double)w[i] * x[i];
+        y[o] = relu && acc < 0.0 ? 0.0f : (float)acc;
+    }
+}
+
+static void host_mlp3(float *const W[3], float *const B[3], const float *x,
+                      int nout, float *y)
+{
+    float h1[SAM_DIM], h2[SAM_DIM];
+
+    host_linear(W[0], B[0], x, SAM_DIM, SAM_DIM, 1, h1);
+    host_linear(W[1], B[1], h1, SAM_DIM, SAM_DIM, 1, h2);
+    host_linear(W[2], B[2], h2, SAM_DIM, nout, 0, y);
+}
+
+static hipb_mem dalloc(struct sam_model *m, size_t floats, const char *what)
+{
+    return hipb_alloc(m->hip, floats * sizeof(float), what);
+}
+
+void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
+{
+    const long G = m->grid, T = G * G, P = batch;
+    float *pe;
+    long x, y;
+
+    if (G < 1 || batch < 1 || d->img < 1) {
+        hipb_fatal("sam_dec_init: invalid grid %ld, batch %d or image side %d",
+                   G, batch, d->img);
+        return;
+    }
+    m->dec = d;
+    d->batch = batch;
+    d->src = dalloc(m, T * SAM_DIM, "decoder src");
+    d->srcpe = dalloc(m, T * SAM_DIM, "decoder src+pe");
+    d->kp0 = dalloc(m, T * 128, "decoder k0");
+    d->vp0 = dalloc(m, T * 128, "decoder v0");
+    d->qp0 = dalloc(m, T * 128, "decoder q0");
+    pe = malloc(T * SAM_DIM * sizeof(float));
+    for (y = 0; y < G; y++)
+        for (x = 0; x < G; x++)
+            pe_encode(d, (x + 0.5f) / G, (y + 0.5f) / G,
+                      pe + (y * G + x) * SAM_DIM);
+    d->pe_img = hipb_upload(m->hip, pe, T * SAM_DIM * sizeof(float),
+                            "decoder pe");
+    free(pe);
+    d->qpe = dalloc(m, P * NTOK * SAM_DIM, "query pe");
+    d->qry = dalloc(m, P * NTOK * SAM_DIM, "queries");
+    d->qin = dalloc(m, P * NTOK * SAM_DIM, "queries+pe");
+    d->sq = dalloc(m, P * NTOK * SAM_DIM, "token q");
+    d->sk = dalloc(m, P * NTOK * SAM_DIM, "token k");
+    d->sv = dalloc(m, P * NTOK * SAM_DIM, "token v");
+    d->so = dalloc(m, P * NTOK * SAM_DIM, "token attention");
+    d->sh = dalloc(m, P * NTOK * 2048, "token mlp");
+    d->keys = dalloc(m, P * T * SAM_DIM, "keys");
+    d->kin = dalloc(m, P * T * SAM_DIM, "keys+pe");
+    d->bq = dalloc(m, P * T * 128, "image q");
+    d->bk = dalloc(m, P * T * 128, "image k");
+    d->bv = dalloc(m, P * T * 128, "image v");
+    d->bo = dalloc(m, P * T * 128, "image attention");
+    d->u1 = dalloc(m, P * 4 * T * 64, "upscaling 1");
+    d->g2 = dalloc(m, P * 4 * T * 128, "upscaling 2 gemm");
+    d->u2 = dalloc(m, P * 16 * T * 32, "upscaling 2");
+    d->hyper = dalloc(m, P * 3 * 32, "hypernetwork");
+    d->lowres = dalloc(m, P * 3 * 16 * T, "low-res masks");
+    d->h_queries = malloc(P * NTOK * SAM_DIM * sizeof(float));
+    d->h_lowres = malloc(P * 3 * 16 * T * sizeof(float));
+    d->sel = hipb_alloc(m->hip, P * 3 * sizeof(int), "mask selection");
+    d->stats = hipb_alloc(m->hip, P * 3 * 6 * sizeof(int), "mask statistics");
+    d->mask = NULL;
+    d->mask_cap = 0;
+}
+
+void sam_dec_free(struct sam_model *m)
+{
+    struct sam_decoder *d = m->dec;
+    size_t i;
+
+    if (!d)
+        return;
+    hipb_mem *bufs[] = {&d->src, &d->pe_img, &d->srcpe, &d->kp0, &d->vp0,
+                        &d->qp0, &d->qpe, &d->qry, &d->qin, &d->sq, &d->sk,
+                        &d->sv, &d->so, &d->sh, &d->keys, &d->kin, &d->bq,
+                        &d->bk, &d->bv, &d->bo, &d->u1, &d->g2, &d->u2,
+                        &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats};
+
+    if (m->hip)
+        hipb_finish(m->hip);
+    for (i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+        hipb_release(bufs[i]);
+    free(d->h_queries);
+    free(d->h_lowres);
+    d->h_queries = d->h_lowres = NULL;
+    d->mask_cap = 0;
+    m->dec = NULL;
+}
+
+static struct sam_decoder *dec_of(struct sam_model *m, const char *op)
+{
+    if (!m->dec)
+        hipb_fatal("%s: no decoder (sam_dec_init)", op);
+    return m->dec;
+}
+
+void sam_dec_prepare(struct sam_model *m)
+{
+    struct sam_decoder *d = dec_of(m, "sam_dec_prepare");
+    const long T = (long)m->grid * m->grid;
+    const struct sam_dec_layer *L0;
+    hipb_mem nm;
+
+    if (!d)
+        return;
+    L0 = &d->layers[0];
+    nm = hipb_upload(m->hip, d->no_mask, SAM_DIM * sizeof(float),
+                     "no-mask embedding");
+    if (!nm)
+        return;
+    add_bcast(m, d->src, d->emb, nm, T * SAM_DIM, SAM_DIM);
+    add_bcast(m, d->srcpe, d->src, d->pe_img, T * SAM_DIM, T * SAM_DIM);
+    linear(m, (int)T, SAM_DIM, 128, d->srcpe, 0, L0->t2i.kw, L0->t2i.kb,
+           d->kp0, 0, ACT_NONE, 0);
+    linear(m, (int)T, SAM_DIM, 128, d->src, 0, L0->t2i.vw, L0->t2i.vb, d->vp0,
+           0, ACT_NONE, 0);
+    linear(m, (int)T, SAM_DIM, 128, d->srcpe, 0, L0->i2t.qw, L0->i2t.qb,
+           d->qp0, 0, ACT_NONE, 0);
+    hipb_finish(m->hip);
+    hipb_release(&nm);
+}
+
+void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a)
+{
+    struct sam_decoder *d = dec_of(m, "t2i_attention");
+    const long T = (long)m->grid * m->grid, n = (long)P * NTOK * SAM_DIM;
+
+    if (!d)
+        return;
+    if (P < 1 || P > d->batch) {
+        hipb_fatal("t2i_attention: %d prompts for a batch of %d", P,
+                   d->batch);
+        return;
+    }
+    add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+    add_bcast(m, d->kin, d->keys, d->pe_img, P * T * SAM_DIM, T * SAM_DIM);
+    linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, a->qw, a->qb, d->sq, 0,
+           ACT_NONE, 0);
+    linear(m, (int)(P * T), SAM_DIM, 128, d->kin, 0, a->kw, a->kb, d->bk, 0,
+           ACT_NONE, 0);
+    linear(m, (int)(P * T), SAM_DIM, 128, d->keys, 0, a->vw, a->vb, d->bv, 0,
+           ACT_NONE, 0);
+    mha(m, P, NTOK, (int)T, 128, d->sq, NTOK * 128, d->bk, T * 128, d->bv,
+        T * 128, d->so);
+    linear(m, P * NTOK, 128, SAM_DIM, d->so, 0, a->ow, a->ob, d->qry, 0,
+           ACT_NONE, 1);
+}
+
+void i2t_attention(struct sam_model *m, int layer, int P)
+{
+    struct sam_decoder *d = dec_of(m, "i2t_attention");
+    const long T = (long)m->grid * m->grid, n = (long)P * NTOK * SAM_DIM;
+    const struct sam_dec_layer *L;
+
+    if (!d)
+        return;
+    if (P < 1 || P > d->batch || layer < 0 || layer > 1) {
+        hipb_fatal("i2t_attention: layer %d, %d prompts for a batch of %d",
+                   layer, P, d->batch);
+        return;
+    }
+    L = &d->layers[layer];
+    add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+    if (layer == 0) {
+        linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, L->i2t.kw, L->i2t.kb,
+               d->sk, 0, ACT_NONE, 0);
+        linear(m, P * NTOK, SAM_DIM, 128, d->qry, 0, L->i2t.vw, L->i2t.vb,
+               d->sv, 0, ACT_NONE, 0);
+        mha(m, P, (int)T, NTOK, 128, d->qp0, 0, d->sk, NTOK * 128, d->sv,
+            NTOK * 128, d->bo);
+        linear(m, (int)(P * T), 128, SAM_DIM, d->bo, 0, L->i2t.ow, L->i2t.ob,
+               d->keys, 0, ACT_NONE, 0);
+        add_bcast(m, d->keys, d->keys, d->src, P * T * SAM_DIM, T * SAM_DIM);
+    }
+    else {
+        linear(m, (int)(P * T), SAM_DIM, 128, d->kin, 0, L->i2t.qw,
+               L->i2t.qb, d->bq, 0, ACT_NONE, 0);
+        linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, L->i2t.kw, L->i2t.kb,
+               d->sk, 0, ACT_NONE, 0);
+        linear(m, P * NTOK, SAM_DIM, 128, d->qry, 0, L->i2t.vw, L->i2t.vb,
+               d->sv, 0, ACT_NONE, 0);
+        mha(m, P, (int)T, NTOK, 128, d->bq, T * 128, d->sk, NTOK * 128,
+            d->sv, NTOK * 128, d->bo);
+        linear(m, (int)(P * T), 128, SAM_DIM, d->bo, 0, L->i2t.ow, L->i2t.ob,
+               d->keys, 0, ACT_NONE, 1);
+    }
+    layernorm(m, P * T, SAM_DIM, d->keys, d->keys, L->n4w, L->n4b, DEC_EPS,
+              ACT_NONE);
+}
+
+/* Prompt-token self attention (sam3_model.c:1274-1286 for layer 0, no
+ * positional encoding and no residual; 1316-1327 for layer 1), norm1. */
+static void self_attention(struct sam_model *m, int layer, int P)
+{
+    struct sam_decoder *d = m->dec;
+    const struct sam_dec_layer *L = &d->layers[layer];
+    const long n = (long)P * NTOK * SAM_DIM;
+    hipb_mem qk = d->qry;
+
+    if (layer) {
+        add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+        qk = d->qin;
+    }
+    linear(m, P * NTOK, SAM_DIM, SAM_DIM, qk, 0, L->self.qw, L->self.qb,
+           d->sq, 0, ACT_NONE, 0);
+    linear(m, P * NTOK, SAM_DIM, SAM_DIM, qk, 0, L->self.kw, L->self.kb,
+           d->sk, 0, ACT_NONE, 0);
+    linear(m, P * NTOK, SAM_DIM, SAM_DIM, d->qry, 0, L->self.vw, L->self.vb,
+           d->sv, 0, ACT_NONE, 0);
+    mha(m, P, NTOK, NTOK, SAM_DIM, d->sq, NTOK * SAM_DIM, d->sk,
+        NTOK * SAM_DIM, d->sv, NTOK * SAM_DIM, d->so);
+    linear(m, P * NTOK, SAM_DIM, SAM_DIM, d->so, 0, L->self.ow, L->self.ob,
+           d->qry, 0, ACT_NONE, layer);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, L->n1w, L->n1b, DEC_EPS,
+              ACT_NONE);
+}
+
+static void token_mlp(struct sam_model *m, int P,
+                      const struct sam_dec_layer *L)
+{
+    struct sam_decoder *d = m->dec;
+
+    linear(m, P * NTOK, SAM_DIM, 2048, d->qry, 0, L->m1w, L->m1b, d->sh, 0,
+           ACT_RELU, 0);
+    linear(m, P * NTOK, 2048, SAM_DIM, d->sh, 0, L->m2w, L->m2b, d->qry, 0,
+           ACT_NONE, 1);
+}
+
+void convt_scatter(struct sam_model *m, hipb_mem G, hipb_mem out,
+                   hipb_mem bias, hipb_mem add, int P, int H, int W, int Co,
+                   int act)
+{
+    struct hipb_backend *be = m->hip;
+    const size_t total = (size_t)P * 4 * H * W * Co;
+    int err;
+
+    if (P < 1 || H < 1 || W < 1 || Co < 1 || act < ACT_NONE ||
+        act > ACT_RELU) {
+        hipb_fatal("convt_scatter: invalid shape P=%d H=%d W=%d Co=%d", P, H,
+                   W, Co);
+        return;
+    }
+    if (!G || !out || !bias || G->dtype != HIPB_F32 ||
+        out->dtype != HIPB_F32 || hipb_count(G) < total ||
+        hipb_count(out) < total || hipb_count(bias) < (size_t)Co ||
+        (add && hipb_count(add) < (size_t)4 * H * W * Co)) {
+        hipb_fatal("convt_scatter: operand missing or too small");
+        return;
+    }
+    hipb_run_begin(be);
+    err = launch_convt_scatter(G->ptr, out->ptr, bias->ptr,
+                               add ? add->ptr : NULL, P, H, W, Co, act,
+                               be->stream);
+    hipb_run_end(be, err, "convt_scatter", 0.0);
+}
+
+void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
+{
+    struct sam_decoder *d = dec_of(m, "sam_decode");
+    const int G = m->grid;
+    const long T = (long)G * G, n = (long)P * NTOK * SAM_DIM;
+    const struct sam_dec_layer *L0, *L1;
+    float *tok, *hyper;
+    int p, i, err;
+
+    if (!d)
+        return;
+    if (P < 1 || P > d->batch) {
+        hipb_fatal("sam_decode: batch overflow");
+        return;
+    }
+    L0 = &d->layers[0];
+    L1 = &d->layers[1];
+    tok = d->h_queries;
+
+    /* Prompt tokens: object score token, IoU token, 4 mask tokens, the
+     * positive point and the padding point (no box prompt). */
+    for (p = 0; p < P; p++) {
+        float *t = tok + (long)p * NTOK * SAM_DIM;
+
+        memcpy(t, d->obj_token, SAM_DIM * sizeof(float));
+        memcpy(t + SAM_DIM, d->iou_token, SAM_DIM * sizeof(float));
+        memcpy(t + 2 * SAM_DIM, d->mask_tokens, 4 * SAM_DIM * sizeof(float));
+        pe_encode(d, (points[2 * p] + 0.5f) / d->img,
+                  (points[2 * p + 1] + 0.5f) / d->img, t + 6 * SAM_DIM);
+        for (i = 0; i < SAM_DIM; i++) {
+            t[6 * SAM_DIM + i] += d->point_emb[1][i];
+            t[7 * SAM_DIM + i] = d->not_a_point[i];
+        }
+    }
+    hipb_write(m->hip, d->qpe, 0, tok, n * sizeof(float));
+    hipb_copy(m->hip, d->qpe, d->qry, 0, 0, n * sizeof(float));
+
+    /* Layer 0: self attention, token -> image attention on the shared
+     * image keys (stride 0), token MLP, image -> token attention. */
+    self_attention(m, 0, P);
+    add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+    linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, L0->t2i.qw, L0->t2i.qb,
+           d->sq, 0, ACT_NONE, 0);
+    mha(m, P, NTOK, (int)T, 128, d->sq, NTOK * 128, d->kp0, 0, d->vp0, 0,
+        d->so);
+    linear(m, P * NTOK, 128, SAM_DIM, d->so, 0, L0->t2i.ow, L0->t2i.ob,
+           d->qry, 0, ACT_NONE, 1);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, L0->n2w, L0->n2b,
+              DEC_EPS, ACT_NONE);
+    token_mlp(m, P, L0);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, L0->n3w, L0->n3b,
+              DEC_EPS, ACT_NONE);
+    i2t_attention(m, 0, P);
+
+    /* Layer 1. */
+    self_attention(m, 1, P);
+    t2i_attention(m, P, &L1->t2i);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, L1->n2w, L1->n2b,
+              DEC_EPS, ACT_NONE);
+    token_mlp(m, P, L1);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, L1->n3w, L1->n3b,
+              DEC_EPS, ACT_NONE);
+    i2t_attention(m, 1, P);
+
+    /* Final token -> image attention. */
+    t2i_attention(m, P, &d->final_t2i);
+    layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, d->nfw, d->nfb, DEC_EPS,
+              ACT_NONE);
+
+    /* Output upscaling: ConvT 256 -> 64 + feat_s1, LayerNorm2d, GELU,
+     * ConvT 64 -> 32 + feat_s0, GELU (the kin buffer holds the first
+     * GEMM). */
+    gemm(m, (int)(P * T), 256, SAM_DIM, mat(d->keys, 0, SAM_DIM),
+         mat(d->up0w, 0, 256), 0, mat(d->kin, 0, 256), 1, 1, NULL, NULL, 0,
+         1.0f, ACT_NONE);
+    convt_scatter(m, d->kin, d->u1, d->up0b, d->feat_s1, P, G, G, 64,
+                  ACT_NONE);
+    layernorm(m, P * 4 * T, 64, d->u1, d->u1, d->up1w, d->up1b, LN2D_EPS,
+              ACT_GELU);
+    gemm(m, (int)(P * 4 * T), 128, 64, mat(d->u1, 0, 64), mat(d->up3w, 0, 128),
+         0, mat(d->g2, 0, 128), 1, 1, NULL, NULL, 0, 1.0f, ACT_NONE);
+    convt_scatter(m, d->g2, d->u2, d->up3b, d->feat_s0, P, 2 * G, 2 * G, 32,
+                  ACT_GELU);
+    if (hipb_failed())
+        return;
+
+    /* Hypernetwork MLPs of mask tokens 1..3 and the IoU head (sigmoid) on
+     * the host. */
+    hipb_read(m->hip, d->qry, 0, tok, n * sizeof(float));
+    hyper = malloc((size_t)P * 96 * sizeof(float));
+    for (p = 0; p < P; p++) {
+        const float *t = tok + (long)p * NTOK * SAM_DIM;
+        float out[4];
+
+        for (i = 1; i <= 3; i++)
+            host_mlp3(d->hyper_w[i], d->hyper_b[i], t + (2 + i) * SAM_DIM,
+                      32, hyper + (long)p * 96 + (i - 1) * 32);
+        host_mlp3(d->iou_w, d->iou_b, t + SAM_DIM, 4, out);
+        for (i = 0; i < 3; i++)
+            iou[p * 3 + i] = 1.0f / (1.0f + expf(-out[1 + i]));
+    }
+    hipb_write(m->hip, d->hyper, 0, hyper, (size_t)P * 96 * sizeof(float));
+    free(hyper);
+
+    hipb_run_begin(m->hip);
+    err = launch_mask_logits(d->u2->ptr, d->hyper->ptr, d->lowres->ptr, P,
+                             (int)(16 * T), m->hip->stream);
+    hipb_run_end(m->hip, err, "mask_logits", 0.0);
+}
+
+/* Background components (v <= 0, 8-connected) of at most max_area pixels
+ * of an L x L map become 10 (fill_holes, sam3_model.c:1406-1443). lab and
+ * queue hold L^2 ints each. Returns 1 if the map changed. */
+static int fill_holes(float *v, int L, int max_area, int *lab, int *queue)
+{
+    const int n = L * L;
+    int i, changed = 0;
+
+    memset(lab, 0, n * sizeof(int));
+    for (i = 0; i < n; i++) {
+        int sp = 0, j;
+
+        if (lab[i] || v[i] > 0.0f)
+            continue;
+        lab[i] = 1;
+        queue[sp++] = i;
+        /* Breadth first; the queue ends up holding the component. */
+        for (j = 0; j < sp; j++) {
+            const int c = queue[j], cx = c % L, cy = c / L;
+            int dy, dx;
+
+            for (dy = -1; dy <= 1; dy++)
+                for (dx = -1; dx <= 1; dx++) {
+                    const int nx = cx + dx, ny = cy + dy;
+
+                    if (nx < 0 || ny < 0 || nx >= L || ny >= L ||
+                        lab[ny * L + nx] || v[ny * L + nx] > 0.0f)
+                        continue;
+                    lab[ny * L + nx] = 1;
+                    queue[sp++] = ny * L + nx;
+                }
+        }
+        if (sp <= max_area) {
+            for (j = 0; j < sp; j++)
+                v[queue[j]] = 10.0f;
+            changed = 1;
+        }
+    }
+    return changed;
+}
+
+void sam_postprocess(struct sam_model *m, int n, const int *sel, int out_h,
+                     int out_w, float offset, int fill, int *stats)
+{
+    struct sam_decoder *d = dec_of(m, "sam_postprocess");
+    const int L = 4 * m->grid;
+    const size_t plane = (size_t)L * L * sizeof(float);
+    const size_t need = (size_t)n * out_h * out_w;
+    int i, err;
+
+    if (!d || n <= 0)
+        return;
+    if (n > 3 * d->batch || out_h < 1 || out_w < 1) {
+        hipb_fatal("sam_postprocess: %d masks of %d x %d", n, out_h, out_w);
+        return;
+    }
+    for (i = 0; i < n; i++)
+        if (sel[i] < 0 || (size_t)sel[i] >= hipb_count(d->lowres) / (L * L)) {
+            hipb_fatal("sam_postprocess: plane %d out of range", sel[i]);
+            return;
+        }
+    if (fill) {
+        int *lab = malloc((size_t)L * L * sizeof(int));
+        int *queue = malloc((size_t)L * L * sizeof(int));
+
+        for (i = 0; i < n; i++) {
+            float *v = d->h_lowres + (size_t)i * L * L;
+
+            hipb_read(m->hip, d->lowres, sel[i] * plane, v, plane);
+            if (fill_holes(v, L, SAM_HOLE, lab, queue))
+                hipb_write(m->hip, d->lowres, sel[i] * plane, v, plane);
+        }
+        free(lab);
+        free(queue);
+    }
+    if (need > d->mask_cap) {
+        hipb_release(&d->mask);
+        d->mask = hipb_alloc(m->hip, need, "postprocessed masks");
+        if (!d->mask)
+            return;
+        d->mask_cap = need;
+    }
+    for (i = 0; i < n; i++) {
+        stats[6 * i + 0] = 0;
+        stats[6 * i + 1] = 0;
+        stats[6 * i + 2] = 0x7fffffff;
+        stats[6 * i + 3] = 0x7fffffff;
+        stats[6 * i + 4] = -1;
+        stats[6 * i + 5] = -1;
+    }
+    hipb_write(m->hip, d->sel, 0, sel, n * sizeof(int));
+    hipb_write(m->hip, d->stats, 0, stats, 6 * n * sizeof(int));
+    hipb_run_begin(m->hip);
+    err = launch_mask_post(d->lowres->ptr, d->sel->ptr, n, L, out_h, out_w,
+                           offset, d->mask->ptr, d->stats->ptr,
+                           m->hip->stream);
+    hipb_run_end(m->hip, err, "mask_post", 0.0);
+    hipb_read(m->hip, d->stats, 0, stats, 6 * n * sizeof(int));
+}
+
+void sam_read_mask(struct sam_model *m, int k, int out_h, int out_w, int x0,
+                   int y0, int x1, int y1, unsigned char *dst)
+{
+    struct sam_decoder *d = dec_of(m, "sam_read_mask");
+    const int w = x1 - x0 + 1;
+    hipError_t err;
+
+    if (!d)
+        return;
+    if (!d->mask || k < 0 || x0 < 0 || y0 < 0 || x1 < x0 || y1 < y0 ||
+        x1 >= out_w || y1 >= out_h ||
+        (size_t)(k + 1) * out_h * out_w > d->mask_cap) {
+        hipb_fatal("sam_read_mask: region outside the postprocessed masks");
+        return;
+    }
+    err = hipMemcpy2DAsync(dst, (size_t)w,
+                           (const char *)d->mask->ptr +
+                               ((size_t)k * out_h + y0) * out_w + x0,
+                           (size_t)out_w, (size_t)w, (size_t)(y1 - y0 + 1),
+                           hipMemcpyDeviceToHost, (hipStream_t)m->hip->stream);
+    if (err == hipSuccess)
+        err = hipStreamSynchronize((hipStream_t)m->hip->stream);
+    hipb_check(err, "hipMemcpy2DAsync");
+}

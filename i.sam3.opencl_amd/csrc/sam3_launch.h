@@ -172,6 +172,22 @@ int launch_mha_manykeys(const float *Q, long sq, const float *K, long sk,
                         int Nk, int dint, float scale, void *scratch,
                         void *stream);
 
+/* Output upscaling scatter of a 2x2 / stride-2 transposed convolution:
+ * G [(P H W)][Co 4] -> out [P][2H][2W][Co] = act(G + bias[co] (+ add,
+ * [2H][2W][Co] shared by the prompts)). */
+int launch_convt_scatter(const float *G, float *out, const float *bias,
+                         const float *add, int P, int H, int W, int Co,
+                         int act, void *stream);
+/* Low-resolution logits out [P][3][npix] = hyper [P][3][32] . U [P][npix][32]. */
+int launch_mask_logits(const float *U, const float *hyper, float *out, int P,
+                       int npix, void *stream);
+/* Bilinear resize of n selected L x L logit planes to out_h x out_w
+ * binary masks, with per-mask counts and bounding boxes accumulated into
+ * stats [n][6] (initialised by the caller). */
+int launch_mask_post(const float *lowres, const int *sel, int n, int L,
+                     int out_h, int out_w, float offset, unsigned char *mask,
+                     int *stats, void *stream);
+
 /* fp32 -> bf16 / half conversion of count elements (weight uploads). */
 int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
                    void *stream);

@@ -1242,6 +1242,8 @@ void sam_path_init(struct sam_model *m, struct hipb_backend *b, int grid,
 
 void sam_path_free(struct sam_model *m)
 {
+    if (m->dec)
+        sam_dec_free(m);
     if (m->hip)
         hipb_finish(m->hip);
     trunk_graph_drop(m);

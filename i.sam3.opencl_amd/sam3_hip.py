@@ -34,7 +34,9 @@ EXPORTS = [
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
     "window_partition", "window_unpartition_add", "mha", "attn_fused",
     "attn_packed", "vit_attention", "vit_block", "sam_encode_trunk",
-    "sam_trunk_graph", "softmax_ext", "attend",
+    "sam_trunk_graph", "softmax_ext", "attend", "sam_dec_init",
+    "sam_dec_free", "sam_dec_prepare", "sam_decode", "t2i_attention",
+    "i2t_attention", "convt_scatter", "sam_postprocess", "sam_read_mask",
 ]
 
 
@@ -88,7 +90,46 @@ class SamModel(ctypes.Structure):
                             "mlpbuf", "mlp16")] + \
         [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
          ("trunk_gen", ctypes.c_ulong), ("abias", Mem),
-         ("apart", Mem)]
+         ("apart", Mem), ("dec", ctypes.c_void_p)]
+
+
+_FP = ctypes.POINTER(ctypes.c_float)
+_ATT = ("qw", "qb", "kw", "kb", "vw", "vb", "ow", "ob")
+_LAYER = ("n1w", "n1b", "n2w", "n2b", "n3w", "n3b", "n4w", "n4b", "m1w",
+          "m1b", "m2w", "m2b")
+_DEC_BUFS = ("emb", "feat_s0", "feat_s1", "src", "pe_img", "srcpe", "kp0",
+             "vp0", "qp0", "qpe", "qry", "qin", "sq", "sk", "sv", "so", "sh",
+             "keys", "kin", "bq", "bk", "bv", "bo", "u1", "g2", "u2", "hyper",
+             "lowres")
+
+
+class SamAttnW(ctypes.Structure):
+    _fields_ = [(n, Mem) for n in _ATT] + [("dint", ctypes.c_int)]
+
+
+class SamDecLayer(ctypes.Structure):
+    _fields_ = [("self_", SamAttnW), ("t2i", SamAttnW), ("i2t", SamAttnW)] + \
+        [(n, Mem) for n in _LAYER]
+
+
+class SamDecoder(ctypes.Structure):
+    _fields_ = [("img", ctypes.c_int), ("batch", ctypes.c_int),
+                ("gauss", ctypes.c_float * 256),
+                ("point_emb", ctypes.c_float * 1024),
+                ("not_a_point", ctypes.c_float * 256),
+                ("no_mask", ctypes.c_float * 256),
+                ("layers", SamDecLayer * 2), ("final_t2i", SamAttnW)] + \
+        [(n, Mem) for n in ("nfw", "nfb", "up0w", "up0b", "up1w", "up1b",
+                            "up3w", "up3b")] + \
+        [("obj_token", ctypes.c_float * 256),
+         ("iou_token", ctypes.c_float * 256),
+         ("mask_tokens", ctypes.c_float * 1024),
+         ("hyper_w", (_FP * 3) * 4), ("hyper_b", (_FP * 3) * 4),
+         ("iou_w", _FP * 3), ("iou_b", _FP * 3)] + \
+        [(n, Mem) for n in _DEC_BUFS] + \
+        [("h_queries", _FP), ("h_lowres", _FP)] + \
+        [(n, Mem) for n in ("mask", "sel", "stats")] + \
+        [("mask_cap", ctypes.c_size_t)]
 
 
 _lib = None
@@ -171,6 +212,19 @@ def lib():
     L.vit_block.argtypes = [MP, ctypes.POINTER(VitBlock), c_int]
     L.sam_encode_trunk.argtypes = [MP, ctypes.c_void_p]
     L.sam_trunk_graph.argtypes = [MP, c_int]
+    DP = ctypes.POINTER(SamDecoder)
+    L.sam_dec_init.argtypes = [MP, DP, c_int]
+    L.sam_dec_free.argtypes = [MP]
+    L.sam_dec_prepare.argtypes = [MP]
+    L.sam_decode.argtypes = [MP, c_int, vp, vp]
+    L.t2i_attention.argtypes = [MP, c_int, ctypes.POINTER(SamAttnW)]
+    L.i2t_attention.argtypes = [MP, c_int, c_int]
+    L.convt_scatter.argtypes = [MP, Mem, Mem, Mem, Mem, c_int, c_int, c_int,
+                                c_int, c_int]
+    L.sam_postprocess.argtypes = [MP, c_int, vp, c_int, c_int, c_float, c_int,
+                                  vp]
+    L.sam_read_mask.argtypes = [MP, c_int, c_int, c_int, c_int, c_int, c_int,
+                                c_int, vp]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
     return L
@@ -442,3 +496,189 @@ def prof_table():
 
 def prof_reset():
     _lib.hipb_prof_reset()
+
+
+# ---------------------------------------------------------------- decoder
+
+def random_decoder_weights(seed):
+    """Synthetic random-init weights of the point-prompt head's prompt
+    encoder and mask decoder, named like the fields of struct sam_decoder
+    (no checkpoint is available): Linear / ConvTranspose weights and biases
+    U(+-1 / sqrt(fan_in)), LayerNorm weights 1 + 0.1 N(0, 1) and biases
+    0.1 N(0, 1), embeddings and the Gaussian matrix N(0, 1)."""
+    g = np.random.default_rng(seed)
+    f32 = np.float32
+
+    def lin(nout, nin):
+        b = 1.0 / np.sqrt(nin)
+        return (g.uniform(-b, b, (nout, nin)).astype(f32),
+                g.uniform(-b, b, nout).astype(f32))
+
+    def norm(n):
+        return ((1 + 0.1 * g.standard_normal(n)).astype(f32),
+                (0.1 * g.standard_normal(n)).astype(f32))
+
+    w = {"gauss": g.standard_normal((2, 128)).astype(f32),
+         "point_emb": g.standard_normal((4, 256)).astype(f32),
+         "not_a_point": g.standard_normal(256).astype(f32),
+         "no_mask": g.standard_normal(256).astype(f32),
+         "obj_token": g.standard_normal(256).astype(f32),
+         "iou_token": g.standard_normal(256).astype(f32),
+         "mask_tokens": g.standard_normal((4, 256)).astype(f32)}
+
+    def attn(prefix, dint):
+        for n, (o, i) in (("q", (dint, 256)), ("k", (dint, 256)),
+                          ("v", (dint, 256)), ("o", (256, dint))):
+            w[prefix + n + "w"], w[prefix + n + "b"] = lin(o, i)
+
+    for layer in range(2):
+        p = "layers.%d." % layer
+        attn(p + "self.", 256)
+        attn(p + "t2i.", 128)
+        attn(p + "i2t.", 128)
+        for k in range(1, 5):
+            w[p + "n%dw" % k], w[p + "n%db" % k] = norm(256)
+        w[p + "m1w"], w[p + "m1b"] = lin(2048, 256)
+        w[p + "m2w"], w[p + "m2b"] = lin(256, 2048)
+    attn("final_t2i.", 128)
+    w["nfw"], w["nfb"] = norm(256)
+    b0, b3 = 1 / 16.0, 1 / 8.0
+    w["up0w"] = g.uniform(-b0, b0, (256, 64 * 4)).astype(f32)
+    w["up0b"] = g.uniform(-b0, b0, 64).astype(f32)
+    w["up1w"], w["up1b"] = norm(64)
+    w["up3w"] = g.uniform(-b3, b3, (64, 32 * 4)).astype(f32)
+    w["up3b"] = g.uniform(-b3, b3, 32).astype(f32)
+    for i in range(4):
+        for j in range(3):
+            w["hyper.%d.%dw" % (i, j)], w["hyper.%d.%db" % (i, j)] = \
+                lin(32 if j == 2 else 256, 256)
+    for j in range(3):
+        w["iou.%dw" % j], w["iou.%db" % j] = lin(4 if j == 2 else 256, 256)
+    return w
+
+
+class Decoder:
+    """struct sam_decoder attached to a Model (sam_dec_init): uploads the
+    weights of `w` (random_decoder_weights' names; matrices with
+    upload_weight, so bf16 on precision=bf16), keeps the host arrays of
+    the MLP heads alive, and wraps the decoder entry points."""
+
+    def __init__(self, model, w, batch, img=1008):
+        be = model.backend
+        self.model, self.be = model, be
+        d = self.d = SamDecoder()
+        self._keep = []
+        self._mems = []
+        d.img = img
+
+        def dev(name, weight=False):
+            a = np.ascontiguousarray(w[name], np.float32)
+            mem = be.upload_weight(a, name) if weight else be.upload(a, name)
+            self._mems.append(mem)
+            return mem
+
+        def host(name):
+            a = np.ascontiguousarray(w[name], np.float32)
+            self._keep.append(a)
+            return a.ctypes.data_as(_FP)
+
+        for name in ("gauss", "point_emb", "not_a_point", "no_mask",
+                     "obj_token", "iou_token", "mask_tokens"):
+            a = np.ascontiguousarray(w[name], np.float32).ravel()
+            ctypes.memmove(getattr(d, name), a.ctypes.data, a.nbytes)
+
+        def attn(dst, prefix, dint):
+            for n in _ATT:
+                setattr(dst, n, dev(prefix + n, n.endswith("w")))
+            dst.dint = dint
+
+        for layer in range(2):
+            p = "layers.%d." % layer
+            L = d.layers[layer]
+            attn(L.self_, p + "self.", 256)
+            attn(L.t2i, p + "t2i.", 128)
+            attn(L.i2t, p + "i2t.", 128)
+            for n in _LAYER:
+                setattr(L, n, dev(p + n, n in ("m1w", "m2w")))
+        attn(d.final_t2i, "final_t2i.", 128)
+        for n in ("nfw", "nfb", "up0b", "up1w", "up1b", "up3b"):
+            setattr(d, n, dev(n))
+        d.up0w = dev("up0w", True)
+        d.up3w = dev("up3w", True)
+        for i in range(4):
+            for j in range(3):
+                d.hyper_w[i][j] = host("hyper.%d.%dw" % (i, j))
+                d.hyper_b[i][j] = host("hyper.%d.%db" % (i, j))
+        for j in range(3):
+            d.iou_w[j] = host("iou.%dw" % j)
+            d.iou_b[j] = host("iou.%db" % j)
+        _call(_lib.sam_dec_init, model.ptr, ctypes.byref(d), batch)
+        self.grid = model.m.grid
+        self.batch = batch
+
+    @property
+    def T(self):
+        return self.grid * self.grid
+
+    def set_image(self, emb, feat_s0, feat_s1):
+        """Upload the image features (emb [grid^2][256], feat_s0 [16
+        grid^2][32], feat_s1 [4 grid^2][64]) and run sam_dec_prepare."""
+        be, d = self.be, self.d
+        for n, a in (("emb", emb), ("feat_s0", feat_s0), ("feat_s1", feat_s1)):
+            old = getattr(d, n)
+            if old:
+                be.release(old)
+            setattr(d, n, be.upload(np.ascontiguousarray(a, np.float32), n))
+        _call(_lib.sam_dec_prepare, self.model.ptr)
+
+    def decode(self, points):
+        """sam_decode; returns iou [P][3]."""
+        pts = np.ascontiguousarray(points, np.float32).reshape(-1, 2)
+        P = pts.shape[0]
+        iou = np.zeros((P, 3), np.float32)
+        _call(_lib.sam_decode, self.model.ptr, P, pts.ctypes.data,
+              iou.ctypes.data)
+        return iou
+
+    def lowres(self, P):
+        L = 4 * self.grid
+        return self.be.read_f32(self.d.lowres, P * 3 * L * L).reshape(
+            P, 3, L, L)
+
+    def buf(self, name):
+        return getattr(self.d, name)
+
+    def postprocess(self, sel, out_h, out_w, offset, fill):
+        sel = np.ascontiguousarray(sel, np.int32)
+        stats = np.zeros((len(sel), 6), np.int32)
+        _call(_lib.sam_postprocess, self.model.ptr, len(sel), sel.ctypes.data,
+              out_h, out_w, offset, int(fill), stats.ctypes.data)
+        return stats
+
+    def read_mask(self, k, out_h, out_w, x0, y0, x1, y1):
+        out = np.zeros((y1 - y0 + 1, x1 - x0 + 1), np.uint8)
+        _call(_lib.sam_read_mask, self.model.ptr, k, out_h, out_w, x0, y0, x1,
+              y1, out.ctypes.data)
+        return out
+
+    def free(self):
+        _lib.sam_dec_free(self.model.ptr)
+        for mem in self._mems + [getattr(self.d, n) for n in ("emb", "feat_s0",
+                                                             "feat_s1")]:
+            if mem:
+                self.be.release(mem)
+        self._mems = []
+        for n in ("emb", "feat_s0", "feat_s1"):
+            setattr(self.d, n, None)
+
+
+def t2i_attention(m, dec, P, a):
+    _call(_lib.t2i_attention, m.ptr, P, ctypes.byref(a))
+
+
+def i2t_attention(m, layer, P):
+    _call(_lib.i2t_attention, m.ptr, layer, P)
+
+
+def convt_scatter(m, G, out, bias, add, P, H, W, Co, act=ACT_NONE):
+    _call(_lib.convt_scatter, m.ptr, G, out, bias, add, P, H, W, Co, act)

@@ -209,6 +209,8 @@ struct sam_model {
     /* Key-split partial records of the bf16 attention ([unit][split][Np]
      * rows of 64 O values, then their (m, l) pairs). */
     hipb_mem apart;
+    /* The point-prompt mask decoder (sam_dec_init), or NULL. */
+    struct sam_decoder *dec;
 };
 
 /* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =
@@ -344,6 +346,109 @@ void sam_encode_trunk(struct sam_model *m, const float *img);
  * one). Profiling (profile=1) always runs the kernels one by one. No
  * counterpart in the reference (whose OpenCL queue has no graphs). */
 void sam_trunk_graph(struct sam_model *m, int enable);
+
+/* ------------------------------------------------------------------ */
+/* Point-prompt mask decoder (sam3_model.c:1212-1517)                  */
+/* ------------------------------------------------------------------ */
+
+#define SAM_DIM 256 /* decoder embedding width (sam3_model.h:12) */
+#define SAM_HOLE 256 /* largest hole filled, pixels (sam3_model.h:14) */
+
+/* Weights of one decoder attention (sam3_model.h:16-19): q/k/v
+ * [dint][256], o [256][dint] (hipb_upload_weight), biases (hipb_upload). */
+struct sam_attn_w {
+    hipb_mem qw, qb, kw, kb, vw, vb, ow, ob;
+    int dint;
+};
+
+/* One two-way transformer layer (sam3_model.h:28-32): mlp lin1
+ * [2048][256], lin2 [256][2048]. */
+struct sam_dec_layer {
+    struct sam_attn_w self, t2i, i2t;
+    hipb_mem n1w, n1b, n2w, n2b, n3w, n3b, n4w, n4b;
+    hipb_mem m1w, m1b, m2w, m2b;
+};
+
+/* The decoder fields of struct sam_model (sam3_model.h:55-75, 100-116).
+ * The caller fills the weights (device: layers, final_t2i, nf*, up*;
+ * host: the prompt encoder tables, tokens and the MLP heads, whose
+ * arrays it keeps alive) and, per image, emb / feat_s0 / feat_s1;
+ * sam_dec_init allocates the rest. up0w [256][64 4] and up3w [64][32 4]
+ * are the ConvTranspose2d weights [in][out][2][2]. hyper_w[i] = {[256]
+ * [256], [256][256], [32][256]}, iou_w = {.., .., [4][256]}. */
+struct sam_decoder {
+    int img;   /* encoder input side, SAM_IMG (points are in its pixels) */
+    int batch; /* prompts per sam_decode call */
+    float gauss[2 * 128];
+    float point_emb[4][SAM_DIM];
+    float not_a_point[SAM_DIM];
+    float no_mask[SAM_DIM];
+    struct sam_dec_layer layers[2];
+    struct sam_attn_w final_t2i;
+    hipb_mem nfw, nfb;
+    hipb_mem up0w, up0b, up1w, up1b, up3w, up3b;
+    float obj_token[SAM_DIM], iou_token[SAM_DIM], mask_tokens[4 * SAM_DIM];
+    float *hyper_w[4][3], *hyper_b[4][3];
+    float *iou_w[3], *iou_b[3];
+    /* Image features [grid^2][256], [16 grid^2][32], [4 grid^2][64]. */
+    hipb_mem emb, feat_s0, feat_s1;
+    /* Per-image caches: src = emb + no_mask, dense PE, src + PE, layer-0
+     * projections of the shared keys / values / image queries. */
+    hipb_mem src, pe_img, srcpe, kp0, vp0, qp0;
+    /* Batch buffers (sam3_model.c:895-916). */
+    hipb_mem qpe, qry, qin, sq, sk, sv, so, sh;
+    hipb_mem keys, kin, bq, bk, bv, bo;
+    hipb_mem u1, g2, u2, hyper, lowres;
+    float *h_queries, *h_lowres;
+    /* Postprocessed masks and their statistics. */
+    hipb_mem mask, sel, stats;
+    size_t mask_cap;
+};
+
+/* Attach decoder d to m (grid from m) and allocate its caches and batch
+ * buffers for `batch` prompts; computes the dense positional encoding
+ * from d->gauss, so call it after filling the prompt-encoder tables. No
+ * counterpart: the reference does this in alloc_buffers
+ * (sam3_model.c:876-916). */
+void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch);
+void sam_dec_free(struct sam_model *m);
+
+/* The decoder part of sam_encode (sam3_model.c:1150-1171): src = emb +
+ * no_mask, srcpe = src + PE, kp0 / vp0 / qp0 layer-0 projections. */
+void sam_dec_prepare(struct sam_model *m);
+
+/* sam_decode (sam3_model.c:1239-1400): P <= batch single-point prompts
+ * (x, y pairs in encoder input pixels); iou [P][3] receives the multimask
+ * IoU predictions, d->lowres the [P][3][4 grid]^2 low-resolution logits. */
+void sam_decode(struct sam_model *m, int P, const float *points, float *iou);
+
+/* Token -> image attention with per-prompt keys and residual into the
+ * queries (static t2i_attention, sam3_model.c:1212-1229); kin = keys +
+ * PE is left in d->kin. */
+void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a);
+
+/* Image -> token attention of decoder layer `layer` with norm4, keys
+ * updated in place (inline in sam_decode: sam3_model.c:1298-1312 for
+ * layer 0, 1330-1345 for layer 1, which reads kin). */
+void i2t_attention(struct sam_model *m, int layer, int P);
+
+/* Transposed-convolution scatter (sam3_model.c convt_scatter, kernel
+ * sam3_kernels.cl:762-786): G [(P H W)][Co 4] -> out [P][2H][2W][Co],
+ * + bias, + add [2H][2W][Co] (NULL for none), then act. */
+void convt_scatter(struct sam_model *m, hipb_mem G, hipb_mem out,
+                   hipb_mem bias, hipb_mem add, int P, int H, int W, int Co,
+                   int act);
+
+/* sam_postprocess (sam3_model.c:1445-1517): optional hole filling (host)
+ * of the n selected planes sel[] of d->lowres, bilinear resize to out_h x
+ * out_w binary masks in d->mask and stats [n][6] = count(logit >
+ * offset), count(logit > -offset), xmin, ymin, xmax, ymax. */
+void sam_postprocess(struct sam_model *m, int n, const int *sel, int out_h,
+                     int out_w, float offset, int fill, int *stats);
+/* Copy rows y0..y1, columns x0..x1 of postprocessed mask k to dst
+ * (sam3_model.c:1519-1530). */
+void sam_read_mask(struct sam_model *m, int k, int out_h, int out_w, int x0,
+                   int y0, int x1, int y1, unsigned char *dst);
 
 #ifdef __cplusplus
 }

@@ -341,3 +341,230 @@ def rope_table(side, hd=64, theta=10000.0):
     y = (pos // side).astype(np.float64)
     ang = np.concatenate([np.outer(x, f), np.outer(y, f)], axis=1)
     return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+# ------------------------------------------------------------ mask decoder
+
+_FP = ctypes.POINTER(ctypes.c_float)
+_ATT = ("qw", "qb", "kw", "kb", "vw", "vb", "ow", "ob")
+_LAYER = ("n1w", "n1b", "n2w", "n2b", "n3w", "n3b", "n4w", "n4b", "m1w",
+          "m1b", "m2w", "m2b")
+
+
+class OrAttnW(ctypes.Structure):
+    _fields_ = [(n, _FP) for n in _ATT] + [("dint", _i)]
+
+
+class OrDecLayer(ctypes.Structure):
+    _fields_ = [("self_", OrAttnW), ("t2i", OrAttnW), ("i2t", OrAttnW)] + \
+        [(n, _FP) for n in _LAYER]
+
+
+class OrDecoder(ctypes.Structure):
+    _fields_ = [("grid", _i), ("img", _i)] + \
+        [(n, _FP) for n in ("gauss", "point_emb", "not_a_point", "no_mask")] + \
+        [("layers", OrDecLayer * 2), ("final_t2i", OrAttnW)] + \
+        [(n, _FP) for n in ("nfw", "nfb", "up0w", "up0b", "up1w", "up1b",
+                            "up3w", "up3b", "obj_token", "iou_token",
+                            "mask_tokens")] + \
+        [("hyper_w", (_FP * 3) * 4), ("hyper_b", (_FP * 3) * 4),
+         ("iou_w", _FP * 3), ("iou_b", _FP * 3)]
+
+
+def _dec_lib():
+    L = lib()
+    if getattr(L, "_dec_ready", False):
+        return L
+    DP = ctypes.POINTER(OrDecoder)
+    L.or_pe_encode.argtypes = [_p, _f, _f, _p]
+    L.or_host_linear.argtypes = [_p, _p, _p, _i, _i, _i, _p]
+    L.or_convt_scatter.argtypes = [_p, _p, _p, _p, _i, _i, _i, _i, _i]
+    L.or_mask_logits.argtypes = [_p, _p, _p, _i, _i]
+    L.or_mask_post.argtypes = [_p, _p, _i, _i, _i, _i, _f, _p, _p]
+    L.or_fill_holes.argtypes = [_p, _i, _i]
+    L.or_fill_holes.restype = _i
+    L.or_postprocess.argtypes = [_p, _i, _i, _p, _i, _i, _f, _i, _i, _p, _p]
+    L.or_dec_prepare.argtypes = [DP, _p, _p, _p, _p, _p, _p, _p]
+    L.or_t2i_attention.argtypes = [_i, _i, _p, _p, _p, _p,
+                                   ctypes.POINTER(OrAttnW), _p]
+    L.or_i2t_attention.argtypes = [_i, _i, _i, _p, _p, _p, _p, _p, _p,
+                                   ctypes.POINTER(OrDecLayer)]
+    L.or_prompt_tokens.argtypes = [DP, _i, _p, _p]
+    L.or_sam_decode.argtypes = [DP, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                _p, _p, _p]
+    L._dec_ready = True
+    return L
+
+
+class DecoderW:
+    """struct or_decoder over the numpy arrays of a weight dict (the names of
+    sam3_hip.random_decoder_weights); the arrays are kept alive here."""
+
+    def __init__(self, w, grid, img=1008):
+        self.keep = {k: _f32(v) for k, v in w.items()}
+        d = self.d = OrDecoder()
+        d.grid, d.img = grid, img
+
+        def fp(name):
+            return self.keep[name].ctypes.data_as(_FP)
+
+        for n in ("gauss", "point_emb", "not_a_point", "no_mask", "nfw", "nfb",
+                  "up0w", "up0b", "up1w", "up1b", "up3w", "up3b", "obj_token",
+                  "iou_token", "mask_tokens"):
+            setattr(d, n, fp(n))
+
+        def attn(dst, prefix, dint):
+            for n in _ATT:
+                setattr(dst, n, fp(prefix + n))
+            dst.dint = dint
+
+        for layer in range(2):
+            p = "layers.%d." % layer
+            Lw = d.layers[layer]
+            attn(Lw.self_, p + "self.", 256)
+            attn(Lw.t2i, p + "t2i.", 128)
+            attn(Lw.i2t, p + "i2t.", 128)
+            for n in _LAYER:
+                setattr(Lw, n, fp(p + n))
+        attn(d.final_t2i, "final_t2i.", 128)
+        for i in range(4):
+            for j in range(3):
+                d.hyper_w[i][j] = fp("hyper.%d.%dw" % (i, j))
+                d.hyper_b[i][j] = fp("hyper.%d.%db" % (i, j))
+        for j in range(3):
+            d.iou_w[j] = fp("iou.%dw" % j)
+            d.iou_b[j] = fp("iou.%db" % j)
+
+    @property
+    def ptr(self):
+        return ctypes.byref(self.d)
+
+
+def pe_encode(gauss, x, y):
+    out = np.zeros(256, np.float32)
+    gauss = _f32(gauss)
+    _dec_lib().or_pe_encode(_ptr(gauss), x, y, _ptr(out))
+    return out
+
+
+def host_linear(W, b, x, relu=False):
+    W, b, x = _f32(W), _f32(b), _f32(x)
+    y = np.zeros(W.shape[0], np.float32)
+    _dec_lib().or_host_linear(_ptr(W), _ptr(b), _ptr(x), W.shape[1],
+                              W.shape[0], int(relu), _ptr(y))
+    return y
+
+
+def convt_scatter(G, bias, add, P, H, W, Co, act=ACT_NONE):
+    G, bias = _f32(G), _f32(bias)
+    add = None if add is None else _f32(add)
+    out = np.zeros((P, 2 * H, 2 * W, Co), np.float32)
+    _dec_lib().or_convt_scatter(_ptr(G), _ptr(out), _ptr(bias), _ptr(add), P,
+                                H, W, Co, act)
+    return out
+
+
+def mask_logits(U, hyper, P, npix):
+    U, hyper = _f32(U), _f32(hyper)
+    out = np.zeros((P, 3, npix), np.float32)
+    _dec_lib().or_mask_logits(_ptr(U), _ptr(hyper), _ptr(out), P, npix)
+    return out
+
+
+def mask_post(lowres, sel, L, out_h, out_w, offset):
+    """Returns (mask [n][out_h][out_w] uint8, stats [n][6])."""
+    lowres = _f32(lowres)
+    sel = np.ascontiguousarray(sel, np.int32)
+    n = len(sel)
+    mask = np.zeros((n, out_h, out_w), np.uint8)
+    stats = np.tile(np.array([0, 0, 0x7fffffff, 0x7fffffff, -1, -1],
+                             np.int32), (n, 1))
+    _dec_lib().or_mask_post(_ptr(lowres), _ptr(sel), n, L, out_h, out_w,
+                            offset, _ptr(mask), _ptr(stats))
+    return mask, stats
+
+
+def fill_holes(v, max_area):
+    v = _f32(v).copy()
+    L = v.shape[0]
+    changed = _dec_lib().or_fill_holes(_ptr(v), L, max_area)
+    return v, bool(changed)
+
+
+def postprocess(lowres, sel, out_h, out_w, offset, fill, max_area=256):
+    """sam_postprocess on a host copy: returns (lowres after filling, mask,
+    stats)."""
+    lowres = _f32(lowres).copy()
+    L = lowres.shape[-1]
+    sel = np.ascontiguousarray(sel, np.int32)
+    n = len(sel)
+    mask = np.zeros((n, out_h, out_w), np.uint8)
+    stats = np.zeros((n, 6), np.int32)
+    _dec_lib().or_postprocess(_ptr(lowres), L, n, _ptr(sel), out_h, out_w,
+                              offset, int(fill), max_area, _ptr(mask),
+                              _ptr(stats))
+    return lowres, mask, stats
+
+
+def dec_prepare(dw, emb):
+    """Returns dict pe, src, srcpe, kp0, vp0, qp0 of or_dec_prepare."""
+    G = dw.d.grid
+    T = G * G
+    emb = _f32(emb)
+    out = {"pe": np.zeros((T, 256), np.float32),
+           "src": np.zeros((T, 256), np.float32),
+           "srcpe": np.zeros((T, 256), np.float32),
+           "kp0": np.zeros((T, 128), np.float32),
+           "vp0": np.zeros((T, 128), np.float32),
+           "qp0": np.zeros((T, 128), np.float32)}
+    _dec_lib().or_dec_prepare(dw.ptr, _ptr(emb), *(_ptr(out[k]) for k in (
+        "pe", "src", "srcpe", "kp0", "vp0", "qp0")))
+    return out
+
+
+def prompt_tokens(dw, points):
+    pts = _f32(points).reshape(-1, 2)
+    P = pts.shape[0]
+    tok = np.zeros((P, 8, 256), np.float32)
+    _dec_lib().or_prompt_tokens(dw.ptr, P, _ptr(pts), _ptr(tok))
+    return tok
+
+
+def t2i_attention(P, T, qry, qpe, keys, pe, attn_w):
+    """Returns (qry after the residual, kin)."""
+    qry = _f32(qry).copy()
+    kin = np.zeros((P, T, 256), np.float32)
+    qpe, keys, pe = _f32(qpe), _f32(keys), _f32(pe)
+    _dec_lib().or_t2i_attention(P, T, _ptr(qry), _ptr(qpe), _ptr(keys),
+                                _ptr(pe), ctypes.byref(attn_w), _ptr(kin))
+    return qry, kin
+
+
+def i2t_attention(layer, P, T, qry, qpe, keys, kin, qp0, src, layer_w):
+    """Returns keys after the image -> token attention and norm4."""
+    keys = _f32(keys).copy()
+    args = [_f32(a) if a is not None else None for a in (qry, qpe, kin, qp0,
+                                                          src)]
+    _dec_lib().or_i2t_attention(layer, P, T, _ptr(args[0]), _ptr(args[1]),
+                                _ptr(keys), _ptr(args[2]), _ptr(args[3]),
+                                _ptr(args[4]), ctypes.byref(layer_w))
+    return keys
+
+
+def sam_decode(dw, points, prep, feat_s0, feat_s1):
+    """Returns (iou [P][3], lowres [P][3][4G][4G], tokens [P][8][256],
+    hyper [P][3][32])."""
+    G = dw.d.grid
+    pts = _f32(points).reshape(-1, 2)
+    P = pts.shape[0]
+    iou = np.zeros((P, 3), np.float32)
+    lowres = np.zeros((P, 3, 4 * G, 4 * G), np.float32)
+    tokens = np.zeros((P, 8, 256), np.float32)
+    hyper = np.zeros((P, 3, 32), np.float32)
+    feat_s0, feat_s1 = _f32(feat_s0), _f32(feat_s1)
+    _dec_lib().or_sam_decode(dw.ptr, P, _ptr(pts), _ptr(prep["pe"]),
+                             _ptr(prep["src"]), _ptr(prep["kp0"]),
+                             _ptr(prep["vp0"]), _ptr(prep["qp0"]),
+                             _ptr(feat_s0), _ptr(feat_s1), _ptr(iou),
+                             _ptr(lowres), _ptr(tokens), _ptr(hyper))
+    return iou, lowres, tokens, hyper

@@ -62,6 +62,11 @@ static float act_f(float v, int act)
     return v;
 }
 
+float or_act(float v, int act)
+{
+    return act_f(v, act);
+}
+
 /* Epilogue shared by every reference GEMM: alpha, bias, activation, then
  * residual (store_one sam3_kernels.cl:306-319; the same sequence in
  * gemm sam3_kernels.cl:141-155 and store_row8 sam3_kernels.cl:158-181). */
@@ -502,6 +507,11 @@ static float dot16(const float *a, const float *b)
 {
     return ((dot4(a, b) + dot4(a + 4, b + 4)) + dot4(a + 8, b + 8)) +
            dot4(a + 12, b + 12);
+}
+
+float or_dot16(const float *a, const float *b)
+{
+    return dot16(a, b);
 }
 
 #define DEC_HEADS 8

@@ -163,6 +163,80 @@ void or_sdpa_f64(int Nq, int Nk, int d, const double *Q, int ldq,
                  const double *K, int ldk, const double *V, int ldv, double *O,
                  int ldo, double scale);
 
+/* Activation epilogue of the reference kernels (exact-erf GELU, ReLU;
+ * sam3_kernels.cl:43-55) and its dot16 of two float16 vectors
+ * (sam3_kernels.cl:516-520). */
+float or_act(float v, int act);
+float or_dot16(const float *a, const float *b);
+
+/* ------------------------------------------------------------------ */
+/* Mask decoder (sam3_oracle_dec.c)                                    */
+/* ------------------------------------------------------------------ */
+
+/* Weights of one decoder attention (struct sam_attn_w, sam3_model.h:16):
+ * q/k/v [dint][256], o [256][dint], biases. */
+struct or_attn_w {
+    const float *qw, *qb, *kw, *kb, *vw, *vb, *ow, *ob;
+    int dint;
+};
+
+/* One two-way transformer layer (struct sam_dec_layer, sam3_model.h:28):
+ * mlp lin1 [2048][256], lin2 [256][2048]. */
+struct or_dec_layer {
+    struct or_attn_w self, t2i, i2t;
+    const float *n1w, *n1b, *n2w, *n2b, *n3w, *n3b, *n4w, *n4b;
+    const float *m1w, *m1b, *m2w, *m2b;
+};
+
+/* The point-prompt head's prompt encoder and mask decoder (the decoder
+ * fields of struct sam_model, sam3_model.h:55-75). grid: embedding side
+ * (SAM_GRID), img: encoder input side (SAM_IMG). gauss [2][128],
+ * point_emb [4][256], up0w [256][64 * 4], up3w [64][32 * 4], hyper_w[i]
+ * {[256][256], [256][256], [32][256]}, iou_w {.., .., [4][256]}. */
+struct or_decoder {
+    int grid, img;
+    const float *gauss, *point_emb, *not_a_point, *no_mask;
+    struct or_dec_layer layers[2];
+    struct or_attn_w final_t2i;
+    const float *nfw, *nfb;
+    const float *up0w, *up0b, *up1w, *up1b, *up3w, *up3b;
+    const float *obj_token, *iou_token, *mask_tokens;
+    const float *hyper_w[4][3], *hyper_b[4][3];
+    const float *iou_w[3], *iou_b[3];
+};
+
+void or_pe_encode(const float *gauss, float x, float y, float *out);
+void or_host_linear(const float *W, const float *b, const float *x, int nin,
+                    int nout, int relu, float *y);
+void or_convt_scatter(const float *G, float *out, const float *bias,
+                      const float *add, int P, int H, int W, int Co, int act);
+void or_mask_logits(const float *U, const float *hyper, float *out, int P,
+                    int npix);
+void or_mask_post(const float *lowres, const int *sel, int n, int L,
+                  int out_h, int out_w, float offset, unsigned char *mask,
+                  int *stats);
+int or_fill_holes(float *v, int L, int max_area);
+void or_postprocess(float *lowres, int L, int n, const int *sel, int out_h,
+                    int out_w, float offset, int fill, int max_area,
+                    unsigned char *mask, int *stats);
+void or_dec_prepare(const struct or_decoder *d, const float *emb, float *pe,
+                    float *src, float *srcpe, float *kp0, float *vp0,
+                    float *qp0);
+void or_t2i_attention(int P, int T, float *qry, const float *qpe,
+                      const float *keys, const float *pe,
+                      const struct or_attn_w *a, float *kin);
+void or_i2t_attention(int layer, int P, int T, const float *qry,
+                      const float *qpe, float *keys, const float *kin,
+                      const float *qp0, const float *src,
+                      const struct or_dec_layer *L);
+void or_prompt_tokens(const struct or_decoder *d, int P, const float *points,
+                      float *tok);
+void or_sam_decode(const struct or_decoder *d, int P, const float *points,
+                   const float *pe, const float *src, const float *kp0,
+                   const float *vp0, const float *qp0, const float *feat_s0,
+                   const float *feat_s1, float *iou, float *lowres,
+                   float *tokens, float *hyper_out);
+
 /* Number of OpenMP threads the oracle runs on. */
 int or_threads(void);
 

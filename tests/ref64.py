@@ -161,3 +161,126 @@ def attend(Q, K, V, heads, hd, causal=False, bias=None):
             s = s + bias[:, :, h]
         out[:, c] = softmax(s) @ V[:, c]
     return out
+
+
+# ------------------------------------------------------------ mask decoder
+# Written from the PyTorch SAM 2 / SAM 3 mask decoder semantics
+# (PositionEmbeddingRandom, TwoWayTransformer with skip_first_layer_pe on
+# layer 0, MaskDecoder with the object-score token, LayerNorm2d, exact GELU,
+# hypernetwork MLPs, sigmoid IoU head), in float64 with heads split by
+# reshape.
+
+
+def gelu_fast(x):
+    from scipy.special import erf
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+
+
+def pe_random(gauss, xy):
+    """xy [..., 2] in [0, 1] -> [..., 256] = [sin, cos](2 pi (2 xy - 1) G)."""
+    c = (2.0 * np.asarray(xy, np.float64) - 1.0) @ gauss.astype(np.float64)
+    c = 2.0 * math.pi * c
+    return np.concatenate([np.sin(c), np.cos(c)], -1)
+
+
+def _lin(x, w, b):
+    return x @ w.astype(np.float64).T + b.astype(np.float64)
+
+
+def dec_attention(w, prefix, q, k, v, heads=8):
+    """SAM Attention: project, split heads, softmax(q k^T / sqrt(c)) v,
+    merge, out-project. q [B, Nq, 256], k / v [B, Nk, 256]."""
+    Q = _lin(q, w[prefix + "qw"], w[prefix + "qb"])
+    K = _lin(k, w[prefix + "kw"], w[prefix + "kb"])
+    V = _lin(v, w[prefix + "vw"], w[prefix + "vb"])
+    B, Nq, D = Q.shape
+    c = D // heads
+    Qh = Q.reshape(B, Nq, heads, c).transpose(0, 2, 1, 3)
+    Kh = K.reshape(B, -1, heads, c).transpose(0, 2, 1, 3)
+    Vh = V.reshape(B, -1, heads, c).transpose(0, 2, 1, 3)
+    s = Qh @ Kh.transpose(0, 1, 3, 2) / math.sqrt(c)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    O = (p @ Vh).transpose(0, 2, 1, 3).reshape(B, Nq, D)
+    return _lin(O, w[prefix + "ow"], w[prefix + "ob"])
+
+
+def conv_transpose2x2(x, wt, b):
+    """ConvTranspose2d(kernel 2, stride 2) on a channel-last map x [B, H,
+    W, Ci] with weight [Ci, Co, 2, 2]: out[b, 2y + i, 2x + j, o] =
+    sum_c x[b, y, x, c] wt[c, o, i, j] + b[o]."""
+    B, H, W, _ = x.shape
+    Co = wt.shape[1]
+    t = np.einsum("byxc,coij->byixjo", x, wt.astype(np.float64))
+    return t.reshape(B, 2 * H, 2 * W, Co) + b.astype(np.float64)
+
+
+def decode64(w, grid, img, points, emb, feat_s0, feat_s1):
+    """Returns (iou [P][3], lowres [P][3][4 grid][4 grid]) in float64."""
+    G, T = grid, grid * grid
+    pts = np.asarray(points, np.float64).reshape(-1, 2)
+    P = pts.shape[0]
+    f = {k: np.asarray(v, np.float64) for k, v in w.items()}
+    ys, xs = np.meshgrid(np.arange(G), np.arange(G), indexing="ij")
+    pe = pe_random(f["gauss"], np.stack([(xs + 0.5) / G, (ys + 0.5) / G],
+                                        -1)).reshape(T, 256)
+    src = np.asarray(emb, np.float64) + f["no_mask"]
+    # Tokens: obj score, IoU, 4 mask tokens, the point, the padding point.
+    tok = np.zeros((P, 8, 256))
+    tok[:, 0] = f["obj_token"]
+    tok[:, 1] = f["iou_token"]
+    tok[:, 2:6] = f["mask_tokens"]
+    tok[:, 6] = pe_random(f["gauss"], (pts + 0.5) / img) + f["point_emb"][1]
+    tok[:, 7] = f["not_a_point"]
+    qpe = tok
+    queries = tok.copy()
+    keys = np.broadcast_to(src, (P, T, 256)).copy()
+    kpe = np.broadcast_to(pe, (P, T, 256))
+
+    def ln(x, pfx):
+        return layernorm(x, f[pfx + "w"], f[pfx + "b"], 1e-5)
+
+    for layer in range(2):
+        p = "layers.%d." % layer
+        if layer == 0:
+            queries = dec_attention(f, p + "self.", queries, queries, queries)
+        else:
+            q = queries + qpe
+            queries = queries + dec_attention(f, p + "self.", q, q, queries)
+        queries = ln(queries, p + "n1")
+        queries = queries + dec_attention(f, p + "t2i.", queries + qpe,
+                                          keys + kpe, keys)
+        queries = ln(queries, p + "n2")
+        h = np.maximum(_lin(queries, f[p + "m1w"], f[p + "m1b"]), 0.0)
+        queries = ln(queries + _lin(h, f[p + "m2w"], f[p + "m2b"]), p + "n3")
+        keys = keys + dec_attention(f, p + "i2t.", keys + kpe, queries + qpe,
+                                    queries)
+        keys = ln(keys, p + "n4")
+    queries = queries + dec_attention(f, "final_t2i.", queries + qpe,
+                                      keys + kpe, keys)
+    queries = ln(queries, "nf")
+    # Upscaling.
+    x = keys.reshape(P, G, G, 256)
+    u = conv_transpose2x2(x, f["up0w"].reshape(256, 64, 2, 2), f["up0b"])
+    u = u + np.asarray(feat_s1, np.float64).reshape(2 * G, 2 * G, 64)
+    u = gelu_fast(layernorm(u, f["up1w"], f["up1b"], 1e-6))
+    u = conv_transpose2x2(u, f["up3w"].reshape(64, 32, 2, 2), f["up3b"])
+    u = gelu_fast(u + np.asarray(feat_s0, np.float64).reshape(4 * G, 4 * G, 32))
+    # Hypernetwork MLPs (mask tokens 1..3) and the IoU head.
+    hyper = np.zeros((P, 3, 32))
+    for i in range(1, 4):
+        h = queries[:, 2 + i]
+        for j in range(3):
+            h = _lin(h, f["hyper.%d.%dw" % (i, j)], f["hyper.%d.%db" % (i, j)])
+            if j < 2:
+                h = np.maximum(h, 0.0)
+        hyper[:, i - 1] = h
+    h = queries[:, 1]
+    for j in range(3):
+        h = _lin(h, f["iou.%dw" % j], f["iou.%db" % j])
+        if j < 2:
+            h = np.maximum(h, 0.0)
+    iou = 1.0 / (1.0 + np.exp(-h[:, 1:4]))
+    lowres = np.einsum("pkc,pyxc->pkyx", hyper, u)
+    return iou, lowres

@@ -361,6 +361,47 @@ def decoder(hip, be, steps, warmup):
     }
 
 
+def mask_decoder(hip, steps, warmup, precisions=("bf16", "fp32"), P=64,
+                 grid=72):
+    """The point-prompt mask decoder, sam_decode (sam3_model.c:1239-1400),
+    P prompts on the 72 x 72 image embedding: prompt tokens, the two-way
+    transformer with per-prompt image keys [P][5184][256], the output
+    upscaling to [P][288][288][32], the host hypernetwork / IoU heads and
+    the low-resolution logits [P][3][288][288]; random-init weights, image
+    features ~ N(0, 1). ms per call of P prompts, and the per-operator
+    profile of one pass."""
+    g = np.random.default_rng(29)
+    T = grid * grid
+    w = hip.random_decoder_weights(29)
+    emb = g.standard_normal((T, 256), dtype=np.float32)
+    s0 = g.standard_normal((16 * T, 32), dtype=np.float32)
+    s1 = g.standard_normal((4 * T, 64), dtype=np.float32)
+    pts = g.uniform(0, 14 * grid, (P, 2)).astype(np.float32)
+    out = {"workload": "sam_decode: %d single-point prompts, 72x72x256 image "
+                       "embedding, per-prompt keys, upscaling to 288x288, "
+                       "3 multimask logits" % P}
+    for p in precisions:
+        be = hip.Backend(precision=p)
+        m = hip.Model(be, embed=1024, heads=16)
+        m.m.grid = grid
+        dec = hip.Decoder(m, w, P, img=14 * grid)
+        dec.set_image(emb, s0, s1)
+        ms = timed(be, lambda: dec.decode(pts), steps, warmup)
+        hip.prof_reset()
+        be._b.profile = 1
+        dec.decode(pts)
+        be.finish()
+        be._b.profile = 0
+        tab = hip.prof_table()
+        out[p] = {"ms": round(ms, 3),
+                  "profile_ms": {r[0]: round(r[1], 3) for r in
+                                 sorted(tab, key=lambda r: -r[1])[:10]}}
+        dec.free()
+        m.free()
+        be.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -373,6 +414,8 @@ def main():
                     help="only the global bf16 attention kernel (profiling)")
     ap.add_argument("--decoder-only", action="store_true",
                     help="only the mask-decoder cross-attention (profiling)")
+    ap.add_argument("--mask-decoder-only", action="store_true",
+                    help="only sam_decode of 64 prompts (profiling)")
     ap.add_argument("--backbone-only", action="store_true",
                     help="only the image encoder trunk (profiling)")
     ap.add_argument("--text-only", action="store_true",
@@ -391,6 +434,11 @@ def main():
         prec = (args.precision,) if args.precision else ("bf16", "fp32")
         print(json.dumps({"backbone": backbone(hip, args.steps, args.warmup,
                                                prec)}))
+        return
+    if args.mask_decoder_only:
+        prec = (args.precision,) if args.precision else ("bf16", "fp32")
+        print(json.dumps({"mask_decoder": mask_decoder(
+            hip, args.steps, min(args.warmup, 5), prec)}))
         return
     if args.text_only:
         print(json.dumps({"text_attention": text_attention(

@@ -154,6 +154,44 @@ __global__ __launch_bounds__(256) void k_layernorm_w(
     }
 }
 
+/* Narrow rows (C = 4 LPR floats, LPR = 8, 16 or 32 lanes per row): 256 / LPR
+ * rows per workgroup, a lane holds one float4 of its row, the sums close
+ * with butterflies inside the lane group. No window partition. */
+template <int LPR>
+__global__ __launch_bounds__(256) void k_layernorm_n(const float *__restrict__ X,
+                                                     float *__restrict__ Y,
+                                                     const float *__restrict__ g,
+                                                     const float *__restrict__ bt,
+                                                     long rows, float eps, int act)
+{
+    constexpr int C = 4 * LPR;
+    const int t = threadIdx.x, c = 4 * (t % LPR);
+    const long r = (long)blockIdx.x * (256 / LPR) + t / LPR;
+
+    if (r >= rows)
+        return;
+    const f32x4 v = *(const f32x4 *)(X + r * C + c);
+    float s = (v.x + v.y) + (v.z + v.w);
+
+    for (int k = 1; k < LPR; k <<= 1)
+        s += __shfl_xor(s, k, 64);
+    const float mean = s / (float)C;
+    const f32x4 d = {v.x - mean, v.y - mean, v.z - mean, v.w - mean};
+
+    s = fmaf(d.w, d.w, fmaf(d.z, d.z, fmaf(d.y, d.y, d.x * d.x)));
+    for (int k = 1; k < LPR; k <<= 1)
+        s += __shfl_xor(s, k, 64);
+    const float rs = 1.0f / sqrtf(s / (float)C + eps);
+    const f32x4 gv = *(const f32x4 *)(g + c), bv = *(const f32x4 *)(bt + c);
+    f32x4 y;
+
+    y.x = act_k(fmaf(d.x * rs, gv.x, bv.x), act);
+    y.y = act_k(fmaf(d.y * rs, gv.y, bv.y), act);
+    y.z = act_k(fmaf(d.z * rs, gv.z, bv.z), act);
+    y.w = act_k(fmaf(d.w * rs, gv.w, bv.w), act);
+    *(f32x4 *)(Y + r * C + c) = y;
+}
+
 extern "C" int launch_layernorm(const float *X, void *Y, int ydt,
                                 const float *g, const float *b, long rows,
                                 int C, float eps, int act, int H, int ws,
@@ -164,6 +202,22 @@ extern "C" int launch_layernorm(const float *X, void *Y, int ydt,
 
     if (out_rows == 0)
         return hipSuccess;
+    if (ws == 0 && ydt == DT_F32 && (C == 32 || C == 64 || C == 128) &&
+        (((uintptr_t)X | (uintptr_t)Y | (uintptr_t)g | (uintptr_t)b) & 15) == 0) {
+        const int rpw = 1024 / C; /* rows per workgroup: 256 / (C / 4) */
+        const dim3 grid((unsigned)((out_rows + rpw - 1) / rpw));
+
+        if (C == 32)
+            hipLaunchKernelGGL(k_layernorm_n<8>, grid, dim3(256), 0, st, X,
+                               (float *)Y, g, b, out_rows, eps, act);
+        else if (C == 64)
+            hipLaunchKernelGGL(k_layernorm_n<16>, grid, dim3(256), 0, st, X,
+                               (float *)Y, g, b, out_rows, eps, act);
+        else
+            hipLaunchKernelGGL(k_layernorm_n<32>, grid, dim3(256), 0, st, X,
+                               (float *)Y, g, b, out_rows, eps, act);
+        return hipGetLastError();
+    }
     /* 16-byte rows of the wave-per-row kernel: C a multiple of 256 up to
      * 4096 (the buffers are hipMalloc'd, so rows start 16-byte aligned). */
     if (C % 256 == 0 && C <= 4096) {

@@ -8,8 +8,10 @@
  */
 #include "k_common.h"
 
-/* One thread per output element of the P x 2H x 2W x Co map: out =
- * act(G[(p, y, x), co 4 + dy 2 + dx] + bias[co] (+ add)). The add map
+/* One thread per (prompt, input pixel, output channel co): the four GEMM
+ * columns co 4 + dy 2 + dx are one float4 (coalesced across co), and each
+ * lands at output pixel (2y + dy, 2x + dx) of the P x 2H x 2W x Co map as
+ * act(G + bias[co] (+ add)), consecutive co again consecutive. The add map
  * (2H x 2W x Co) is shared by the prompts. */
 __global__ __launch_bounds__(256) void k_convt_scatter(const float *__restrict__ G,
                                                        float *__restrict__ out,
@@ -24,16 +26,22 @@ __global__ __launch_bounds__(256) void k_convt_scatter(const float *__restrict__
         return;
     const int co = (int)(gid % Co);
     const long pix = gid / Co;
-    const int ox = (int)(pix % (2 * W));
-    const long rest = pix / (2 * W);
-    const int oy = (int)(rest % (2 * H));
-    const long p = rest / (2 * H);
-    const int y = oy >> 1, x = ox >> 1, dy = oy & 1, dx = ox & 1;
-    float v = G[((p * H + y) * W + x) * (Co * 4) + co * 4 + dy * 2 + dx] + bias[co];
+    const int x = (int)(pix % W);
+    const long rest = pix / W;
+    const int y = (int)(rest % H);
+    const long p = rest / H;
+    const f32x4 v = *(const f32x4 *)(G + 4 * gid);
+    const float bc = bias[co];
 
-    if (add)
-        v += add[gid % (4L * H * W * Co)];
-    out[gid] = act_k(v, act);
+    for (int dy = 0; dy < 2; dy++)
+        for (int dx = 0; dx < 2; dx++) {
+            const long o = ((2 * y + dy) * 2L * W + 2 * x + dx) * Co + co;
+            float u = v[2 * dy + dx] + bc;
+
+            if (add)
+                u += add[o];
+            out[p * 4L * H * W * Co + o] = act_k(u, act);
+        }
 }
 
 extern "C" int launch_convt_scatter(const float *G, float *out,
@@ -41,11 +49,11 @@ extern "C" int launch_convt_scatter(const float *G, float *out,
                                     int P, int H, int W, int Co, int act,
                                     void *stream)
 {
-    const long total = (long)P * 4 * H * W * Co;
+    const long total = (long)P * H * W * Co;
 
     if (total <= 0)
         return hipSuccess;
-    if ((total + 255) / 256 > 0x7fffffffL)
+    if ((total + 255) / 256 > 0x7fffffffL || ((uintptr_t)G & 15))
         return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_convt_scatter, dim3((unsigned)((total + 255) / 256)),
                        dim3(256), 0, (hipStream_t)stream, G, out, bias, add,

@@ -41,33 +41,6 @@ static void pe_encode(const struct sam_decoder *d, float x, float y,
     }
 }
 
-/* y = W x + b with double accumulation, optional ReLU
- * (host_linear, sam3_model.c:1185-1198). */
-static void host_linear(const float *W, const float *b, const float *x,
-                        int nin, int nout, int relu, float *y)
-{
-    int o, i;
-
-    for (o = 0; o < nout; o++) {
-        const float *w = W + (long)o * nin;
-        double acc = b[o];
-
-        for (i = 0; i < nin; i++)
-            acc += (double)w[i] * x[i];
-        y[o] = relu && acc < 0.0 ? 0.0f : (float)acc;
-    }
-}
-
-static void host_mlp3(float *const W[3], float *const B[3], const float *x,
-                      int nout, float *y)
-{
-    float h1[SAM_DIM], h2[SAM_DIM];
-
-    host_linear(W[0], B[0], x, SAM_DIM, SAM_DIM, 1, h1);
-    host_linear(W[1], B[1], h1, SAM_DIM, SAM_DIM, 1, h2);
-    host_linear(W[2], B[2], h2, SAM_DIM, nout, 0, y);
-}
-
 static hipb_mem dalloc(struct sam_model *m, size_t floats, const char *what)
 {
     return hipb_alloc(m->hip, floats * sizeof(float), what);
@@ -323,7 +296,7 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
     const int G = m->grid;
     const long T = (long)G * G, n = (long)P * NTOK * SAM_DIM;
     const struct sam_dec_layer *L0, *L1;
-    float *tok, *hyper;
+    float *tok;
     int p, i, err;
 
     if (!d)
@@ -403,28 +376,42 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
     if (hipb_failed())
         return;
 
-    /* Hypernetwork MLPs of mask tokens 1..3 and the IoU head (sigmoid) on
-     * the host. */
-    hipb_read(m->hip, d->qry, 0, tok, n * sizeof(float));
-    hyper = malloc((size_t)P * 96 * sizeof(float));
-    for (p = 0; p < P; p++) {
-        const float *t = tok + (long)p * NTOK * SAM_DIM;
-        float out[4];
+    /* Hypernetwork MLPs of mask tokens 1..3 (into d->hyper [P][3][32])
+     * and the IoU head as GEMMs over the P prompts' token rows (row
+     * stride NTOK x 256), the hidden layers in d->sq / d->sk, the IoU
+     * head's 4 outputs in d->sv; then the logits. */
+    for (i = 0; i <= 3; i++) {
+        hipb_mem const *W = i ? d->hyper_w[i] : d->iou_w;
+        hipb_mem const *B = i ? d->hyper_b[i] : d->iou_b;
+        const int tok_row = i ? 2 + i : 1, nout = i ? 32 : 4;
 
-        for (i = 1; i <= 3; i++)
-            host_mlp3(d->hyper_w[i], d->hyper_b[i], t + (2 + i) * SAM_DIM,
-                      32, hyper + (long)p * 96 + (i - 1) * 32);
-        host_mlp3(d->iou_w, d->iou_b, t + SAM_DIM, 4, out);
-        for (i = 0; i < 3; i++)
-            iou[p * 3 + i] = 1.0f / (1.0f + expf(-out[1 + i]));
+        gemm(m, P, SAM_DIM, SAM_DIM, mat(d->qry, (long)tok_row * SAM_DIM,
+                                         NTOK * SAM_DIM),
+             mat(W[0], 0, SAM_DIM), 1, mat(d->sq, 0, SAM_DIM), 1, 1, B[0],
+             NULL, 0, 1.0f, ACT_RELU);
+        gemm(m, P, SAM_DIM, SAM_DIM, mat(d->sq, 0, SAM_DIM),
+             mat(W[1], 0, SAM_DIM), 1, mat(d->sk, 0, SAM_DIM), 1, 1, B[1],
+             NULL, 0, 1.0f, ACT_RELU);
+        gemm(m, P, nout, SAM_DIM, mat(d->sk, 0, SAM_DIM),
+             mat(W[2], 0, SAM_DIM), 1,
+             i ? mat(d->hyper, (long)(i - 1) * 32, 96) : mat(d->sv, 0, 4), 1,
+             1, B[2], NULL, 0, 1.0f, ACT_NONE);
     }
-    hipb_write(m->hip, d->hyper, 0, hyper, (size_t)P * 96 * sizeof(float));
-    free(hyper);
-
+    if (hipb_failed())
+        return;
     hipb_run_begin(m->hip);
     err = launch_mask_logits(d->u2->ptr, d->hyper->ptr, d->lowres->ptr, P,
                              (int)(16 * T), m->hip->stream);
     hipb_run_end(m->hip, err, "mask_logits", 0.0);
+    /* IoU predictions 1..3 through the sigmoid (iou_prediction_use_sigmoid). */
+    {
+        float *raw = d->h_queries;
+
+        hipb_read(m->hip, d->sv, 0, raw, (size_t)P * 4 * sizeof(float));
+        for (p = 0; p < P; p++)
+            for (i = 0; i < 3; i++)
+                iou[p * 3 + i] = 1.0f / (1.0f + expf(-raw[p * 4 + 1 + i]));
+    }
 }
 
 /* Background components (v <= 0, 8-connected) of at most max_area pixels

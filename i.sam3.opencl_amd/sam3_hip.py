@@ -124,8 +124,8 @@ class SamDecoder(ctypes.Structure):
         [("obj_token", ctypes.c_float * 256),
          ("iou_token", ctypes.c_float * 256),
          ("mask_tokens", ctypes.c_float * 1024),
-         ("hyper_w", (_FP * 3) * 4), ("hyper_b", (_FP * 3) * 4),
-         ("iou_w", _FP * 3), ("iou_b", _FP * 3)] + \
+         ("hyper_w", (Mem * 3) * 4), ("hyper_b", (Mem * 3) * 4),
+         ("iou_w", Mem * 3), ("iou_b", Mem * 3)] + \
         [(n, Mem) for n in _DEC_BUFS] + \
         [("h_queries", _FP), ("h_lowres", _FP)] + \
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
@@ -560,14 +560,13 @@ def random_decoder_weights(seed):
 class Decoder:
     """struct sam_decoder attached to a Model (sam_dec_init): uploads the
     weights of `w` (random_decoder_weights' names; matrices with
-    upload_weight, so bf16 on precision=bf16), keeps the host arrays of
-    the MLP heads alive, and wraps the decoder entry points."""
+    upload_weight, so bf16 on precision=bf16) and wraps the decoder entry
+    points."""
 
     def __init__(self, model, w, batch, img=1008):
         be = model.backend
         self.model, self.be = model, be
         d = self.d = SamDecoder()
-        self._keep = []
         self._mems = []
         d.img = img
 
@@ -576,11 +575,6 @@ class Decoder:
             mem = be.upload_weight(a, name) if weight else be.upload(a, name)
             self._mems.append(mem)
             return mem
-
-        def host(name):
-            a = np.ascontiguousarray(w[name], np.float32)
-            self._keep.append(a)
-            return a.ctypes.data_as(_FP)
 
         for name in ("gauss", "point_emb", "not_a_point", "no_mask",
                      "obj_token", "iou_token", "mask_tokens"):
@@ -607,11 +601,11 @@ class Decoder:
         d.up3w = dev("up3w", True)
         for i in range(4):
             for j in range(3):
-                d.hyper_w[i][j] = host("hyper.%d.%dw" % (i, j))
-                d.hyper_b[i][j] = host("hyper.%d.%db" % (i, j))
+                d.hyper_w[i][j] = dev("hyper.%d.%dw" % (i, j), True)
+                d.hyper_b[i][j] = dev("hyper.%d.%db" % (i, j))
         for j in range(3):
-            d.iou_w[j] = host("iou.%dw" % j)
-            d.iou_b[j] = host("iou.%db" % j)
+            d.iou_w[j] = dev("iou.%dw" % j, True)
+            d.iou_b[j] = dev("iou.%db" % j)
         _call(_lib.sam_dec_init, model.ptr, ctypes.byref(d), batch)
         self.grid = model.m.grid
         self.batch = batch

@@ -370,9 +370,9 @@ struct sam_dec_layer {
 };
 
 /* The decoder fields of struct sam_model (sam3_model.h:55-75, 100-116).
- * The caller fills the weights (device: layers, final_t2i, nf*, up*;
- * host: the prompt encoder tables, tokens and the MLP heads, whose
- * arrays it keeps alive) and, per image, emb / feat_s0 / feat_s1;
+ * The caller fills the weights (device: layers, final_t2i, nf*, up*,
+ * the MLP heads; host: the prompt encoder tables and tokens) and, per
+ * image, emb / feat_s0 / feat_s1;
  * sam_dec_init allocates the rest. up0w [256][64 4] and up3w [64][32 4]
  * are the ConvTranspose2d weights [in][out][2][2]. hyper_w[i] = {[256]
  * [256], [256][256], [32][256]}, iou_w = {.., .., [4][256]}. */
@@ -388,8 +388,10 @@ struct sam_decoder {
     hipb_mem nfw, nfb;
     hipb_mem up0w, up0b, up1w, up1b, up3w, up3b;
     float obj_token[SAM_DIM], iou_token[SAM_DIM], mask_tokens[4 * SAM_DIM];
-    float *hyper_w[4][3], *hyper_b[4][3];
-    float *iou_w[3], *iou_b[3];
+    /* Hypernetwork MLPs and IoU head, device weights (the reference keeps
+     * them on the host; here they run as small GEMMs on the stream). */
+    hipb_mem hyper_w[4][3], hyper_b[4][3];
+    hipb_mem iou_w[3], iou_b[3];
     /* Image features [grid^2][256], [16 grid^2][32], [4 grid^2][64]. */
     hipb_mem emb, feat_s0, feat_s1;
     /* Per-image caches: src = emb + no_mask, dense PE, src + PE, layer-0

@@ -1,0 +1,349 @@
+/* SPDX-License-Identifier: Unlicense
+ *
+ * Fused image -> token attention of the mask decoder (the block
+ * sam3_model.c:1298-1312 / 1330-1345: image-query projection, attention
+ * over the 8 prompt tokens, output projection, residual, norm4) on bf16
+ * MFMA, for the bf16 path.
+ *
+ * The projections are folded into per-prompt matrices so the per-token
+ * work is two small products against the prompt's 8 tokens. For image
+ * token j with input x_j (kin_j = keys_j + PE_j in layer 1, the shared
+ * projected query qp0_j in layer 0), head h and prompt token t:
+ *
+ *   score(j, h, t) = s (Wq_h x_j + bq_h) . k_{t,h}
+ *                  = x_j . Wt[h,t] + bt[h,t],
+ *       Wt[h,t] = s Wq_h^T k_{t,h} (256 wide; layer 0, where x_j is already
+ *       projected: s k_{t,h} on head h's 16 columns of 128), bt[h,t] =
+ *       s bq_h . k_{t,h} (0 in layer 0), s = log2(e) / sqrt(16);
+ *   out_j = Wo (concat_h sum_t a(j,h,t) v_{t,h}) + bo
+ *         = sum_{h,t} a(j,h,t) Y[h,t] + bo,   Y[h,t] = Wo_h v_{t,h},
+ *
+ * with a the softmax over t per head (exp2 domain). k_i2t_fold builds Wt,
+ * bt and Y^T per prompt; k_i2t_fused runs a wave per 32 image tokens:
+ * S^T = Wt X^T (64 rows (h, t) x 32 tokens), the grouped softmax in
+ * registers, U^T = Y^T A^T (256 channels x 32 tokens), then + bo +
+ * residual and the LayerNorm over the 256 channels, written once.
+ *
+ * MFMA 32x32x16 bf16 lane layouts (l = lane, hh = l / 32): A operand lane
+ * l holds A[l % 32][8 hh .. 8 hh + 7 of the k step]; B operand B[same k
+ * slice][l % 32]; D register r of lane l is D[8 (r / 4) + 4 hh + r % 4][l % 32].
+ */
+#include "k_common.h"
+
+#define FOLD_ROWS 64 /* (head, prompt token) pairs: 8 x 8 */
+
+__device__ __forceinline__ float wld(const void *p, int dt, long i)
+{
+    if (dt == DT_BF16)
+        return bf2f(((const uint16_t *)p)[i]);
+    if (dt == DT_F16)
+        return h2f(((const uint16_t *)p)[i]);
+    return ((const float *)p)[i];
+}
+
+/* Column kappa of Y^T (the k index of the second product) holds Y row
+ * rho(kappa) = kappa with bits 2 and 3 swapped: k step s, lane half hh
+ * and element e = 4 e2 + e10 of the B operand are D register 8 (s % 2) +
+ * e of score tile s / 2, whose row is 16 s + 8 e2 + 4 hh + e10. */
+__device__ __forceinline__ int yt_row(int kappa)
+{
+    return (kappa & ~12) | ((kappa & 4) << 1) | ((kappa & 8) >> 1);
+}
+
+/* One workgroup per prompt p. sk / sv [P][8][128] (token keys and values
+ * of the image -> token attention), Wq [128][256] (layer 1) with bias bq,
+ * Wo [256][128]. Writes Wt16 [P][64][K] (bf16), bt [P][64], YT16
+ * [P][256][64] (bf16, columns in yt_row order). Row r of Wt is (h, t) =
+ * (r / 8, r % 8). */
+__global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
+                                                  const float *__restrict__ sv,
+                                                  int layer, const void *Wq,
+                                                  int wq_dt,
+                                                  const float *__restrict__ bq,
+                                                  const void *Wo, int wo_dt,
+                                                  float s,
+                                                  uint16_t *__restrict__ Wt16,
+                                                  float *__restrict__ bt,
+                                                  uint16_t *__restrict__ YT16)
+{
+    __shared__ float ks[8][128], vs[8][128];
+    const int p = blockIdx.x, t = threadIdx.x;
+    const int K = layer ? 256 : 128;
+
+    for (int i = t; i < 8 * 128; i += 256) {
+        ks[i / 128][i % 128] = sk[(long)p * 1024 + i];
+        vs[i / 128][i % 128] = sv[(long)p * 1024 + i];
+    }
+    __syncthreads();
+    uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
+    if (layer) {
+        /* Thread t = input column d of the 256. */
+        for (int h = 0; h < 8; h++) {
+            float w[16];
+
+            for (int c = 0; c < 16; c++)
+                w[c] = wld(Wq, wq_dt, (long)(16 * h + c) * 256 + t);
+            for (int tk = 0; tk < 8; tk++) {
+                float acc = 0.0f;
+
+                for (int c = 0; c < 16; c++)
+                    acc = fmaf(ks[tk][16 * h + c], w[c], acc);
+                wt[(8 * h + tk) * K + t] = f2bf(s * acc);
+            }
+        }
+        if (t < FOLD_ROWS) {
+            const int h = t / 8, tk = t % 8;
+            float acc = 0.0f;
+
+            for (int c = 0; c < 16; c++)
+                acc = fmaf(ks[tk][16 * h + c], bq[16 * h + c], acc);
+            bt[p * FOLD_ROWS + t] = s * acc;
+        }
+    }
+    else {
+        /* Block diagonal: row (h, t) holds s k_{t,h} on columns 16 h ..
+         * 16 h + 15 of 128. */
+        for (int i = t; i < FOLD_ROWS * 128; i += 256) {
+            const int r = i / 128, d = i % 128, h = r / 8, tk = r % 8;
+
+            wt[i] = f2bf(d / 16 == h ? s * ks[tk][d] : 0.0f);
+        }
+        if (t < FOLD_ROWS)
+            bt[p * FOLD_ROWS + t] = 0.0f;
+    }
+    /* Y^T: thread t = output channel ch. */
+    {
+        uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS + (long)t * FOLD_ROWS;
+        float wo[128];
+
+        for (int c = 0; c < 128; c++)
+            wo[c] = wld(Wo, wo_dt, (long)t * 128 + c);
+        for (int kap = 0; kap < FOLD_ROWS; kap++) {
+            const int r = yt_row(kap), h = r / 8, tk = r % 8;
+            float acc = 0.0f;
+
+            for (int c = 0; c < 16; c++)
+                acc = fmaf(wo[16 * h + c], vs[tk][16 * h + c], acc);
+            yt[kap] = f2bf(acc);
+        }
+    }
+}
+
+extern "C" int launch_i2t_fold(const float *sk, const float *sv, int layer,
+                               const void *Wq, int wq_dt, const float *bq,
+                               const void *Wo, int wo_dt, float s, int P,
+                               void *Wt16, float *bt, void *YT16,
+                               void *stream)
+{
+    if (P < 1 || (layer && (!Wq || !bq)) || !Wo)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_i2t_fold, dim3(P), dim3(256), 0, (hipStream_t)stream,
+                       sk, sv, layer, Wq, wq_dt, bq, Wo, wo_dt, s,
+                       (uint16_t *)Wt16, bt, (uint16_t *)YT16);
+    return hipGetLastError();
+}
+
+/* Byte offset of 16-byte chunk `chunk` of row `row` in an LDS tile with
+ * rows of `rowbytes`: XOR-swizzled so that the 16 rows one ds_read_b128
+ * phase reads fall on distinct banks. */
+__device__ __forceinline__ unsigned swz_off(int row, int chunk, int rowbytes)
+{
+    const int nch = rowbytes / 16;
+    const int sw = rowbytes >= 256 ? (row & 15) : ((row >> 1) & 7);
+
+    return (unsigned)(row * rowbytes + 16 * ((chunk ^ sw) & (nch - 1)));
+}
+
+/* Workgroup = 4 waves = 128 image tokens of one prompt; item (prompt,
+ * 128-token chunk) in XCD-contiguous order. X rows of K floats (per-prompt
+ * stride xs, 0 = shared), plus PE rows when pe != NULL; residual R
+ * (stride rs, 0 = shared); out [P][T][256] may alias R. */
+template <int K>
+__global__ __launch_bounds__(256, 2) void k_i2t_fused(
+    const float *X, long xs, const float *__restrict__ pe,
+    const uint16_t *__restrict__ Wt16, const float *__restrict__ bt,
+    const uint16_t *__restrict__ YT16, const float *__restrict__ bo,
+    const float *R, long rs, const float *__restrict__ g,
+    const float *__restrict__ bln, float *out, int T, int P, float eps)
+{
+    __shared__ __attribute__((aligned(16))) char Ws[FOLD_ROWS * K * 2];
+    __shared__ __attribute__((aligned(16))) char Ys[256 * FOLD_ROWS * 2];
+    __shared__ float bts[FOLD_ROWS];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
+              l32 = l & 31;
+    const int chunks = (T + 127) / 128;
+    const unsigned total = (unsigned)P * chunks, per_xcd = (total + 7) / 8;
+    const unsigned item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+
+    if (item >= total)
+        return;
+    const int p = (int)(item / chunks), ch0 = (int)(item % chunks) * 128;
+
+    /* Stage the prompt's Wt (64 x K) and Y^T (256 x 64) in LDS. */
+    {
+        const uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
+        const uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS;
+
+        for (int i = tid; i < FOLD_ROWS * K / 8; i += 256) {
+            const int row = i / (K / 8), c = i % (K / 8);
+
+            *(u32x4 *)(Ws + swz_off(row, c, 2 * K)) = *(const u32x4 *)(wt + 8 * i);
+        }
+        for (int i = tid; i < 256 * FOLD_ROWS / 8; i += 256) {
+            const int row = i / 8, c = i % 8;
+
+            *(u32x4 *)(Ys + swz_off(row, c, 2 * FOLD_ROWS)) = *(const u32x4 *)(yt + 8 * i);
+        }
+        if (tid < FOLD_ROWS)
+            bts[tid] = bt[p * FOLD_ROWS + tid];
+    }
+    __syncthreads();
+
+    const int j = ch0 + 32 * w + l32;
+    const bool valid = j < T;
+    const float *xr = X + (long)p * xs + (long)(valid ? j : 0) * K;
+    const float *per = pe ? pe + (long)(valid ? j : 0) * K : nullptr;
+    f32x16 s0 = {}, s1 = {};
+
+    /* S^T = Wt X^T over K / 16 steps; the lane's B operand is 8
+     * consecutive inputs of its token, converted to bf16. */
+#pragma unroll 4
+    for (int st = 0; st < K / 16; st++) {
+        const int c0 = 16 * st + 8 * hh;
+        f32x4 a0 = *(const f32x4 *)(xr + c0), a1 = *(const f32x4 *)(xr + c0 + 4);
+        bf16x8 bx;
+
+        if (per) {
+            const f32x4 p0 = *(const f32x4 *)(per + c0), p1 = *(const f32x4 *)(per + c0 + 4);
+
+            a0 += p0;
+            a1 += p1;
+        }
+        for (int e = 0; e < 4; e++) {
+            bx[e] = (__bf16)a0[e];
+            bx[4 + e] = (__bf16)a1[e];
+        }
+        const bf16x8 w0 = *(const bf16x8 *)(Ws + swz_off(l32, 2 * st + hh, 2 * K));
+        const bf16x8 w1 = *(const bf16x8 *)(Ws + swz_off(32 + l32, 2 * st + hh, 2 * K));
+
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, bx, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, bx, s1, 0, 0, 0);
+    }
+
+    /* Grouped softmax: register r of tile T_ is row 32 T_ + 8 (r / 4) +
+     * 4 hh + r % 4, i.e. head 4 T_ + r / 4 and prompt token 4 hh + r % 4:
+     * each head's 8 scores are 4 registers here and 4 in lane l ^ 32. */
+    for (int tt = 0; tt < 2; tt++) {
+        f32x16 &sc = tt ? s1 : s0;
+
+        for (int q = 0; q < 4; q++) {
+            float m = -INFINITY, sum = 0.0f;
+
+            for (int i = 0; i < 4; i++) {
+                sc[4 * q + i] += bts[32 * tt + 8 * q + 4 * hh + i];
+                m = fmaxf(m, sc[4 * q + i]);
+            }
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            for (int i = 0; i < 4; i++) {
+                sc[4 * q + i] = __builtin_amdgcn_exp2f(sc[4 * q + i] - m);
+                sum += sc[4 * q + i];
+            }
+            sum += __shfl_xor(sum, 32, 64);
+            const float inv = 1.0f / sum;
+
+            for (int i = 0; i < 4; i++)
+                sc[4 * q + i] *= inv;
+        }
+    }
+
+    /* U^T = Y^T A^T: 8 channel tiles x 4 k steps; the B operand of step st
+     * is registers 8 (st % 2) .. + 7 of score tile st / 2. */
+    f32x16 u[8];
+
+    for (int c = 0; c < 8; c++)
+        u[c] = (f32x16){};
+    for (int st = 0; st < 4; st++) {
+        const f32x16 &sc = st < 2 ? s0 : s1;
+        bf16x8 pb;
+
+        for (int e = 0; e < 8; e++)
+            pb[e] = (__bf16)sc[8 * (st & 1) + e];
+        for (int c = 0; c < 8; c++) {
+            const bf16x8 y = *(const bf16x8 *)(Ys + swz_off(32 * c + l32, 2 * st + hh, 2 * FOLD_ROWS));
+
+            u[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(y, pb, u[c], 0, 0, 0);
+        }
+    }
+
+    /* + bo + residual, LayerNorm over the 256 channels (128 here, 128 in
+     * lane l ^ 32): channel of register r of tile c is 32 c + 8 (r / 4) +
+     * 4 hh + r % 4, four consecutive channels per (c, r / 4). */
+    const float *rr = R + (long)p * rs + (long)(valid ? j : 0) * 256;
+    float sum = 0.0f;
+
+    for (int c = 0; c < 8; c++)
+        for (int q = 0; q < 4; q++) {
+            const int ch = 32 * c + 8 * q + 4 * hh;
+            const f32x4 b4 = *(const f32x4 *)(bo + ch), r4 = *(const f32x4 *)(rr + ch);
+
+            for (int i = 0; i < 4; i++) {
+                u[c][4 * q + i] += b4[i] + r4[i];
+                sum += u[c][4 * q + i];
+            }
+        }
+    sum += __shfl_xor(sum, 32, 64);
+    const float mean = sum * (1.0f / 256.0f);
+    float var = 0.0f;
+
+    for (int c = 0; c < 8; c++)
+        for (int r = 0; r < 16; r++) {
+            const float d = u[c][r] - mean;
+
+            var = fmaf(d, d, var);
+        }
+    var += __shfl_xor(var, 32, 64);
+    const float rsd = 1.0f / sqrtf(var * (1.0f / 256.0f) + eps);
+
+    if (!valid)
+        return;
+    float *orow = out + ((long)p * T + j) * 256;
+    for (int c = 0; c < 8; c++)
+        for (int q = 0; q < 4; q++) {
+            const int ch = 32 * c + 8 * q + 4 * hh;
+            const f32x4 g4 = *(const f32x4 *)(g + ch), b4 = *(const f32x4 *)(bln + ch);
+            f32x4 y;
+
+            for (int i = 0; i < 4; i++)
+                y[i] = fmaf((u[c][4 * q + i] - mean) * rsd, g4[i], b4[i]);
+            *(f32x4 *)(orow + ch) = y;
+        }
+}
+
+extern "C" int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
+                                const void *Wt16, const float *bt,
+                                const void *YT16, const float *bo,
+                                const float *R, long rs, const float *g,
+                                const float *b, float *out, int T, int P,
+                                float eps, void *stream)
+{
+    const long items = (long)P * ((T + 127) / 128);
+    const long grid = (items + 7) / 8 * 8;
+
+    if (P < 1 || T < 1 || grid > 0x7fffffffL || (K != 128 && K != 256) ||
+        ((xs | rs) & 3) ||
+        (((uintptr_t)X | (uintptr_t)R | (uintptr_t)out | (uintptr_t)bo |
+          (uintptr_t)g | (uintptr_t)b | (uintptr_t)(pe ? pe : X) |
+          (uintptr_t)Wt16 | (uintptr_t)YT16) & 15))
+        return hipErrorInvalidValue;
+    if (K == 256)
+        hipLaunchKernelGGL(k_i2t_fused<256>, dim3((unsigned)grid), dim3(256), 0,
+                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
+                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
+                           eps);
+    else
+        hipLaunchKernelGGL(k_i2t_fused<128>, dim3((unsigned)grid), dim3(256), 0,
+                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
+                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
+                           eps);
+    return hipGetLastError();
+}

@@ -97,6 +97,13 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
     d->stats = hipb_alloc(m->hip, P * 3 * 6 * sizeof(int), "mask statistics");
     d->mask = NULL;
     d->mask_cap = 0;
+    if (m->hip->bf16) {
+        d->fold_w = hipb_alloc_typed(m->hip, P * 64 * SAM_DIM, HIPB_BF16,
+                                     "folded image queries");
+        d->fold_b = dalloc(m, P * 64, "folded score bias");
+        d->fold_y = hipb_alloc_typed(m->hip, P * SAM_DIM * 64, HIPB_BF16,
+                                     "folded output projection");
+    }
 }
 
 void sam_dec_free(struct sam_model *m)
@@ -110,7 +117,8 @@ void sam_dec_free(struct sam_model *m)
                         &d->qp0, &d->qpe, &d->qry, &d->qin, &d->sq, &d->sk,
                         &d->sv, &d->so, &d->sh, &d->keys, &d->kin, &d->bq,
                         &d->bk, &d->bv, &d->bo, &d->u1, &d->g2, &d->u2,
-                        &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats};
+                        &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats,
+                        &d->fold_w, &d->fold_b, &d->fold_y};
 
     if (m->hip)
         hipb_finish(m->hip);
@@ -197,6 +205,41 @@ void i2t_attention(struct sam_model *m, int layer, int P)
     }
     L = &d->layers[layer];
     add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+    if (d->fold_w) {
+        /* bf16: the token keys / values as in the reference, then the
+         * folded block, one pass over the image tokens (keys + PE formed
+         * on the fly in layer 1, so kin is not read). */
+        struct hipb_backend *be = m->hip;
+        const float s = 1.4426950408889634f / sqrtf(16.0f);
+        int err;
+
+        linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, L->i2t.kw, L->i2t.kb,
+               d->sk, 0, ACT_NONE, 0);
+        linear(m, P * NTOK, SAM_DIM, 128, d->qry, 0, L->i2t.vw, L->i2t.vb,
+               d->sv, 0, ACT_NONE, 0);
+        if (hipb_failed())
+            return;
+        hipb_run_begin(be);
+        err = launch_i2t_fold(d->sk->ptr, d->sv->ptr, layer,
+                              layer ? L->i2t.qw->ptr : NULL,
+                              L->i2t.qw->dtype, layer ? L->i2t.qb->ptr : NULL,
+                              L->i2t.ow->ptr, L->i2t.ow->dtype, s, P,
+                              d->fold_w->ptr, d->fold_b->ptr, d->fold_y->ptr,
+                              be->stream);
+        hipb_run_end(be, err, "i2t_fold", 0.0);
+        hipb_run_begin(be);
+        err = launch_i2t_fused(layer ? d->keys->ptr : d->qp0->ptr,
+                               layer ? T * SAM_DIM : 0, layer ? 256 : 128,
+                               layer ? d->pe_img->ptr : NULL, d->fold_w->ptr,
+                               d->fold_b->ptr, d->fold_y->ptr, L->i2t.ob->ptr,
+                               layer ? d->keys->ptr : d->src->ptr,
+                               layer ? T * SAM_DIM : 0, L->n4w->ptr,
+                               L->n4b->ptr, d->keys->ptr, (int)T, P, DEC_EPS,
+                               be->stream);
+        hipb_run_end(be, err, "i2t_fused",
+                     4.0 * P * T * 64.0 * ((layer ? 256 : 128) + SAM_DIM));
+        return;
+    }
     if (layer == 0) {
         linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, L->i2t.kw, L->i2t.kb,
                d->sk, 0, ACT_NONE, 0);

@@ -188,6 +188,24 @@ int launch_mask_post(const float *lowres, const int *sel, int n, int L,
                      int out_h, int out_w, float offset, unsigned char *mask,
                      int *stats, void *stream);
 
+/* Image -> token attention folded per prompt (bf16 path): k_i2t_fold
+ * builds Wt16 [P][64][K] (bf16), bt [P][64] and YT16 [P][256][64] from
+ * the token keys / values sk, sv [P][8][128], the image-query projection
+ * Wq [128][256] + bq (layer 1; NULL in layer 0, K = 128) and the output
+ * projection Wo [256][128]; s = log2(e) / sqrt(head width). */
+int launch_i2t_fold(const float *sk, const float *sv, int layer,
+                    const void *Wq, int wq_dt, const float *bq,
+                    const void *Wo, int wo_dt, float s, int P, void *Wt16,
+                    float *bt, void *YT16, void *stream);
+/* out [P][T][256] = LayerNorm(R + bo + attention of X (+ pe) over the
+ * folded prompt tokens); X rows of K floats with per-prompt stride xs,
+ * R with stride rs (0 = shared); out may alias R. */
+int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
+                     const void *Wt16, const float *bt, const void *YT16,
+                     const float *bo, const float *R, long rs, const float *g,
+                     const float *b, float *out, int T, int P, float eps,
+                     void *stream);
+
 /* fp32 -> bf16 / half conversion of count elements (weight uploads). */
 int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
                    void *stream);

@@ -129,7 +129,8 @@ class SamDecoder(ctypes.Structure):
         [(n, Mem) for n in _DEC_BUFS] + \
         [("h_queries", _FP), ("h_lowres", _FP)] + \
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
-        [("mask_cap", ctypes.c_size_t)]
+        [("mask_cap", ctypes.c_size_t)] + \
+        [(n, Mem) for n in ("fold_w", "fold_b", "fold_y")]
 
 
 _lib = None

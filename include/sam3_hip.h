@@ -405,6 +405,9 @@ struct sam_decoder {
     /* Postprocessed masks and their statistics. */
     hipb_mem mask, sel, stats;
     size_t mask_cap;
+    /* precision=bf16: per-prompt folded image -> token attention, Wt
+     * [batch][64][256] bf16, bt [batch][64], Y^T [batch][256][64] bf16. */
+    hipb_mem fold_w, fold_b, fold_y;
 };
 
 /* Attach decoder d to m (grid from m) and allocate its caches and batch

@@ -347,3 +347,312 @@ extern "C" int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
                            eps);
     return hipGetLastError();
 }
+
+/* ------------------------------------------------------------------ */
+/* Output upscaling and mask logits, fused                             */
+/* ------------------------------------------------------------------ */
+
+/* Per image token (y, x) of prompt p, from keys [P][T][256]:
+ *   G1 = keys_j up0w (256 -> 64 channels x 4 pixels (dy, dx)),
+ *   u1 = GELU(LN2d(G1 + up0b + feat_s1[2y + dy][2x + dx]))   (per pixel, 64 ch),
+ *   G2 = u1 up3w (64 -> 32 channels x 4 sub-pixels (dy', dx')),
+ *   u2 = GELU(G2 + up3b + feat_s0[4y + 2dy + dy'][4x + 2dx + dx']),
+ *   lowres[p][k][4y + 2dy + dy'][4x + 2dx + dx'] = hyper[p][k] . u2 (k < 3),
+ * the sequence of sam3_model.c:1357-1366 and mask_logits with none of the
+ * [P][144][144][64] / [P][288][288][32] maps written.
+ *
+ * Products on bf16 MFMA, a wave per 32 tokens. G1^T = W1T keys^T: physical
+ * output row 32 c + 8 q + 4 hh + i (tile c, D register 4 q + i, lane half
+ * hh) is pixel dydx = c / 2, channel co = 32 (c % 2) + 16 (q / 2) + 8 hh +
+ * 4 (q % 2) + i, so that registers 8 (s % 2) .. + 7 of tile 2 dydx + s / 2
+ * are exactly the B operand (channels 16 s + 8 hh .. + 7) of k step s of
+ * G2^T = W2T u1^T. G2 row 32 c2 + 8 q2 + 4 hh + i2 is sub-pixel dydx' = c2,
+ * channel co' = 8 q2 + 4 hh + i2. */
+__device__ __forceinline__ int up1_col(int row)
+{
+    const int c = row >> 5, q = (row >> 3) & 3, hh = (row >> 2) & 1, i = row & 3;
+    const int co = 32 * (c & 1) + 16 * (q >> 1) + 8 * hh + 4 * (q & 1) + i;
+
+    return co * 4 + (c >> 1);
+}
+
+/* G2 row 32 c2 + 8 q2 + 4 hh + i2 is sub-pixel c2, channel co' = 16 (q2 /
+ * 2) + 8 hh + 4 (q2 % 2) + i2: registers 8 s .. 8 s + 7 of the tile are
+ * then the B operand (channels 16 s + 8 hh .. + 7) of k step s of the
+ * logits product. */
+__device__ __forceinline__ int up2_col(int r2)
+{
+    const int c2 = r2 >> 5, q2 = (r2 >> 3) & 3, hh = (r2 >> 2) & 1, i2 = r2 & 3;
+
+    return (16 * (q2 >> 1) + 8 * hh + 4 * (q2 & 1) + i2) * 4 + c2;
+}
+
+/* W1T16 [256][256] bf16: row r = up0w column up1_col(r) (over the 256
+ * inputs); W2T16 [128][64]: row r2 = up3w column up2_col(r2). */
+__global__ __launch_bounds__(256) void k_upscale_prep(const void *up0w, int dt0,
+                                                      const void *up3w, int dt3,
+                                                      uint16_t *__restrict__ W1T16,
+                                                      uint16_t *__restrict__ W2T16)
+{
+    const int r = blockIdx.x, t = threadIdx.x;
+
+    if (r < 256) {
+        W1T16[r * 256 + t] = f2bf(wld(up0w, dt0, (long)t * 256 + up1_col(r)));
+    }
+    else {
+        const int r2 = r - 256;
+
+        if (t < 64)
+            W2T16[r2 * 64 + t] = f2bf(wld(up3w, dt3, (long)t * 128 + up2_col(r2)));
+    }
+}
+
+extern "C" int launch_upscale_prep(const void *up0w, int dt0, const void *up3w,
+                                   int dt3, void *W1T16, void *W2T16,
+                                   void *stream)
+{
+    hipLaunchKernelGGL(k_upscale_prep, dim3(256 + 128), dim3(256), 0,
+                       (hipStream_t)stream, up0w, dt0, up3w, dt3,
+                       (uint16_t *)W1T16, (uint16_t *)W2T16);
+    return hipGetLastError();
+}
+
+/* GELU with erf from Abramowitz & Stegun, Handbook of Mathematical
+ * Functions, formula 7.1.26 (|error| <= 1.5e-7 on erf): erf(z) = 1 -
+ * (a1 t + ... + a5 t^5) exp(-z^2), t = 1 / (1 + p z), z >= 0, odd
+ * extension; far below the bf16 rounding of its result's consumers. */
+__device__ __forceinline__ float gelu_as(float v)
+{
+    const float z = fabsf(v) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+    float poly = fmaf(1.061405429f, t, -1.453152027f);
+
+    poly = fmaf(poly, t, 1.421413741f);
+    poly = fmaf(poly, t, -0.284496736f);
+    poly = fmaf(poly, t, 0.254829592f);
+    poly *= t;
+    const float e = __builtin_amdgcn_exp2f(-z * z * LOG2E_F);
+    const float erf_abs = fmaf(-poly, e, 1.0f);
+
+    return 0.5f * v * (1.0f + copysignf(erf_abs, v));
+}
+
+/* Persistent: one 8-wave workgroup per CU keeps W1T (128 KB) and W2T
+ * (16 KB) in LDS, XOR-swizzled by 16-byte chunk, and each wave walks the
+ * (prompt, 32-token group) items with stride 8 x gridDim.x. */
+__global__ __launch_bounds__(512, 1) void k_upscale_fused(
+    const float *__restrict__ keys, const uint16_t *__restrict__ W1T16,
+    const uint16_t *__restrict__ W2T16, const float *__restrict__ b0,
+    const float *__restrict__ lnw, const float *__restrict__ lnb,
+    const float *__restrict__ b3, const float *__restrict__ fs1,
+    const float *__restrict__ fs0, const float *__restrict__ hyper,
+    float *__restrict__ lowres, int G, int P, float eps)
+{
+    __shared__ __attribute__((aligned(16))) char W1s[256 * 512];
+    __shared__ __attribute__((aligned(16))) char W2s[128 * 128];
+    __shared__ __attribute__((aligned(16))) float vec[64 * 3 + 32];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
+              l32 = l & 31;
+    const int T = G * G, groups = (T + 31) / 32, L = 4 * G;
+    const unsigned items = (unsigned)P * groups; /* < 2^31 (launcher) */
+
+    for (int i = tid; i < 256 * 32; i += 512)
+        *(u32x4 *)(W1s + swz_off(i / 32, i % 32, 512)) = *(const u32x4 *)(W1T16 + 8 * i);
+    for (int i = tid; i < 128 * 8; i += 512)
+        *(u32x4 *)(W2s + swz_off(i / 8, i % 8, 128)) = *(const u32x4 *)(W2T16 + 8 * i);
+    if (tid < 64) {
+        vec[tid] = b0[tid];
+        vec[64 + tid] = lnw[tid];
+        vec[128 + tid] = lnb[tid];
+        if (tid < 32)
+            vec[192 + tid] = b3[tid];
+    }
+    __syncthreads();
+    const float *vb0 = vec, *vlw = vec + 64, *vlb = vec + 128, *vb3 = vec + 192;
+
+    for (unsigned item = blockIdx.x * 8 + w; item < items; item += gridDim.x * 8) {
+        const int p = (int)(item / (unsigned)groups);
+        const int j = (int)(item - (unsigned)p * groups) * 32 + l32;
+        const bool valid = j < T;
+        const int jj = valid ? j : 0, y = jj / G, x = jj % G;
+        const float *kr = keys + ((long)p * T + jj) * 256;
+        float *lr = lowres + (long)p * 3 * (16L * T);
+        /* A operand of the logits product: row l32 < 3 is mask l32's
+         * hypernetwork output, channels 16 s + 8 hh .. + 7; rows 3..31
+         * zero. */
+        bf16x8 hyb[2];
+
+        for (int s = 0; s < 2; s++) {
+            const float *hr = hyper + p * 96 + 32 * (l32 < 3 ? l32 : 0) + 16 * s + 8 * hh;
+            const f32x4 h0 = *(const f32x4 *)hr, h1 = *(const f32x4 *)(hr + 4);
+
+            for (int e = 0; e < 4; e++) {
+                hyb[s][e] = (__bf16)(l32 < 3 ? h0[e] : 0.0f);
+                hyb[s][4 + e] = (__bf16)(l32 < 3 ? h1[e] : 0.0f);
+            }
+        }
+
+        #pragma unroll 1
+        for (int dy = 0; dy < 2; dy++) {
+            /* Logits of this lane's two output rows' 4 columns per mask,
+             * collected over dx, dx': lg[dy'][k][2 dx + dx']. */
+            float lg[2][3][4];
+
+            #pragma unroll
+            for (int dx = 0; dx < 2; dx++) {
+                asm volatile("" ::: "memory");
+                const int px = 2 * dy + dx;
+                const float *f1 = fs1 + ((long)(2 * y + dy) * (2 * G) + 2 * x + dx) * 64;
+                float sum = 0.0f;
+                /* G1^T tiles 2 px, 2 px + 1: this pixel's 64 channels; the
+                 * token's inputs (re-read per pixel from the cache) as bf16
+                 * B operands. */
+                f32x16 g1[2] = {};
+
+                #pragma unroll 2
+                for (int st = 0; st < 16; st++) {
+                    const int c0 = 16 * st + 8 * hh;
+                    const f32x4 a0 = *(const f32x4 *)(kr + c0), a1 = *(const f32x4 *)(kr + c0 + 4);
+                    bf16x8 kb;
+
+                    #pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        kb[e] = (__bf16)a0[e];
+                        kb[4 + e] = (__bf16)a1[e];
+                    }
+                    #pragma unroll
+                    for (int half = 0; half < 2; half++) {
+                        const bf16x8 wa = *(const bf16x8 *)(W1s + swz_off(64 * px + 32 * half + l32,
+                                                                          2 * st + hh, 512));
+
+                        g1[half] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa, kb, g1[half], 0, 0, 0);
+                    }
+                }
+
+                /* + up0b + feat_s1, LayerNorm2d over the pixel's 64
+                 * channels. */
+                #pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    f32x16 &v = g1[half];
+
+                    #pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int co = 32 * half + 16 * (q >> 1) + 8 * hh + 4 * (q & 1);
+                        const f32x4 bb = *(const f32x4 *)(vb0 + co), ff = *(const f32x4 *)(f1 + co);
+
+                        #pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            v[4 * q + i] += bb[i] + ff[i];
+                            sum += v[4 * q + i];
+                        }
+                    }
+                }
+                sum += __shfl_xor(sum, 32, 64);
+                const float mean = sum * (1.0f / 64.0f);
+                float var = 0.0f;
+
+                #pragma unroll
+                for (int half = 0; half < 2; half++)
+                    #pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float d = g1[half][r] - mean;
+
+                        var = fmaf(d, d, var);
+                    }
+                var += __shfl_xor(var, 32, 64);
+                const float rs = __builtin_amdgcn_rsqf(var * (1.0f / 64.0f) + eps);
+                bf16x8 ub[4];
+
+                #pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const f32x16 &v = g1[half];
+
+                    #pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int co = 32 * half + 16 * (q >> 1) + 8 * hh + 4 * (q & 1);
+                        const f32x4 gw = *(const f32x4 *)(vlw + co), gb = *(const f32x4 *)(vlb + co);
+
+                        /* k step s = 2 half + q / 2, element 4 (q % 2) + i. */
+                        #pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            ub[2 * half + (q >> 1)][4 * (q & 1) + i] =
+                                (__bf16)gelu_as(fmaf((v[4 * q + i] - mean) * rs, gw[i], gb[i]));
+                    }
+                }
+                /* Per sub-pixel tile c2: G2^T (4 k steps), + up3b + feat_s0,
+                 * GELU, then the logits as a product of the prompt's
+                 * hypernetwork rows (3 of 32 used) with u2^T. */
+                #pragma unroll
+                for (int c2 = 0; c2 < 4; c2++) {
+                    const int dyp = c2 >> 1, dxp = c2 & 1;
+                    const float *f0 = fs0 + ((long)(4 * y + 2 * dy + dyp) * (4 * G) + 4 * x + 2 * dx + dxp) * 32;
+                    f32x16 g2 = {}, d3 = {};
+
+                    #pragma unroll
+                    for (int s = 0; s < 4; s++) {
+                        const bf16x8 wa = *(const bf16x8 *)(W2s + swz_off(32 * c2 + l32, 2 * s + hh, 128));
+
+                        g2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa, ub[s], g2, 0, 0, 0);
+                    }
+                    #pragma unroll
+                    for (int s = 0; s < 2; s++) {
+                        bf16x8 ub2;
+
+                        #pragma unroll
+                        for (int h2 = 0; h2 < 2; h2++) {
+                            const int co = 16 * s + 8 * hh + 4 * h2;
+                            const f32x4 bb = *(const f32x4 *)(vb3 + co), ff = *(const f32x4 *)(f0 + co);
+
+                            #pragma unroll
+                            for (int i = 0; i < 4; i++)
+                                ub2[4 * h2 + i] = (__bf16)gelu_as(g2[8 * s + 4 * h2 + i] + bb[i] + ff[i]);
+                        }
+                        d3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hyb[s], ub2, d3, 0, 0, 0);
+                    }
+                    /* Rows 0..2 (the masks) are registers 0..2 of lanes
+                     * 0..31. */
+                    #pragma unroll
+                    for (int k = 0; k < 3; k++)
+                        lg[dyp][k][2 * dx + dxp] = d3[k];
+                }
+            }
+            /* Lanes 0..31 store output rows 4 y + 2 dy + dy' of each mask. */
+            if (valid && hh == 0)
+                #pragma unroll
+                for (int dyp = 0; dyp < 2; dyp++) {
+                    const int Y = 4 * y + 2 * dy + dyp;
+
+                    #pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        const f32x4 o = {lg[dyp][k][0], lg[dyp][k][1], lg[dyp][k][2], lg[dyp][k][3]};
+
+                        *(f32x4 *)(lr + (long)k * 16 * T + (long)Y * L + 4 * x) = o;
+                    }
+                }
+        }
+    }
+}
+
+extern "C" int launch_upscale_fused(const float *keys, const void *W1T16,
+                                    const void *W2T16, const float *b0,
+                                    const float *lnw, const float *lnb,
+                                    const float *b3, const float *fs1,
+                                    const float *fs0, const float *hyper,
+                                    float *lowres, int G, int P, float eps,
+                                    int cus, void *stream)
+{
+    const long T = (long)G * G, items = (long)P * ((T + 31) / 32);
+    const long grid = (items + 7) / 8 < cus ? (items + 7) / 8 : cus;
+
+    if (P < 1 || G < 1 || cus < 1 || items + 8L * cus > 0x7fffffffL ||
+        ((uintptr_t)hyper & 15) ||
+        (((uintptr_t)keys | (uintptr_t)W1T16 | (uintptr_t)W2T16 |
+          (uintptr_t)b0 | (uintptr_t)lnw | (uintptr_t)lnb | (uintptr_t)b3 |
+          (uintptr_t)fs1 | (uintptr_t)fs0 | (uintptr_t)lowres) & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_upscale_fused, dim3((unsigned)grid), dim3(512), 0,
+                       (hipStream_t)stream, keys, (const uint16_t *)W1T16,
+                       (const uint16_t *)W2T16, b0, lnw, lnb, b3, fs1, fs0,
+                       hyper, lowres, G, P, eps);
+    return hipGetLastError();
+}

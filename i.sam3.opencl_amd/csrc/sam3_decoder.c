@@ -86,9 +86,12 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
     d->bk = dalloc(m, P * T * 128, "image k");
     d->bv = dalloc(m, P * T * 128, "image v");
     d->bo = dalloc(m, P * T * 128, "image attention");
-    d->u1 = dalloc(m, P * 4 * T * 64, "upscaling 1");
-    d->g2 = dalloc(m, P * 4 * T * 128, "upscaling 2 gemm");
-    d->u2 = dalloc(m, P * 16 * T * 32, "upscaling 2");
+    if (!m->hip->bf16) {
+        /* The fp32 path's upscaled maps (the bf16 path fuses them away). */
+        d->u1 = dalloc(m, P * 4 * T * 64, "upscaling 1");
+        d->g2 = dalloc(m, P * 4 * T * 128, "upscaling 2 gemm");
+        d->u2 = dalloc(m, P * 16 * T * 32, "upscaling 2");
+    }
     d->hyper = dalloc(m, P * 3 * 32, "hypernetwork");
     d->lowres = dalloc(m, P * 3 * 16 * T, "low-res masks");
     d->h_queries = malloc(P * NTOK * SAM_DIM * sizeof(float));
@@ -103,6 +106,10 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
         d->fold_b = dalloc(m, P * 64, "folded score bias");
         d->fold_y = hipb_alloc_typed(m->hip, P * SAM_DIM * 64, HIPB_BF16,
                                      "folded output projection");
+        d->up_w1t = hipb_alloc_typed(m->hip, 256 * 256, HIPB_BF16,
+                                     "upscaling weights 1");
+        d->up_w2t = hipb_alloc_typed(m->hip, 128 * 64, HIPB_BF16,
+                                     "upscaling weights 2");
     }
 }
 
@@ -118,7 +125,8 @@ void sam_dec_free(struct sam_model *m)
                         &d->sv, &d->so, &d->sh, &d->keys, &d->kin, &d->bq,
                         &d->bk, &d->bv, &d->bo, &d->u1, &d->g2, &d->u2,
                         &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats,
-                        &d->fold_w, &d->fold_b, &d->fold_y};
+                        &d->fold_w, &d->fold_b, &d->fold_y, &d->up_w1t,
+                        &d->up_w2t};
 
     if (m->hip)
         hipb_finish(m->hip);
@@ -402,27 +410,10 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
     layernorm(m, P * NTOK, SAM_DIM, d->qry, d->qry, d->nfw, d->nfb, DEC_EPS,
               ACT_NONE);
 
-    /* Output upscaling: ConvT 256 -> 64 + feat_s1, LayerNorm2d, GELU,
-     * ConvT 64 -> 32 + feat_s0, GELU (the kin buffer holds the first
-     * GEMM). */
-    gemm(m, (int)(P * T), 256, SAM_DIM, mat(d->keys, 0, SAM_DIM),
-         mat(d->up0w, 0, 256), 0, mat(d->kin, 0, 256), 1, 1, NULL, NULL, 0,
-         1.0f, ACT_NONE);
-    convt_scatter(m, d->kin, d->u1, d->up0b, d->feat_s1, P, G, G, 64,
-                  ACT_NONE);
-    layernorm(m, P * 4 * T, 64, d->u1, d->u1, d->up1w, d->up1b, LN2D_EPS,
-              ACT_GELU);
-    gemm(m, (int)(P * 4 * T), 128, 64, mat(d->u1, 0, 64), mat(d->up3w, 0, 128),
-         0, mat(d->g2, 0, 128), 1, 1, NULL, NULL, 0, 1.0f, ACT_NONE);
-    convt_scatter(m, d->g2, d->u2, d->up3b, d->feat_s0, P, 2 * G, 2 * G, 32,
-                  ACT_GELU);
-    if (hipb_failed())
-        return;
-
     /* Hypernetwork MLPs of mask tokens 1..3 (into d->hyper [P][3][32])
      * and the IoU head as GEMMs over the P prompts' token rows (row
      * stride NTOK x 256), the hidden layers in d->sq / d->sk, the IoU
-     * head's 4 outputs in d->sv; then the logits. */
+     * head's 4 outputs in d->sv. */
     for (i = 0; i <= 3; i++) {
         hipb_mem const *W = i ? d->hyper_w[i] : d->iou_w;
         hipb_mem const *B = i ? d->hyper_b[i] : d->iou_b;
@@ -442,10 +433,49 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
     }
     if (hipb_failed())
         return;
-    hipb_run_begin(m->hip);
-    err = launch_mask_logits(d->u2->ptr, d->hyper->ptr, d->lowres->ptr, P,
-                             (int)(16 * T), m->hip->stream);
-    hipb_run_end(m->hip, err, "mask_logits", 0.0);
+
+    if (d->up_w1t) {
+        /* bf16: the whole upscaling and the logits in one pass over the
+         * keys, per token 16 output pixels of the 3 masks. */
+        hipb_run_begin(m->hip);
+        err = launch_upscale_prep(d->up0w->ptr, d->up0w->dtype, d->up3w->ptr,
+                                  d->up3w->dtype, d->up_w1t->ptr,
+                                  d->up_w2t->ptr, m->hip->stream);
+        hipb_run_end(m->hip, err, "upscale_prep", 0.0);
+        hipb_run_begin(m->hip);
+        err = launch_upscale_fused(d->keys->ptr, d->up_w1t->ptr,
+                                   d->up_w2t->ptr, d->up0b->ptr, d->up1w->ptr,
+                                   d->up1b->ptr, d->up3b->ptr,
+                                   d->feat_s1->ptr, d->feat_s0->ptr,
+                                   d->hyper->ptr, d->lowres->ptr, G, P,
+                                   LN2D_EPS, m->hip->cu_count,
+                                   m->hip->stream);
+        hipb_run_end(m->hip, err, "upscale_fused",
+                     2.0 * P * T * (256.0 * 256 + 4 * 64 * 128 + 16 * 96));
+    }
+    else {
+        /* Output upscaling: ConvT 256 -> 64 + feat_s1, LayerNorm2d, GELU,
+         * ConvT 64 -> 32 + feat_s0, GELU (the kin buffer holds the first
+         * GEMM), then the logits. */
+        gemm(m, (int)(P * T), 256, SAM_DIM, mat(d->keys, 0, SAM_DIM),
+             mat(d->up0w, 0, 256), 0, mat(d->kin, 0, 256), 1, 1, NULL, NULL,
+             0, 1.0f, ACT_NONE);
+        convt_scatter(m, d->kin, d->u1, d->up0b, d->feat_s1, P, G, G, 64,
+                      ACT_NONE);
+        layernorm(m, P * 4 * T, 64, d->u1, d->u1, d->up1w, d->up1b, LN2D_EPS,
+                  ACT_GELU);
+        gemm(m, (int)(P * 4 * T), 128, 64, mat(d->u1, 0, 64),
+             mat(d->up3w, 0, 128), 0, mat(d->g2, 0, 128), 1, 1, NULL, NULL, 0,
+             1.0f, ACT_NONE);
+        convt_scatter(m, d->g2, d->u2, d->up3b, d->feat_s0, P, 2 * G, 2 * G,
+                      32, ACT_GELU);
+        if (hipb_failed())
+            return;
+        hipb_run_begin(m->hip);
+        err = launch_mask_logits(d->u2->ptr, d->hyper->ptr, d->lowres->ptr, P,
+                                 (int)(16 * T), m->hip->stream);
+        hipb_run_end(m->hip, err, "mask_logits", 0.0);
+    }
     /* IoU predictions 1..3 through the sigmoid (iou_prediction_use_sigmoid). */
     {
         float *raw = d->h_queries;

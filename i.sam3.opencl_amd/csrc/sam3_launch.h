@@ -206,6 +206,19 @@ int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
                      const float *b, float *out, int T, int P, float eps,
                      void *stream);
 
+/* Output upscaling fused with the mask logits (bf16 path): prep writes
+ * the permuted bf16 transposes W1T16 [256][256] of up0w [256][64 4] and
+ * W2T16 [128][64] of up3w [64][32 4]; the fused kernel maps keys
+ * [P][G^2][256] to lowres [P][3][4G][4G] (feat_s1 [(2G)^2][64], feat_s0
+ * [(4G)^2][32], hyper [P][3][32]). */
+int launch_upscale_prep(const void *up0w, int dt0, const void *up3w, int dt3,
+                        void *W1T16, void *W2T16, void *stream);
+int launch_upscale_fused(const float *keys, const void *W1T16,
+                         const void *W2T16, const float *b0, const float *lnw,
+                         const float *lnb, const float *b3, const float *fs1,
+                         const float *fs0, const float *hyper, float *lowres,
+                         int G, int P, float eps, int cus, void *stream);
+
 /* fp32 -> bf16 / half conversion of count elements (weight uploads). */
 int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
                    void *stream);

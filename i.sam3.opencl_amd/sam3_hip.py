@@ -130,7 +130,8 @@ class SamDecoder(ctypes.Structure):
         [("h_queries", _FP), ("h_lowres", _FP)] + \
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
         [("mask_cap", ctypes.c_size_t)] + \
-        [(n, Mem) for n in ("fold_w", "fold_b", "fold_y")]
+        [(n, Mem) for n in ("fold_w", "fold_b", "fold_y", "up_w1t",
+                            "up_w2t")]
 
 
 _lib = None

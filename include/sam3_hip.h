@@ -408,6 +408,9 @@ struct sam_decoder {
     /* precision=bf16: per-prompt folded image -> token attention, Wt
      * [batch][64][256] bf16, bt [batch][64], Y^T [batch][256][64] bf16. */
     hipb_mem fold_w, fold_b, fold_y;
+    /* precision=bf16: up0w / up3w as the fused upscaling's permuted bf16
+     * transposes [256][256] and [128][64]. */
+    hipb_mem up_w1t, up_w2t;
 };
 
 /* Attach decoder d to m (grid from m) and allocate its caches and batch

@@ -91,12 +91,23 @@ def test_decode(hip, be, orc, weights, G, P):
     try:
         pts = np.random.default_rng(G).uniform(0, 14 * G, (P, 2)).astype(np.float32)
         print("sam_decode G=%d P=%d %s" % (G, P, be.precision), flush=True)
-        iou = d.dec.decode(pts)
+        hip.prof_reset()
+        be.set_profile(True)
+        try:
+            iou = d.dec.decode(pts)
+        finally:
+            be.set_profile(False)
+        ran = {r[0] for r in hip.prof_table()}
+        # bf16 runs the fused image -> token block and upscaling.
+        fused = {"i2t_fused", "upscale_fused"}
+        assert fused <= ran if be.precision == "bf16" else not (fused & ran), ran
         low = d.dec.lowres(P)
         oiou, olow, _, _ = orc.sam_decode(d.dw, pts, d.prep, d.s0, d.s1)
         tol = TOL[be.precision]
         assert report("decode lowres G=%d %s" % (G, be.precision), low, olow) <= tol
         assert np.abs(iou - oiou).max() <= 4 * tol
+        if be.precision != "fp32":
+            return  # the bf16 path fuses the upscaling (no u2 map)
         # The logits kernel alone, on the device's own upscaled map and
         # hypernetwork outputs: the same fused multiply-add chain.
         T = G * G

@@ -52,9 +52,11 @@ __device__ __forceinline__ int yt_row(int kappa)
 
 /* One workgroup per prompt p. sk / sv [P][8][128] (token keys and values
  * of the image -> token attention), Wq [128][256] (layer 1) with bias bq,
- * Wo [256][128]. Writes Wt16 [P][64][K] (bf16), bt [P][64], YT16
- * [P][256][64] (bf16, columns in yt_row order). Row r of Wt is (h, t) =
- * (r / 8, r % 8). */
+ * Wo [256][128]. Writes Wt16 [P][64][K] (bf16), bt [P][64] (when bq is
+ * given), YT16 [P][256][64] (bf16, columns in yt_row order; when Wo is
+ * given). Row r of Wt is (h, t) = (r / 8, r % 8). The token -> image
+ * attention uses the same fold for its queries (sk = projected queries,
+ * Wq = the key projection, no bq or Wo). */
 __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
                                                   const float *__restrict__ sv,
                                                   int layer, const void *Wq,
@@ -72,7 +74,8 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
 
     for (int i = t; i < 8 * 128; i += 256) {
         ks[i / 128][i % 128] = sk[(long)p * 1024 + i];
-        vs[i / 128][i % 128] = sv[(long)p * 1024 + i];
+        if (Wo)
+            vs[i / 128][i % 128] = sv[(long)p * 1024 + i];
     }
     __syncthreads();
     uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
@@ -91,7 +94,7 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
                 wt[(8 * h + tk) * K + t] = f2bf(s * acc);
             }
         }
-        if (t < FOLD_ROWS) {
+        if (bq && t < FOLD_ROWS) {
             const int h = t / 8, tk = t % 8;
             float acc = 0.0f;
 
@@ -111,8 +114,8 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
         if (t < FOLD_ROWS)
             bt[p * FOLD_ROWS + t] = 0.0f;
     }
-    /* Y^T: thread t = output channel ch. */
-    {
+    /* Y^T: thread t = output channel ch (skipped without Wo). */
+    if (Wo) {
         uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS + (long)t * FOLD_ROWS;
         float wo[128];
 
@@ -135,7 +138,7 @@ extern "C" int launch_i2t_fold(const float *sk, const float *sv, int layer,
                                void *Wt16, float *bt, void *YT16,
                                void *stream)
 {
-    if (P < 1 || (layer && (!Wq || !bq)) || !Wo)
+    if (P < 1 || (layer && !Wq) || (!layer && !Wo))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_i2t_fold, dim3(P), dim3(256), 0, (hipStream_t)stream,
                        sk, sv, layer, Wq, wq_dt, bq, Wo, wo_dt, s,
@@ -654,5 +657,273 @@ extern "C" int launch_upscale_fused(const float *keys, const void *W1T16,
                        (hipStream_t)stream, keys, (const uint16_t *)W1T16,
                        (const uint16_t *)W2T16, b0, lnw, lnb, b3, fs1, fs0,
                        hyper, lowres, G, P, eps);
+    return hipGetLastError();
+}
+
+
+/* ------------------------------------------------------------------ */
+/* Token -> image attention on per-prompt keys, fused                  */
+/* ------------------------------------------------------------------ */
+
+/* For prompt p, head h, prompt token i (row r = 8 h + i):
+ *   score(r, j) = s q_{i,h} . (Wk_h kin_j + bk_h) = U[r] . kin_j + const(r),
+ *   U[r] = s Wk_h^T q_{i,h} (k_i2t_fold on the projected queries),
+ *   o_{i,h} = Wv_h (sum_j a(r, j) keys_j) + bv_h = Wv_h Z[r] + bv_h,
+ * with kin_j = keys_j + PE_j formed on the fly; the constant drops out of
+ * the softmax. k_t2i_fused: workgroup = (prompt, key split), 4 waves =
+ * 2 row tiles x 2 key streams; per 64-key block the workgroup stages Kin
+ * [64 keys][256] and keys^T [256][64 keys] in LDS as bf16, and each wave
+ * does S^T = Kin U^T (32 keys x 32 rows, rows = lanes), the online
+ * softmax, and Z^T += keys^T P^T (256 x 32). The two streams of a row
+ * tile merge through LDS; each split leaves (Z, m, l) partials for
+ * k_t2i_merge; k_t2i_unfold applies Wv and bv. */
+
+/* Byte offset of keys^T element (dim d, key k) in a [256][64] bf16 tile:
+ * rows of 128 B, 16-byte chunk k / 8 at chunk (k / 8) ^ ((d >> 1) & 7). */
+__device__ __forceinline__ unsigned vt_off(int d, int k)
+{
+    return (unsigned)(d * 128 + 16 * ((k >> 3) ^ ((d >> 1) & 7)) + 2 * (k & 7));
+}
+
+__global__ __launch_bounds__(256, 2) void k_t2i_fused(
+    const float *__restrict__ keys, const float *__restrict__ pe,
+    const uint16_t *__restrict__ U16, float *__restrict__ part, int T,
+    int nsplit)
+{
+    __shared__ __attribute__((aligned(16))) char Ks[64 * 512];
+    __shared__ __attribute__((aligned(16))) char Vs[256 * 128];
+    const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
+              l32 = l & 31;
+    const int rt = w & 1, kh = w >> 1;
+    const int p = blockIdx.x / nsplit, sp = blockIdx.x % nsplit;
+    const int nblk = (T + 63) / 64;
+    const int kb0 = sp * nblk / nsplit, kb1 = (sp + 1) * nblk / nsplit;
+    const float *kp = keys + (long)p * T * 256;
+    const int row = 32 * rt + l32;
+
+    /* U^T B operands of this lane's row come from the cache each block. */
+    const uint16_t *ur = U16 + ((long)p * FOLD_ROWS + row) * 256 + 8 * hh;
+    f32x16 z[8];
+    for (int dt = 0; dt < 8; dt++)
+        z[dt] = (f32x16){};
+    float m = -INFINITY, lsum = 0.0f;
+    const int krow = 32 * kh + ((l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1));
+
+    for (int kb = kb0; kb < kb1; kb++) {
+        /* Stage: task = (8-dim chunk c, key pair) with c fastest, so a
+         * wave reads two contiguous 1 KB rows; keys past T are zero. */
+        for (int task = tid; task < 32 * 32; task += 256) {
+            const int c = task & 31, k0 = 2 * (task >> 5);
+            f32x4 a[2][2], b[2][2];
+
+            for (int e = 0; e < 2; e++) {
+                const int key = kb * 64 + k0 + e;
+
+                if (key < T) {
+                    const float *kr = kp + (long)key * 256 + 8 * c;
+                    const float *pr = pe + (long)key * 256 + 8 * c;
+
+                    a[e][0] = *(const f32x4 *)kr;
+                    a[e][1] = *(const f32x4 *)(kr + 4);
+                    b[e][0] = *(const f32x4 *)pr;
+                    b[e][1] = *(const f32x4 *)(pr + 4);
+                }
+                else {
+                    a[e][0] = a[e][1] = b[e][0] = b[e][1] = (f32x4){};
+                }
+            }
+            for (int e = 0; e < 2; e++) {
+                bf16x8 kin;
+
+                for (int i = 0; i < 4; i++) {
+                    kin[i] = (__bf16)(a[e][0][i] + b[e][0][i]);
+                    kin[4 + i] = (__bf16)(a[e][1][i] + b[e][1][i]);
+                }
+                *(bf16x8 *)(Ks + swz_off(k0 + e, c, 512)) = kin;
+            }
+            for (int i = 0; i < 8; i++) {
+                const float v0 = i < 4 ? a[0][0][i] : a[0][1][i - 4];
+                const float v1 = i < 4 ? a[1][0][i] : a[1][1][i - 4];
+
+                *(uint32_t *)(Vs + vt_off(8 * c + i, k0)) = pack_bf16x2(v0, v1);
+            }
+        }
+        __syncthreads();
+
+        /* S^T for this wave's 32 keys (A rows in kperm order) x 32 rows;
+         * the fence keeps the U loads here rather than hoisted into 64
+         * registers for the whole loop. */
+        asm volatile("" ::: "memory");
+        f32x16 sc = {};
+
+        for (int st = 0; st < 16; st++) {
+            const bf16x8 ka = *(const bf16x8 *)(Ks + swz_off(krow, 2 * st + hh, 512));
+            const bf16x8 ub = *(const bf16x8 *)(ur + 16 * st);
+
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, ub, sc, 0, 0, 0);
+        }
+        /* Register r of lane half hh is key 32 kh + 16 (r / 8) + 8 hh + r % 8. */
+        for (int r = 0; r < 16; r++) {
+            const int key = kb * 64 + 32 * kh + 16 * (r >> 3) + 8 * hh + (r & 7);
+
+            if (key >= T)
+                sc[r] = -INFINITY;
+        }
+        float bm = -INFINITY;
+
+        for (int r = 0; r < 16; r++)
+            bm = __builtin_fmaxf(bm, sc[r]);
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        /* Lazy rescale: m moves only when a score passes it by 2^8. */
+        if (bm > m + 8.0f) {
+            const float corr = __builtin_amdgcn_exp2f(m - bm);
+
+            lsum *= corr;
+            for (int dt = 0; dt < 8; dt++)
+                for (int r = 0; r < 16; r++)
+                    z[dt][r] *= corr;
+            m = bm;
+        }
+        bf16x8 pb[2];
+        /* No finite score in this stream yet: every exp2 below is 0. */
+        const float mref = m == -INFINITY ? 0.0f : m;
+
+        for (int r = 0; r < 16; r++) {
+            const float e = __builtin_amdgcn_exp2f(sc[r] - mref);
+
+            lsum += e;
+            pb[r >> 3][r & 7] = (__bf16)e;
+        }
+        /* Z^T += keys^T P^T: 8 dim tiles x 2 k steps of 16 keys. */
+        for (int a = 0; a < 2; a++)
+            for (int dt = 0; dt < 8; dt++) {
+                const bf16x8 va = *(const bf16x8 *)(Vs + vt_off(32 * dt + l32, 32 * kh + 16 * a + 8 * hh));
+
+                z[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[a], z[dt], 0, 0, 0);
+            }
+        __syncthreads();
+    }
+    lsum += __shfl_xor(lsum, 32, 64);
+
+    /* Merge the key streams of each row tile through LDS (the staging
+     * tiles are free after the last barrier; row l32's 256 values are
+     * stored with their float4 slots XOR 4 l32): stream 1 writes (m, l,
+     * Z^T), stream 0 combines and stores the split's partial record:
+     * part [p][split][64 rows][256] then [p][split][64][2]. */
+    float *zs = (float *)(rt ? Vs : Ks); /* 32 rows x 256 = 32 KB per tile */
+    __shared__ float mls[2][32][2];
+
+    if (kh == 1) {
+        for (int dt = 0; dt < 8; dt++)
+            for (int q = 0; q < 4; q++) {
+                const int d = 32 * dt + 8 * q + 4 * hh;
+                const f32x4 v = {z[dt][4 * q], z[dt][4 * q + 1], z[dt][4 * q + 2], z[dt][4 * q + 3]};
+
+                *(f32x4 *)(zs + l32 * 256 + (d ^ (4 * l32))) = v;
+            }
+        if (hh == 0) {
+            mls[rt][l32][0] = m;
+            mls[rt][l32][1] = lsum;
+        }
+    }
+    __syncthreads();
+    if (kh == 0) {
+        const float m1 = mls[rt][l32][0], l1 = mls[rt][l32][1];
+        const float mm = fmaxf(m, m1);
+        const float c0 = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mm);
+        const float c1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - mm);
+        const long rec = ((long)p * nsplit + sp) * FOLD_ROWS + row;
+        float *zo = part + rec * 256;
+
+        for (int dt = 0; dt < 8; dt++)
+            for (int q = 0; q < 4; q++) {
+                const int d = 32 * dt + 8 * q + 4 * hh;
+                const f32x4 v1 = *(const f32x4 *)(zs + l32 * 256 + (d ^ (4 * l32)));
+                f32x4 o;
+
+                for (int i = 0; i < 4; i++)
+                    o[i] = z[dt][4 * q + i] * c0 + v1[i] * c1;
+                *(f32x4 *)(zo + d) = o;
+            }
+        if (hh == 0) {
+            float *ml = part + (long)gridDim.x * FOLD_ROWS * 256 + rec * 2;
+
+            ml[0] = mm;
+            ml[1] = lsum * c0 + l1 * c1;
+        }
+    }
+}
+
+/* Z [P][64][256] from the nsplit partial records: thread per (p, row, d). */
+__global__ __launch_bounds__(256) void k_t2i_merge(const float *__restrict__ part,
+                                                   float *__restrict__ Z, int P,
+                                                   int nsplit)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= (long)P * FOLD_ROWS * 256)
+        return;
+    const int d = (int)(gid & 255);
+    const long pr = gid >> 8; /* p * 64 + row */
+    const int p = (int)(pr / FOLD_ROWS), row = (int)(pr % FOLD_ROWS);
+    const float *ml = part + (long)P * nsplit * FOLD_ROWS * 256;
+    float M = -INFINITY;
+
+    for (int s = 0; s < nsplit; s++)
+        M = fmaxf(M, ml[(((long)p * nsplit + s) * FOLD_ROWS + row) * 2]);
+    float num = 0.0f, den = 0.0f;
+
+    for (int s = 0; s < nsplit; s++) {
+        const long rec = ((long)p * nsplit + s) * FOLD_ROWS + row;
+        const float ms = ml[rec * 2];
+        const float wgt = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+
+        num = fmaf(wgt, part[rec * 256 + d], num);
+        den = fmaf(wgt, ml[rec * 2 + 1], den);
+    }
+    Z[gid] = num / den;
+}
+
+/* o [P][8][128]: o[p][i][16 h + c] = Wv[16 h + c] . Z[p][8 h + i] + bv. */
+__global__ __launch_bounds__(256) void k_t2i_unfold(const float *__restrict__ Z,
+                                                    const void *Wv, int wv_dt,
+                                                    const float *__restrict__ bv,
+                                                    float *__restrict__ o, int P)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= (long)P * 8 * 128)
+        return;
+    const int col = (int)(gid & 127), i = (int)((gid >> 7) & 7);
+    const long p = gid >> 10;
+    const int h = col >> 4;
+    const float *zr = Z + (p * FOLD_ROWS + 8 * h + i) * 256;
+    float acc = bv[col];
+
+    for (int d = 0; d < 256; d++)
+        acc = fmaf(wld(Wv, wv_dt, (long)col * 256 + d), zr[d], acc);
+    o[gid] = acc;
+}
+
+extern "C" int launch_t2i_fused(const float *keys, const float *pe,
+                                const void *U16, float *part, float *Z,
+                                const void *Wv, int wv_dt, const float *bv,
+                                float *o, int T, int P, int nsplit,
+                                void *stream)
+{
+    const int nblk = (T + 63) / 64;
+    const long n = (long)P * FOLD_ROWS * 256;
+
+    if (P < 1 || T < 1 || nsplit < 1 || nsplit > nblk ||
+        (long)P * nsplit > 0x7fffffffL ||
+        (((uintptr_t)keys | (uintptr_t)pe | (uintptr_t)U16 | (uintptr_t)part) & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_t2i_fused, dim3((unsigned)(P * nsplit)), dim3(256), 0,
+                       (hipStream_t)stream, keys, pe, (const uint16_t *)U16,
+                       part, T, nsplit);
+    hipLaunchKernelGGL(k_t2i_merge, dim3((unsigned)((n + 255) / 256)), dim3(256),
+                       0, (hipStream_t)stream, part, Z, P, nsplit);
+    hipLaunchKernelGGL(k_t2i_unfold, dim3((unsigned)((P * 1024L + 255) / 256)),
+                       dim3(256), 0, (hipStream_t)stream, Z, Wv, wv_dt, bv, o, P);
     return hipGetLastError();
 }

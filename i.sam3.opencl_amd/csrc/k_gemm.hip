@@ -289,6 +289,42 @@ __global__ __launch_bounds__(256) void k_gemm_bf16(gemm_desc d, int avec,
 /* 16-byte alignment of every 8-element load: offset, batch strides and
  * leading dimension are multiples of the elements per 16 bytes (the
  * buffers themselves come from hipMalloc, 256-byte aligned). */
+/* Small GEMMs (a few 128 x 128 tiles: the decoder's per-token linears of
+ * 8 P rows): one wave per 32 x 32 tile, no LDS; each lane loads its MFMA
+ * operand fragments straight from memory (A row m = lane % 32 and B row
+ * n = lane % 32 of the Linear weight, 8 consecutive k per lane half), bf16
+ * MFMA with f32 accumulation over K / 16 steps, the usual epilogue.
+ * Unbatched, B stored N x K, K % 16 == 0, 16-byte aligned operand rows
+ * (checked by the launcher). Rows / columns past M / N read row 0 and are
+ * not stored. */
+__global__ __launch_bounds__(64) void k_gemm_small(gemm_desc d)
+{
+    const int l = threadIdx.x, h = l >> 5, l32 = l & 31;
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    const int m = m0 + l32 < d.M ? m0 + l32 : 0, n = n0 + l32 < d.N ? n0 + l32 : 0;
+    f32x16 acc = {};
+
+    for (int k = 8 * h; k < d.K; k += 16) {
+        float fa[8], fb[8];
+        bf16x8 a, b;
+
+        load8(d.A, d.adt, d.aoff + (long)m * d.lda + k, 8, true, fa);
+        load8(d.B, d.bdt, d.boff + (long)n * d.ldb + k, 8, true, fb);
+        for (int e = 0; e < 8; e++) {
+            a[e] = (__bf16)fa[e];
+            b[e] = (__bf16)fb[e];
+        }
+        /* D = A B^T tile: rows m (A operand), columns n (B operand). */
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+    }
+    const void *R = d.R ? (const void *)((d.cdt == DT_F32 ? 4 : 2) * d.roff +
+                                         (const char *)d.R) : nullptr;
+    void *C = (char *)d.C + (d.cdt == DT_F32 ? 4 : 2) * d.coff;
+
+    if (n0 + l32 < d.N)
+        store_block(d, C, R, acc, m0, n0 + l32);
+}
+
 static int vec_ok(int dt, long off, long s0, long s1, int ld)
 {
     const long q = dt == DT_F32 ? 4 : 8;
@@ -313,6 +349,13 @@ extern "C" int launch_gemm(const gemm_desc *d, void *stream)
     }
     if (d->unpart_ws > 0)
         return hipErrorInvalidValue; /* row remap: NT kernel only */
+    if (d->mode == MODE_BF16 && d->transb && d->nb == 1 && d->K % 16 == 0 &&
+        avec && bvec && (long)grid.x * grid.y < 64 &&
+        ((uintptr_t)d->A & 15) == 0 && ((uintptr_t)d->B & 15) == 0) {
+        hipLaunchKernelGGL(k_gemm_small, dim3((d->N + 31) / 32, (d->M + 31) / 32),
+                           dim3(64), 0, s, *d);
+        return hipGetLastError();
+    }
     if (d->mode == MODE_BF16) {
         if (d->transb)
             hipLaunchKernelGGL(k_gemm_bf16<true>, grid, dim3(256), 0, s, *d,

@@ -110,6 +110,9 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
                                      "upscaling weights 1");
         d->up_w2t = hipb_alloc_typed(m->hip, 128 * 64, HIPB_BF16,
                                      "upscaling weights 2");
+        d->t2i_part = dalloc(m, (2L * m->hip->cu_count + P) * 64 * 258,
+                             "token -> image partials");
+        d->t2i_z = dalloc(m, P * 64 * SAM_DIM, "token -> image key sums");
     }
 }
 
@@ -126,7 +129,7 @@ void sam_dec_free(struct sam_model *m)
                         &d->bk, &d->bv, &d->bo, &d->u1, &d->g2, &d->u2,
                         &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats,
                         &d->fold_w, &d->fold_b, &d->fold_y, &d->up_w1t,
-                        &d->up_w2t};
+                        &d->up_w2t, &d->t2i_part, &d->t2i_z};
 
     if (m->hip)
         hipb_finish(m->hip);
@@ -185,6 +188,38 @@ void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a)
         return;
     }
     add_bcast(m, d->qin, d->qry, d->qpe, n, n);
+    if (d->fold_w) {
+        /* bf16: the queries folded through the key projection, then one
+         * pass over the prompt's keys (keys + PE formed on the fly, the
+         * key and value projections never applied to the 256-wide image
+         * tokens), then Wv per head, then the output projection. kin is
+         * not written: the fused image -> token block forms it itself. */
+        struct hipb_backend *be = m->hip;
+        const int nblk = (int)((T + 63) / 64);
+        int nsplit = (2 * be->cu_count + P - 1) / P, err;
+
+        if (nsplit > nblk)
+            nsplit = nblk;
+        linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, a->qw, a->qb, d->sq, 0,
+               ACT_NONE, 0);
+        if (hipb_failed())
+            return;
+        hipb_run_begin(be);
+        err = launch_i2t_fold(d->sq->ptr, NULL, 1, a->kw->ptr, a->kw->dtype,
+                              NULL, NULL, 0,
+                              1.4426950408889634f / sqrtf(16.0f), P,
+                              d->fold_w->ptr, NULL, NULL, be->stream);
+        hipb_run_end(be, err, "t2i_fold", 0.0);
+        hipb_run_begin(be);
+        err = launch_t2i_fused(d->keys->ptr, d->pe_img->ptr, d->fold_w->ptr,
+                               d->t2i_part->ptr, d->t2i_z->ptr, a->vw->ptr,
+                               a->vw->dtype, a->vb->ptr, d->so->ptr, (int)T, P,
+                               nsplit, be->stream);
+        hipb_run_end(be, err, "t2i_fused", 4.0 * P * 64.0 * T * SAM_DIM);
+        linear(m, P * NTOK, 128, SAM_DIM, d->so, 0, a->ow, a->ob, d->qry, 0,
+               ACT_NONE, 1);
+        return;
+    }
     add_bcast(m, d->kin, d->keys, d->pe_img, P * T * SAM_DIM, T * SAM_DIM);
     linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, a->qw, a->qb, d->sq, 0,
            ACT_NONE, 0);

@@ -219,6 +219,16 @@ int launch_upscale_fused(const float *keys, const void *W1T16,
                          const float *fs0, const float *hyper, float *lowres,
                          int G, int P, float eps, int cus, void *stream);
 
+/* Token -> image attention on per-prompt keys (bf16 path): keys [P][T]
+ * [256] + pe [T][256] against the folded queries U16 [P][64][256] (bf16,
+ * k_i2t_fold on the projected queries with the key projection), nsplit
+ * key splits with partials in part (P nsplit 64 258 floats), merged into
+ * Z [P][64][256], then o [P][8][128] = Wv Z + bv per head. */
+int launch_t2i_fused(const float *keys, const float *pe, const void *U16,
+                     float *part, float *Z, const void *Wv, int wv_dt,
+                     const float *bv, float *o, int T, int P, int nsplit,
+                     void *stream);
+
 /* fp32 -> bf16 / half conversion of count elements (weight uploads). */
 int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
                    void *stream);

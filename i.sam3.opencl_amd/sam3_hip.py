@@ -131,7 +131,7 @@ class SamDecoder(ctypes.Structure):
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
         [("mask_cap", ctypes.c_size_t)] + \
         [(n, Mem) for n in ("fold_w", "fold_b", "fold_y", "up_w1t",
-                            "up_w2t")]
+                            "up_w2t", "t2i_part", "t2i_z")]
 
 
 _lib = None

@@ -411,6 +411,10 @@ struct sam_decoder {
     /* precision=bf16: up0w / up3w as the fused upscaling's permuted bf16
      * transposes [256][256] and [128][64]. */
     hipb_mem up_w1t, up_w2t;
+    /* precision=bf16: token -> image attention key-split partials
+     * ((2 CUs + batch) records of 64 rows x 258 floats) and the merged
+     * weighted key sums Z [batch][64][256]. */
+    hipb_mem t2i_part, t2i_z;
 };
 
 /* Attach decoder d to m (grid from m) and allocate its caches and batch

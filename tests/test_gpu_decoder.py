@@ -98,8 +98,8 @@ def test_decode(hip, be, orc, weights, G, P):
         finally:
             be.set_profile(False)
         ran = {r[0] for r in hip.prof_table()}
-        # bf16 runs the fused image -> token block and upscaling.
-        fused = {"i2t_fused", "upscale_fused"}
+        # bf16 runs the fused attention blocks and upscaling.
+        fused = {"i2t_fused", "t2i_fused", "upscale_fused"}
         assert fused <= ran if be.precision == "bf16" else not (fused & ran), ran
         low = d.dec.lowres(P)
         oiou, olow, _, _ = orc.sam_decode(d.dw, pts, d.prep, d.s0, d.s1)

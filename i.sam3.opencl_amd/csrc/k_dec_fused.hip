@@ -68,66 +68,68 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
                                                   float *__restrict__ bt,
                                                   uint16_t *__restrict__ YT16)
 {
-    __shared__ float ks[8][128], vs[8][128];
-    const int p = blockIdx.x, t = threadIdx.x;
+    /* Workgroup (p, h): head h's 16 columns of the 8 tokens' keys and
+     * values, rows 8 h .. 8 h + 7 of Wt and bt, those columns of Y^T. */
+    __shared__ float ks[8][16], vs[8][16];
+    const int p = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
     const int K = layer ? 256 : 128;
 
-    for (int i = t; i < 8 * 128; i += 256) {
-        ks[i / 128][i % 128] = sk[(long)p * 1024 + i];
+    if (t < 128) {
+        const int tk = t / 16, c = t % 16;
+
+        ks[tk][c] = sk[(long)p * 1024 + tk * 128 + 16 * h + c];
         if (Wo)
-            vs[i / 128][i % 128] = sv[(long)p * 1024 + i];
+            vs[tk][c] = sv[(long)p * 1024 + tk * 128 + 16 * h + c];
     }
     __syncthreads();
-    uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
+    uint16_t *wt = Wt16 + ((long)p * FOLD_ROWS + 8 * h) * K;
     if (layer) {
         /* Thread t = input column d of the 256. */
-        for (int h = 0; h < 8; h++) {
-            float w[16];
+        float w[16];
 
-            for (int c = 0; c < 16; c++)
-                w[c] = wld(Wq, wq_dt, (long)(16 * h + c) * 256 + t);
-            for (int tk = 0; tk < 8; tk++) {
-                float acc = 0.0f;
-
-                for (int c = 0; c < 16; c++)
-                    acc = fmaf(ks[tk][16 * h + c], w[c], acc);
-                wt[(8 * h + tk) * K + t] = f2bf(s * acc);
-            }
-        }
-        if (bq && t < FOLD_ROWS) {
-            const int h = t / 8, tk = t % 8;
+        for (int c = 0; c < 16; c++)
+            w[c] = wld(Wq, wq_dt, (long)(16 * h + c) * 256 + t);
+        for (int tk = 0; tk < 8; tk++) {
             float acc = 0.0f;
 
             for (int c = 0; c < 16; c++)
-                acc = fmaf(ks[tk][16 * h + c], bq[16 * h + c], acc);
-            bt[p * FOLD_ROWS + t] = s * acc;
+                acc = fmaf(ks[tk][c], w[c], acc);
+            wt[tk * K + t] = f2bf(s * acc);
+        }
+        if (bq && t < 8) {
+            float acc = 0.0f;
+
+            for (int c = 0; c < 16; c++)
+                acc = fmaf(ks[t][c], bq[16 * h + c], acc);
+            bt[p * FOLD_ROWS + 8 * h + t] = s * acc;
         }
     }
     else {
-        /* Block diagonal: row (h, t) holds s k_{t,h} on columns 16 h ..
-         * 16 h + 15 of 128. */
-        for (int i = t; i < FOLD_ROWS * 128; i += 256) {
-            const int r = i / 128, d = i % 128, h = r / 8, tk = r % 8;
+        /* Block diagonal: row (h, tk) holds s k_{tk,h} on columns 16 h ..
+         * 16 h + 15 of 128, zero elsewhere. */
+        for (int i = t; i < 8 * 128; i += 256) {
+            const int tk = i / 128, d = i % 128;
 
-            wt[i] = f2bf(d / 16 == h ? s * ks[tk][d] : 0.0f);
+            wt[i] = f2bf(d / 16 == h ? s * ks[tk][d % 16] : 0.0f);
         }
-        if (t < FOLD_ROWS)
-            bt[p * FOLD_ROWS + t] = 0.0f;
+        if (t < 8)
+            bt[p * FOLD_ROWS + 8 * h + t] = 0.0f;
     }
-    /* Y^T: thread t = output channel ch (skipped without Wo). */
+    /* Y^T: thread t = output channel ch (skipped without Wo); Y row
+     * 8 h + tk lands in column yt_row(8 h + tk) (yt_row is its own
+     * inverse). */
     if (Wo) {
         uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS + (long)t * FOLD_ROWS;
-        float wo[128];
+        float wo[16];
 
-        for (int c = 0; c < 128; c++)
-            wo[c] = wld(Wo, wo_dt, (long)t * 128 + c);
-        for (int kap = 0; kap < FOLD_ROWS; kap++) {
-            const int r = yt_row(kap), h = r / 8, tk = r % 8;
+        for (int c = 0; c < 16; c++)
+            wo[c] = wld(Wo, wo_dt, (long)t * 128 + 16 * h + c);
+        for (int tk = 0; tk < 8; tk++) {
             float acc = 0.0f;
 
             for (int c = 0; c < 16; c++)
-                acc = fmaf(wo[16 * h + c], vs[tk][16 * h + c], acc);
-            yt[kap] = f2bf(acc);
+                acc = fmaf(wo[c], vs[tk][c], acc);
+            yt[yt_row(8 * h + tk)] = f2bf(acc);
         }
     }
 }
@@ -140,7 +142,7 @@ extern "C" int launch_i2t_fold(const float *sk, const float *sv, int layer,
 {
     if (P < 1 || (layer && !Wq) || (!layer && !Wo))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_i2t_fold, dim3(P), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(k_i2t_fold, dim3(P, 8), dim3(256), 0, (hipStream_t)stream,
                        sk, sv, layer, Wq, wq_dt, bq, Wo, wo_dt, s,
                        (uint16_t *)Wt16, bt, (uint16_t *)YT16);
     return hipGetLastError();

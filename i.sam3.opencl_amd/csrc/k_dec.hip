@@ -179,6 +179,83 @@ __global__ __launch_bounds__(256) void k_mha_fewkeys(
     }
 }
 
+/* Few keys (<= 8), head width 32, for precision=bf16: four lanes per
+ * (prompt, query, head), each holding 8 of the 32 channels; the partial
+ * dot products close over the four lanes, the softmax runs on the exp2
+ * domain, and each lane writes its 8 output channels. Rows are read as
+ * float4 (16-byte aligned strides, checked by the launcher). */
+__global__ __launch_bounds__(256) void k_mha_few32x4(
+    const float *__restrict__ Q, long sq, const float *__restrict__ K,
+    long sk, const float *__restrict__ V, long sv, float *__restrict__ O,
+    int Nq, int Nk, int dint, float scale2, long total)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= total)
+        return;
+    const int qt = (int)(gid & 3), h = (int)((gid >> 2) & 7);
+    const long row = gid >> 5, p = row / Nq, i = row % Nq;
+    const int c0 = 32 * h + 8 * qt;
+    const float *qr = Q + p * sq + i * dint + c0;
+    const f32x4 q0 = *(const f32x4 *)qr, q1 = *(const f32x4 *)(qr + 4);
+    float sc[8], mx = -INFINITY;
+
+    for (int j = 0; j < 8; j++) {
+        float s = 0.0f;
+
+        if (j < Nk) {
+            const float *kr = K + p * sk + (long)j * dint + c0;
+            const f32x4 k0 = *(const f32x4 *)kr, k1 = *(const f32x4 *)(kr + 4);
+
+            for (int e = 0; e < 4; e++) {
+                s = fmaf(q0[e], k0[e], s);
+                s = fmaf(q1[e], k1[e], s);
+            }
+        }
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        sc[j] = j < Nk ? s * scale2 : -INFINITY;
+        mx = fmaxf(mx, sc[j]);
+    }
+    float sum = 0.0f;
+    f32x4 o0 = {}, o1 = {};
+
+    for (int j = 0; j < 8; j++) {
+        if (j >= Nk)
+            break;
+        const float e = __builtin_amdgcn_exp2f(sc[j] - mx);
+        const float *vr = V + p * sv + (long)j * dint + c0;
+        const f32x4 v0 = *(const f32x4 *)vr, v1 = *(const f32x4 *)(vr + 4);
+
+        sum += e;
+        for (int x = 0; x < 4; x++) {
+            o0[x] = fmaf(e, v0[x], o0[x]);
+            o1[x] = fmaf(e, v1[x], o1[x]);
+        }
+    }
+    const float inv = 1.0f / sum;
+    float *out = O + (p * Nq + i) * dint + c0;
+
+    *(f32x4 *)out = o0 * inv;
+    *(f32x4 *)(out + 4) = o1 * inv;
+}
+
+extern "C" int launch_mha_few32x4(const float *Q, long sq, const float *K,
+                                  long sk, const float *V, long sv, float *O,
+                                  int P, int Nq, int Nk, int dint, float scale,
+                                  void *stream)
+{
+    const long total = (long)P * Nq * 32;
+
+    if (dint != 256 || Nk < 1 || Nk > 8 || ((sq | sk | sv) & 3) ||
+        (((uintptr_t)Q | (uintptr_t)K | (uintptr_t)V | (uintptr_t)O) & 15))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_mha_few32x4, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, (hipStream_t)stream, Q, sq, K, sk, V, sv,
+                       O, Nq, Nk, dint, scale * LOG2E_F, total);
+    return hipGetLastError();
+}
+
 static bool aligned16(long sq, long sk, long sv)
 {
     return sq % 4 == 0 && sk % 4 == 0 && sv % 4 == 0;

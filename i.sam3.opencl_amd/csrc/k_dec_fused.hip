@@ -886,25 +886,29 @@ __global__ __launch_bounds__(256) void k_t2i_merge(const float *__restrict__ par
     Z[gid] = num / den;
 }
 
-/* o [P][8][128]: o[p][i][16 h + c] = Wv[16 h + c] . Z[p][8 h + i] + bv. */
-__global__ __launch_bounds__(256) void k_t2i_unfold(const float *__restrict__ Z,
+/* o [P][8][128]: o[p][i][16 h + c] = Wv[16 h + c] . Z[p][8 h + i] + bv.
+ * Workgroup (p, h): Z rows 8 h .. + 7 and Wv rows 16 h .. + 15 staged in
+ * LDS (Wv rows padded to 257 floats), thread (i, c) one dot product. */
+__global__ __launch_bounds__(128) void k_t2i_unfold(const float *__restrict__ Z,
                                                     const void *Wv, int wv_dt,
                                                     const float *__restrict__ bv,
                                                     float *__restrict__ o, int P)
 {
-    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+    __shared__ float zs[8][256], ws[16][257];
+    const int p = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+    const float *zr = Z + ((long)p * FOLD_ROWS + 8 * h) * 256;
 
-    if (gid >= (long)P * 8 * 128)
-        return;
-    const int col = (int)(gid & 127), i = (int)((gid >> 7) & 7);
-    const long p = gid >> 10;
-    const int h = col >> 4;
-    const float *zr = Z + (p * FOLD_ROWS + 8 * h + i) * 256;
-    float acc = bv[col];
+    for (int x = t; x < 8 * 256; x += 128)
+        zs[x / 256][x % 256] = zr[x];
+    for (int x = t; x < 16 * 256; x += 128)
+        ws[x / 256][x % 256] = wld(Wv, wv_dt, (long)16 * h * 256 + x);
+    __syncthreads();
+    const int i = t / 16, c = t % 16;
+    float acc = bv[16 * h + c];
 
     for (int d = 0; d < 256; d++)
-        acc = fmaf(wld(Wv, wv_dt, (long)col * 256 + d), zr[d], acc);
-    o[gid] = acc;
+        acc = fmaf(ws[c][d], zs[i][d], acc);
+    o[((long)p * 8 + i) * 128 + 16 * h + c] = acc;
 }
 
 extern "C" int launch_t2i_fused(const float *keys, const float *pe,
@@ -925,7 +929,7 @@ extern "C" int launch_t2i_fused(const float *keys, const float *pe,
                        part, T, nsplit);
     hipLaunchKernelGGL(k_t2i_merge, dim3((unsigned)((n + 255) / 256)), dim3(256),
                        0, (hipStream_t)stream, part, Z, P, nsplit);
-    hipLaunchKernelGGL(k_t2i_unfold, dim3((unsigned)((P * 1024L + 255) / 256)),
-                       dim3(256), 0, (hipStream_t)stream, Z, Wv, wv_dt, bv, o, P);
+    hipLaunchKernelGGL(k_t2i_unfold, dim3(P, 8), dim3(128), 0, (hipStream_t)stream,
+                       Z, Wv, wv_dt, bv, o, P);
     return hipGetLastError();
 }

@@ -290,21 +290,25 @@ __global__ __launch_bounds__(256) void k_gemm_bf16(gemm_desc d, int avec,
  * leading dimension are multiples of the elements per 16 bytes (the
  * buffers themselves come from hipMalloc, 256-byte aligned). */
 /* Small GEMMs (a few 128 x 128 tiles: the decoder's per-token linears of
- * 8 P rows): one wave per 32 x 32 tile, no LDS; each lane loads its MFMA
- * operand fragments straight from memory (A row m = lane % 32 and B row
- * n = lane % 32 of the Linear weight, 8 consecutive k per lane half), bf16
- * MFMA with f32 accumulation over K / 16 steps, the usual epilogue.
- * Unbatched, B stored N x K, K % 16 == 0, 16-byte aligned operand rows
+ * 8 P rows): a workgroup per 32 x 32 tile whose 4 waves split K four
+ * ways; no operand staging: each lane loads its MFMA fragments straight
+ * from memory (A row m = lane % 32 and B row n = lane % 32 of the Linear
+ * weight, 8 consecutive k per lane half), bf16 MFMA with f32 accumulation;
+ * the four partial tiles are summed through LDS, then the usual epilogue.
+ * Unbatched, B stored N x K, K % 64 == 0, 16-byte aligned operand rows
  * (checked by the launcher). Rows / columns past M / N read row 0 and are
  * not stored. */
-__global__ __launch_bounds__(64) void k_gemm_small(gemm_desc d)
+__global__ __launch_bounds__(256) void k_gemm_small(gemm_desc d)
 {
-    const int l = threadIdx.x, h = l >> 5, l32 = l & 31;
+    __shared__ float red[3][16][64];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5, l32 = l & 31;
     const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
     const int m = m0 + l32 < d.M ? m0 + l32 : 0, n = n0 + l32 < d.N ? n0 + l32 : 0;
+    const int kq = d.K / 4; /* a multiple of 16 */
     f32x16 acc = {};
 
-    for (int k = 8 * h; k < d.K; k += 16) {
+#pragma unroll 4
+    for (int k = w * kq + 8 * h; k < (w + 1) * kq; k += 16) {
         float fa[8], fb[8];
         bf16x8 a, b;
 
@@ -317,6 +321,14 @@ __global__ __launch_bounds__(64) void k_gemm_small(gemm_desc d)
         /* D = A B^T tile: rows m (A operand), columns n (B operand). */
         acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
     }
+    if (w > 0)
+        for (int r = 0; r < 16; r++)
+            red[w - 1][r][l] = acc[r];
+    __syncthreads();
+    if (w > 0)
+        return;
+    for (int r = 0; r < 16; r++)
+        acc[r] += (red[0][r][l] + red[1][r][l]) + red[2][r][l];
     const void *R = d.R ? (const void *)((d.cdt == DT_F32 ? 4 : 2) * d.roff +
                                          (const char *)d.R) : nullptr;
     void *C = (char *)d.C + (d.cdt == DT_F32 ? 4 : 2) * d.coff;
@@ -349,11 +361,11 @@ extern "C" int launch_gemm(const gemm_desc *d, void *stream)
     }
     if (d->unpart_ws > 0)
         return hipErrorInvalidValue; /* row remap: NT kernel only */
-    if (d->mode == MODE_BF16 && d->transb && d->nb == 1 && d->K % 16 == 0 &&
-        avec && bvec && (long)grid.x * grid.y < 64 &&
+    if (d->mode == MODE_BF16 && d->transb && d->nb == 1 && d->K % 64 == 0 &&
+        avec && bvec && (long)grid.x * grid.y <= 64 &&
         ((uintptr_t)d->A & 15) == 0 && ((uintptr_t)d->B & 15) == 0) {
         hipLaunchKernelGGL(k_gemm_small, dim3((d->N + 31) / 32, (d->M + 31) / 32),
-                           dim3(64), 0, s, *d);
+                           dim3(256), 0, s, *d);
         return hipGetLastError();
     }
     if (d->mode == MODE_BF16) {

@@ -163,6 +163,11 @@ int launch_box_bias(float *out, const float *dy, const float *dx, int heads,
 int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,
                        const float *V, long sv, float *O, int P, int Nq,
                        int Nk, int dint, float scale, void *stream);
+/* precision=bf16 few-keys attention for dint 256 (head width 32), Nk <= 8,
+ * 16-byte aligned rows: four lanes per (prompt, query, head). */
+int launch_mha_few32x4(const float *Q, long sq, const float *K, long sk,
+                       const float *V, long sv, float *O, int P, int Nq,
+                       int Nk, int dint, float scale, void *stream);
 /* Split-K token->image attention for c == 16; scratch holds the
  * partial results, mha_manykeys_scratch() bytes (0 when the key range is
  * not split: scratch may then be NULL). */

@@ -403,6 +403,14 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
         hipb_run_end(be, err, "attn_manykeys",
                      4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
     }
+    else if (be->bf16 && c == 32 && Nk <= 8 && (sq | sk | sv) % 4 == 0) {
+        /* precision=bf16: the decoder's token self-attention, four lanes
+         * per (query, head) instead of the reference's one. */
+        err = launch_mha_few32x4(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
+                                 o->ptr, P, Nq, Nk, dint, scale, be->stream);
+        hipb_run_end(be, err, "attn_fewkeys",
+                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+    }
     else {
         err = launch_mha_fewkeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
                                  o->ptr, P, Nq, Nk, dint, scale, be->stream);

@@ -235,6 +235,10 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, bx, s1, 0, 0, 0);
     }
 
+    /* Every wave's reads of Wt are done past this point: the epilogue
+     * reuses its LDS for staging. */
+    __syncthreads();
+
     /* Grouped softmax: register r of tile T_ is row 32 T_ + 8 (r / 4) +
      * 4 hh + r % 4, i.e. head 4 T_ + r / 4 and prompt token 4 hh + r % 4:
      * each head's 8 scores are 4 registers here and 4 in lane l ^ 32. */
@@ -280,22 +284,43 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
         }
     }
 
-    /* + bo + residual, LayerNorm over the 256 channels (128 here, 128 in
-     * lane l ^ 32): channel of register r of tile c is 32 c + 8 (r / 4) +
-     * 4 hh + r % 4, four consecutive channels per (c, r / 4). */
-    const float *rr = R + (long)p * rs + (long)(valid ? j : 0) * 256;
+    /* Epilogue through a per-wave [32 tokens][32 channels] fp32 staging
+     * tile in the (now free) Wt area, so that the residual is read and the
+     * output written as whole 128-byte row segments: in the coalesced
+     * phase lane L takes token 8 k + L / 8, 16-byte chunk L % 8 of the
+     * tile; chunk c of staging row r sits at c ^ (r & 7). Register r of
+     * U^T tile c is channel 32 c + 8 (r / 4) + 4 hh + r % 4, i.e. chunk
+     * 2 (r / 4) + hh of the tile's row l32. The barrier after the S^T
+     * product guarantees every wave is done reading Wt. */
+    /* Nothing of the epilogue is scheduled into the products above (its
+     * loads would stay live across them and spill). */
+    __builtin_amdgcn_sched_barrier(0);
+    char *stg = Ws + 4096 * w;
+    const int j0 = ch0 + 32 * w;
+    const float *rbase = R + (long)p * rs;
+
     float sum = 0.0f;
 
-    for (int c = 0; c < 8; c++)
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        for (int k = 0; k < 4; k++) {
+            /* Rows past T read row T - 1 (no branch around the load). */
+            const int tok = 8 * k + (l >> 3), ck = l & 7;
+            const int jr = j0 + tok < T ? j0 + tok : T - 1;
+            const f32x4 v = *(const f32x4 *)(rbase + (long)jr * 256 + 32 * c + 4 * ck);
+
+            *(f32x4 *)(stg + 128 * tok + 16 * (ck ^ (tok & 7))) = v;
+        }
         for (int q = 0; q < 4; q++) {
-            const int ch = 32 * c + 8 * q + 4 * hh;
-            const f32x4 b4 = *(const f32x4 *)(bo + ch), r4 = *(const f32x4 *)(rr + ch);
+            const f32x4 r4 = *(const f32x4 *)(stg + 128 * l32 + 16 * ((2 * q + hh) ^ (l32 & 7)));
+            const f32x4 b4 = *(const f32x4 *)(bo + 32 * c + 8 * q + 4 * hh);
 
             for (int i = 0; i < 4; i++) {
                 u[c][4 * q + i] += b4[i] + r4[i];
                 sum += u[c][4 * q + i];
             }
         }
+    }
     sum += __shfl_xor(sum, 32, 64);
     const float mean = sum * (1.0f / 256.0f);
     float var = 0.0f;
@@ -307,12 +332,12 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
             var = fmaf(d, d, var);
         }
     var += __shfl_xor(var, 32, 64);
-    const float rsd = 1.0f / sqrtf(var * (1.0f / 256.0f) + eps);
+    const float rsd = __builtin_amdgcn_rsqf(var * (1.0f / 256.0f) + eps);
+    float *obase = out + (long)p * T * 256;
 
-    if (!valid)
-        return;
-    float *orow = out + ((long)p * T + j) * 256;
-    for (int c = 0; c < 8; c++)
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        asm volatile("" ::: "memory");
         for (int q = 0; q < 4; q++) {
             const int ch = 32 * c + 8 * q + 4 * hh;
             const f32x4 g4 = *(const f32x4 *)(g + ch), b4 = *(const f32x4 *)(bln + ch);
@@ -320,8 +345,16 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
 
             for (int i = 0; i < 4; i++)
                 y[i] = fmaf((u[c][4 * q + i] - mean) * rsd, g4[i], b4[i]);
-            *(f32x4 *)(orow + ch) = y;
+            *(f32x4 *)(stg + 128 * l32 + 16 * ((2 * q + hh) ^ (l32 & 7))) = y;
         }
+        for (int k = 0; k < 4; k++) {
+            const int tok = 8 * k + (l >> 3), ck = l & 7;
+            const f32x4 v = *(const f32x4 *)(stg + 128 * tok + 16 * (ck ^ (tok & 7)));
+
+            if (j0 + tok < T)
+                *(f32x4 *)(obase + (long)(j0 + tok) * 256 + 32 * c + 4 * ck) = v;
+        }
+    }
 }
 
 extern "C" int launch_i2t_fused(const float *X, long xs, int K, const float *pe,

@@ -515,6 +515,20 @@ __global__ __launch_bounds__(512, 1) void k_upscale_fused(
         const int jj = valid ? j : 0, y = jj / G, x = jj % G;
         const float *kr = keys + ((long)p * T + jj) * 256;
         float *lr = lowres + (long)p * 3 * (16L * T);
+        /* The token's 256 inputs as the 16 bf16 B operands of G1^T, read
+         * once for the four pixels. */
+        bf16x8 kb[16];
+
+#pragma unroll
+        for (int st = 0; st < 16; st++) {
+            const int c0 = 16 * st + 8 * hh;
+            const f32x4 a0 = *(const f32x4 *)(kr + c0), a1 = *(const f32x4 *)(kr + c0 + 4);
+
+            for (int e = 0; e < 4; e++) {
+                kb[st][e] = (__bf16)a0[e];
+                kb[st][4 + e] = (__bf16)a1[e];
+            }
+        }
         /* A operand of the logits product: row l32 < 3 is mask l32's
          * hypernetwork output, channels 16 s + 8 hh .. + 7; rows 3..31
          * zero. */
@@ -542,28 +556,17 @@ __global__ __launch_bounds__(512, 1) void k_upscale_fused(
                 const int px = 2 * dy + dx;
                 const float *f1 = fs1 + ((long)(2 * y + dy) * (2 * G) + 2 * x + dx) * 64;
                 float sum = 0.0f;
-                /* G1^T tiles 2 px, 2 px + 1: this pixel's 64 channels; the
-                 * token's inputs (re-read per pixel from the cache) as bf16
-                 * B operands. */
+                /* G1^T tiles 2 px, 2 px + 1: this pixel's 64 channels. */
                 f32x16 g1[2] = {};
 
-                #pragma unroll 2
+                #pragma unroll
                 for (int st = 0; st < 16; st++) {
-                    const int c0 = 16 * st + 8 * hh;
-                    const f32x4 a0 = *(const f32x4 *)(kr + c0), a1 = *(const f32x4 *)(kr + c0 + 4);
-                    bf16x8 kb;
-
-                    #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        kb[e] = (__bf16)a0[e];
-                        kb[4 + e] = (__bf16)a1[e];
-                    }
                     #pragma unroll
                     for (int half = 0; half < 2; half++) {
                         const bf16x8 wa = *(const bf16x8 *)(W1s + swz_off(64 * px + 32 * half + l32,
                                                                           2 * st + hh, 512));
 
-                        g1[half] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa, kb, g1[half], 0, 0, 0);
+                        g1[half] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa, kb[st], g1[half], 0, 0, 0);
                     }
                 }
 

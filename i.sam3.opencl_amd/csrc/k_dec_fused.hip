@@ -159,8 +159,8 @@ __device__ __forceinline__ unsigned swz_off(int row, int chunk, int rowbytes)
     return (unsigned)(row * rowbytes + 16 * ((chunk ^ sw) & (nch - 1)));
 }
 
-/* Workgroup = 4 waves = 128 image tokens of one prompt; item (prompt,
- * 128-token chunk) in XCD-contiguous order. X rows of K floats (per-prompt
+/* Workgroup = 4 waves = 128 image tokens of one prompt; items in
+ * XCD-contiguous order, blocked as described at the item decode. X rows of K floats (per-prompt
  * stride xs, 0 = shared), plus PE rows when pe != NULL; residual R
  * (stride rs, 0 = shared); out [P][T][256] may alias R. */
 template <int K>
@@ -182,7 +182,13 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
 
     if (item >= total)
         return;
-    const int p = (int)(item / chunks), ch0 = (int)(item % chunks) * 128;
+    /* Blocks of 8 token chunks, prompt next, chunk fastest: one XCD's
+     * workgroups take 8 chunks of a prompt (its Wt / Y^T reused from L2),
+     * then the same 8 chunks of the next prompt (the rows shared by the
+     * prompts, PE or qp0 and src, reused from L2). */
+    const unsigned cb = item / (8u * P), rem = item - cb * 8u * P;
+    const unsigned nin = chunks - 8 * cb < 8 ? chunks - 8 * cb : 8;
+    const int p = (int)(rem / nin), ch0 = (int)(8 * cb + rem % nin) * 128;
 
     /* Stage the prompt's Wt (64 x K) and Y^T (256 x 64) in LDS. */
     {
@@ -508,9 +514,16 @@ __global__ __launch_bounds__(512, 1) void k_upscale_fused(
     __syncthreads();
     const float *vb0 = vec, *vlw = vec + 64, *vlb = vec + 128, *vb3 = vec + 192;
 
-    for (unsigned item = blockIdx.x * 8 + w; item < items; item += gridDim.x * 8) {
-        const int p = (int)(item / (unsigned)groups);
-        const int j = (int)(item - (unsigned)p * groups) * 32 + l32;
+    /* Items (32-token group, prompt) with the prompt fastest; XCD x (the
+     * workgroups b with b % 8 == x) walks the x-th eighth of that list, so
+     * the feature rows of a group, shared by the prompts, stay in its L2. */
+    const unsigned per_xcd = (items + 7) / 8, ranks = gridDim.x / 8;
+    const unsigned lo = (blockIdx.x % 8) * per_xcd;
+    const unsigned hi = lo + per_xcd < items ? lo + per_xcd : items;
+
+    for (unsigned item = lo + (blockIdx.x / 8) * 8 + w; item < hi; item += ranks * 8) {
+        const int p = (int)(item % (unsigned)P);
+        const int j = (int)(item / (unsigned)P) * 32 + l32;
         const bool valid = j < T;
         const int jj = valid ? j : 0, y = jj / G, x = jj % G;
         const float *kr = keys + ((long)p * T + jj) * 256;
@@ -683,7 +696,10 @@ extern "C" int launch_upscale_fused(const float *keys, const void *W1T16,
                                     int cus, void *stream)
 {
     const long T = (long)G * G, items = (long)P * ((T + 31) / 32);
-    const long grid = (items + 7) / 8 < cus ? (items + 7) / 8 : cus;
+    /* A multiple of 8 workgroups (the XCD split of the item list), at most
+     * one per CU. */
+    const long fill = ((items + 7) / 8 < cus ? (items + 7) / 8 : cus) / 8 * 8;
+    const long grid = fill > 8 ? fill : 8;
 
     if (P < 1 || G < 1 || cus < 1 || items + 8L * cus > 0x7fffffffL ||
         ((uintptr_t)hyper & 15) ||
@@ -726,14 +742,21 @@ __device__ __forceinline__ unsigned vt_off(int d, int k)
 __global__ __launch_bounds__(256, 2) void k_t2i_fused(
     const float *__restrict__ keys, const float *__restrict__ pe,
     const uint16_t *__restrict__ U16, float *__restrict__ part, int T,
-    int nsplit)
+    int P, int nsplit)
 {
     __shared__ __attribute__((aligned(16))) char Ks[64 * 512];
     __shared__ __attribute__((aligned(16))) char Vs[256 * 128];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
               l32 = l & 31;
     const int rt = w & 1, kh = w >> 1;
-    const int p = blockIdx.x / nsplit, sp = blockIdx.x % nsplit;
+    /* XCD-contiguous items, prompt fastest: one XCD's workgroups take the
+     * same key range for consecutive prompts and share its PE rows in L2. */
+    const unsigned total = (unsigned)P * nsplit, per_xcd = (total + 7) / 8;
+    const unsigned item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+
+    if (item >= total)
+        return;
+    const int p = (int)(item % (unsigned)P), sp = (int)(item / (unsigned)P);
     const int nblk = (T + 63) / 64;
     const int kb0 = sp * nblk / nsplit, kb1 = (sp + 1) * nblk / nsplit;
     const float *kp = keys + (long)p * T * 256;
@@ -884,7 +907,7 @@ __global__ __launch_bounds__(256, 2) void k_t2i_fused(
                 *(f32x4 *)(zo + d) = o;
             }
         if (hh == 0) {
-            float *ml = part + (long)gridDim.x * FOLD_ROWS * 256 + rec * 2;
+            float *ml = part + (long)P * nsplit * FOLD_ROWS * 256 + rec * 2;
 
             ml[0] = mm;
             ml[1] = lsum * c0 + l1 * c1;
@@ -960,9 +983,9 @@ extern "C" int launch_t2i_fused(const float *keys, const float *pe,
         (long)P * nsplit > 0x7fffffffL ||
         (((uintptr_t)keys | (uintptr_t)pe | (uintptr_t)U16 | (uintptr_t)part) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_t2i_fused, dim3((unsigned)(P * nsplit)), dim3(256), 0,
-                       (hipStream_t)stream, keys, pe, (const uint16_t *)U16,
-                       part, T, nsplit);
+    hipLaunchKernelGGL(k_t2i_fused, dim3((unsigned)((P * nsplit + 7) / 8 * 8)),
+                       dim3(256), 0, (hipStream_t)stream, keys, pe,
+                       (const uint16_t *)U16, part, T, P, nsplit);
     hipLaunchKernelGGL(k_t2i_merge, dim3((unsigned)((n + 255) / 256)), dim3(256),
                        0, (hipStream_t)stream, part, Z, P, nsplit);
     hipLaunchKernelGGL(k_t2i_unfold, dim3(P, 8), dim3(128), 0, (hipStream_t)stream,

@@ -200,6 +200,7 @@ void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a)
 
         if (nsplit > nblk)
             nsplit = nblk;
+
         linear(m, P * NTOK, SAM_DIM, 128, d->qin, 0, a->qw, a->qb, d->sq, 0,
                ACT_NONE, 0);
         if (hipb_failed())

@@ -386,20 +386,50 @@ def mask_decoder(hip, steps, warmup, precisions=("bf16", "fp32"), P=64,
         m.m.grid = grid
         dec = hip.Decoder(m, w, P, img=14 * grid)
         dec.set_image(emb, s0, s1)
+        ms_eager = timed(be, lambda: dec.decode(pts), steps, warmup)
+        # The device sequence replayed from a HIP graph (one launch after
+        # the token upload).
+        dec.graph(P)
         ms = timed(be, lambda: dec.decode(pts), steps, warmup)
+        dec.graph(P, False)
         hip.prof_reset()
         be._b.profile = 1
         dec.decode(pts)
         be.finish()
         be._b.profile = 0
         tab = hip.prof_table()
-        out[p] = {"ms": round(ms, 3),
+        out[p] = {"ms": round(ms, 3), "ms_kernel_by_kernel": round(ms_eager, 3),
                   "profile_ms": {r[0]: round(r[1], 3) for r in
                                  sorted(tab, key=lambda r: -r[1])[:10]}}
         dec.free()
         m.free()
         be.free()
     return out
+
+
+def mask_decoder_cpu(P=2, grid=72):
+    """The oracle's restatement of sam_decode (fp32, the reference's GPU
+    dispatch arithmetic, OpenMP over the host cores) for P prompts on the
+    same synthetic inputs: seconds per prompt, for scale against the
+    64-prompt GPU figure."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as orc
+    hip = load_hip()
+    g = np.random.default_rng(29)
+    T = grid * grid
+    w = hip.random_decoder_weights(29)
+    emb = g.standard_normal((T, 256), dtype=np.float32)
+    s0 = g.standard_normal((16 * T, 32), dtype=np.float32)
+    s1 = g.standard_normal((4 * T, 64), dtype=np.float32)
+    pts = g.uniform(0, 14 * grid, (P, 2)).astype(np.float32)
+    dw = orc.DecoderW(w, grid, img=14 * grid)
+    prep = orc.dec_prepare(dw, emb)
+    t0 = time.perf_counter()
+    orc.sam_decode(dw, pts, prep, s0, s1)
+    sec = time.perf_counter() - t0
+    return {"ms_per_prompt": round(1e3 * sec / P, 2), "cores": orc.threads(),
+            "kind": "port", "sample": "%d prompts, fp32, oracle restatement"
+                                      % P}
 
 
 def main():
@@ -494,6 +524,9 @@ def main():
     w32_ms = timed(be32, w32.attn_f32, max(3, args.steps // 10), sub_warm)
 
     dec = decoder(hip, be32, sub_steps, sub_warm)
+    mdec = mask_decoder(hip, max(3, sub_steps // 2), 2)
+    if not args.no_cpu:
+        mdec["cpu_oracle"] = mask_decoder_cpu()
     bb = backbone(hip, 5, 2)
     text = text_attention(hip, sub_steps, sub_warm)
 
@@ -535,6 +568,7 @@ def main():
             "windowed_ms": round(w32_ms, 4),
             "windowed_TFLOP/s": round(win.flops() / w32_ms / 1e9, 2)},
         "decoder_fp32": dec,
+        "mask_decoder": mdec,
         "backbone": bb,
         "text_attention": text,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),

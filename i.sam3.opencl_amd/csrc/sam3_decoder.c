@@ -116,6 +116,16 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
     }
 }
 
+static void dec_graph_drop(struct sam_decoder *d)
+{
+    if (d->graph_exec)
+        hipGraphExecDestroy((hipGraphExec_t)d->graph_exec);
+    if (d->graph)
+        hipGraphDestroy((hipGraph_t)d->graph);
+    d->graph_exec = d->graph = NULL;
+    d->graph_P = 0;
+}
+
 void sam_dec_free(struct sam_model *m)
 {
     struct sam_decoder *d = m->dec;
@@ -133,6 +143,7 @@ void sam_dec_free(struct sam_model *m)
 
     if (m->hip)
         hipb_finish(m->hip);
+    dec_graph_drop(d);
     for (i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         hipb_release(bufs[i]);
     free(d->h_queries);
@@ -377,42 +388,17 @@ void convt_scatter(struct sam_model *m, hipb_mem G, hipb_mem out,
     hipb_run_end(be, err, "convt_scatter", 0.0);
 }
 
-void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
+/* The device part of sam_decode for P prompts whose tokens are in qpe /
+ * qry: the two-way transformer, the hypernetwork and IoU heads (raw IoU
+ * outputs in sv), the upscaling and the logits. Host-synchronisation
+ * free, so that sam_dec_graph can capture it. */
+static void dec_kernels(struct sam_model *m, int P)
 {
-    struct sam_decoder *d = dec_of(m, "sam_decode");
+    struct sam_decoder *d = m->dec;
     const int G = m->grid;
     const long T = (long)G * G, n = (long)P * NTOK * SAM_DIM;
-    const struct sam_dec_layer *L0, *L1;
-    float *tok;
-    int p, i, err;
-
-    if (!d)
-        return;
-    if (P < 1 || P > d->batch) {
-        hipb_fatal("sam_decode: batch overflow");
-        return;
-    }
-    L0 = &d->layers[0];
-    L1 = &d->layers[1];
-    tok = d->h_queries;
-
-    /* Prompt tokens: object score token, IoU token, 4 mask tokens, the
-     * positive point and the padding point (no box prompt). */
-    for (p = 0; p < P; p++) {
-        float *t = tok + (long)p * NTOK * SAM_DIM;
-
-        memcpy(t, d->obj_token, SAM_DIM * sizeof(float));
-        memcpy(t + SAM_DIM, d->iou_token, SAM_DIM * sizeof(float));
-        memcpy(t + 2 * SAM_DIM, d->mask_tokens, 4 * SAM_DIM * sizeof(float));
-        pe_encode(d, (points[2 * p] + 0.5f) / d->img,
-                  (points[2 * p + 1] + 0.5f) / d->img, t + 6 * SAM_DIM);
-        for (i = 0; i < SAM_DIM; i++) {
-            t[6 * SAM_DIM + i] += d->point_emb[1][i];
-            t[7 * SAM_DIM + i] = d->not_a_point[i];
-        }
-    }
-    hipb_write(m->hip, d->qpe, 0, tok, n * sizeof(float));
-    hipb_copy(m->hip, d->qpe, d->qry, 0, 0, n * sizeof(float));
+    const struct sam_dec_layer *L0 = &d->layers[0], *L1 = &d->layers[1];
+    int i, err;
 
     /* Layer 0: self attention, token -> image attention on the shared
      * image keys (stride 0), token MLP, image -> token attention. */
@@ -512,6 +498,114 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
                                  (int)(16 * T), m->hip->stream);
         hipb_run_end(m->hip, err, "mask_logits", 0.0);
     }
+}
+
+void sam_dec_graph(struct sam_model *m, int P, int enable)
+{
+    struct sam_decoder *d = dec_of(m, "sam_dec_graph");
+    struct hipb_backend *b = m->hip;
+    hipGraph_t g = NULL;
+    hipGraphExec_t x = NULL;
+    void *scratch;
+    int err;
+
+    if (!d)
+        return;
+    hipb_finish(b);
+    dec_graph_drop(d);
+    if (!enable)
+        return;
+    if (b->profile) {
+        hipb_fatal("sam_dec_graph: profiling runs the kernels one by one");
+        return;
+    }
+    if (P < 1 || P > d->batch) {
+        hipb_fatal("sam_dec_graph: %d prompts for a batch of %d", P, d->batch);
+        return;
+    }
+    dec_kernels(m, P); /* allocates whatever scratch is still missing */
+    hipb_finish(b);
+    if (hipb_failed())
+        return;
+    scratch = b->scratch;
+    err = hipStreamBeginCapture((hipStream_t)b->stream,
+                                hipStreamCaptureModeRelaxed);
+    if (err != hipSuccess) {
+        hipb_fatal("sam_dec_graph: hipStreamBeginCapture: %s (%d)",
+                   hipb_errstr(err), err);
+        return;
+    }
+    dec_kernels(m, P);
+    err = hipStreamEndCapture((hipStream_t)b->stream, &g);
+    if (hipb_failed() || err != hipSuccess || !g || b->scratch != scratch) {
+        if (g)
+            hipGraphDestroy(g);
+        if (!hipb_failed())
+            hipb_fatal("sam_dec_graph: capture failed: %s (%d)",
+                       hipb_errstr(err), err);
+        return;
+    }
+    err = hipGraphInstantiate(&x, g, NULL, NULL, 0);
+    if (err != hipSuccess) {
+        hipGraphDestroy(g);
+        hipb_fatal("sam_dec_graph: hipGraphInstantiate: %s (%d)",
+                   hipb_errstr(err), err);
+        return;
+    }
+    d->graph = g;
+    d->graph_exec = x;
+    d->graph_P = P;
+    d->graph_scratch = scratch;
+}
+
+void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
+{
+    struct sam_decoder *d = dec_of(m, "sam_decode");
+    const long n = (long)P * NTOK * SAM_DIM;
+    float *tok;
+    int p, i, err;
+
+    if (!d)
+        return;
+    if (P < 1 || P > d->batch) {
+        hipb_fatal("sam_decode: batch overflow");
+        return;
+    }
+    tok = d->h_queries;
+
+    /* Prompt tokens: object score token, IoU token, 4 mask tokens, the
+     * positive point and the padding point (no box prompt). */
+    for (p = 0; p < P; p++) {
+        float *t = tok + (long)p * NTOK * SAM_DIM;
+
+        memcpy(t, d->obj_token, SAM_DIM * sizeof(float));
+        memcpy(t + SAM_DIM, d->iou_token, SAM_DIM * sizeof(float));
+        memcpy(t + 2 * SAM_DIM, d->mask_tokens, 4 * SAM_DIM * sizeof(float));
+        pe_encode(d, (points[2 * p] + 0.5f) / d->img,
+                  (points[2 * p + 1] + 0.5f) / d->img, t + 6 * SAM_DIM);
+        for (i = 0; i < SAM_DIM; i++) {
+            t[6 * SAM_DIM + i] += d->point_emb[1][i];
+            t[7 * SAM_DIM + i] = d->not_a_point[i];
+        }
+    }
+    hipb_write(m->hip, d->qpe, 0, tok, n * sizeof(float));
+    hipb_copy(m->hip, d->qpe, d->qry, 0, 0, n * sizeof(float));
+
+    /* The captured device sequence when it was captured for this P and
+     * the backend scratch it uses has not moved since. */
+    if (d->graph_exec && !m->hip->profile) {
+        if (d->graph_P == P && d->graph_scratch == m->hip->scratch) {
+            err = hipGraphLaunch((hipGraphExec_t)d->graph_exec,
+                                 (hipStream_t)m->hip->stream);
+            hipb_run_end(m->hip, err, "decoder_graph", 0.0);
+        }
+        else
+            dec_kernels(m, P);
+    }
+    else
+        dec_kernels(m, P);
+    if (hipb_failed())
+        return;
     /* IoU predictions 1..3 through the sigmoid (iou_prediction_use_sigmoid). */
     {
         float *raw = d->h_queries;

@@ -37,6 +37,7 @@ EXPORTS = [
     "sam_trunk_graph", "softmax_ext", "attend", "sam_dec_init",
     "sam_dec_free", "sam_dec_prepare", "sam_decode", "t2i_attention",
     "i2t_attention", "convt_scatter", "sam_postprocess", "sam_read_mask",
+    "sam_dec_graph",
 ]
 
 
@@ -131,7 +132,9 @@ class SamDecoder(ctypes.Structure):
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
         [("mask_cap", ctypes.c_size_t)] + \
         [(n, Mem) for n in ("fold_w", "fold_b", "fold_y", "up_w1t",
-                            "up_w2t", "t2i_part", "t2i_z")]
+                            "up_w2t", "t2i_part", "t2i_z")] + \
+        [("graph", ctypes.c_void_p), ("graph_exec", ctypes.c_void_p),
+         ("graph_P", ctypes.c_int), ("graph_scratch", ctypes.c_void_p)]
 
 
 _lib = None
@@ -219,6 +222,7 @@ def lib():
     L.sam_dec_free.argtypes = [MP]
     L.sam_dec_prepare.argtypes = [MP]
     L.sam_decode.argtypes = [MP, c_int, vp, vp]
+    L.sam_dec_graph.argtypes = [MP, c_int, c_int]
     L.t2i_attention.argtypes = [MP, c_int, ctypes.POINTER(SamAttnW)]
     L.i2t_attention.argtypes = [MP, c_int, c_int]
     L.convt_scatter.argtypes = [MP, Mem, Mem, Mem, Mem, c_int, c_int, c_int,
@@ -635,6 +639,10 @@ class Decoder:
         _call(_lib.sam_decode, self.model.ptr, P, pts.ctypes.data,
               iou.ctypes.data)
         return iou
+
+    def graph(self, P, enable=True):
+        """sam_dec_graph: capture (or drop) the device sequence for P."""
+        _call(_lib.sam_dec_graph, self.model.ptr, P, int(enable))
 
     def lowres(self, P):
         L = 4 * self.grid

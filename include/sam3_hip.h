@@ -415,6 +415,11 @@ struct sam_decoder {
      * ((2 CUs + batch) records of 64 rows x 258 floats) and the merged
      * weighted key sums Z [batch][64][256]. */
     hipb_mem t2i_part, t2i_z;
+    /* sam_dec_graph: hipGraph_t, hipGraphExec_t of the device sequence
+     * for graph_P prompts, and the backend scratch it was captured with. */
+    void *graph, *graph_exec;
+    int graph_P;
+    void *graph_scratch;
 };
 
 /* Attach decoder d to m (grid from m) and allocate its caches and batch
@@ -433,6 +438,14 @@ void sam_dec_prepare(struct sam_model *m);
  * (x, y pairs in encoder input pixels); iou [P][3] receives the multimask
  * IoU predictions, d->lowres the [P][3][4 grid]^2 low-resolution logits. */
 void sam_decode(struct sam_model *m, int P, const float *points, float *iou);
+
+/* Capture (enable = 1) or drop (0) a HIP graph of sam_decode's device
+ * sequence for P prompts; sam_decode then replays it (one launch after
+ * the token upload) whenever it is called with that P and the backend's
+ * scratch has not been reallocated, and runs the kernels one by one
+ * otherwise. Profiling (profile=1) always runs them one by one. No
+ * counterpart in the reference (whose OpenCL queue has no graphs). */
+void sam_dec_graph(struct sam_model *m, int P, int enable);
 
 /* Token -> image attention with per-prompt keys and residual into the
  * queries (static t2i_attention, sam3_model.c:1212-1229); kin = keys +

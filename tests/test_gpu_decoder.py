@@ -209,3 +209,30 @@ def test_logits_postprocess_and_read(hip, be, orc, weights):
             assert np.all(got_low[1, 10:13, 10:13] == 10.0)
     finally:
         d.free()
+
+
+def test_decode_graph_replays(hip, be, orc, weights):
+    """sam_dec_graph: replays of the captured device sequence give the
+    eager decode's IoU and logits bit for bit, for new points on every
+    call, with eager work and host reads between the replays; another P
+    runs the kernels one by one."""
+    G, P = 16, 4
+    d = Dec(hip, be, orc, weights, G, P, 48)
+    try:
+        g = np.random.default_rng(49)
+        pts = [g.uniform(0, 14 * G, (P, 2)).astype(np.float32) for _ in range(3)]
+        eager = [(d.dec.decode(x), d.dec.lowres(P)) for x in pts]
+        d.dec.graph(P)
+        for rep in range(2):
+            for x, (iou, low) in zip(pts, eager):
+                got_iou = d.dec.decode(x)
+                assert np.array_equal(got_iou, iou)
+                assert np.array_equal(d.dec.lowres(P), low)
+        # A different prompt count is not the captured one: eager path
+        # (its key splits differ, so the match is to the precision's bar).
+        d.dec.decode(pts[0][:2])
+        assert report("graph other P %s" % be.precision, d.dec.lowres(2),
+                      eager[0][1][:2]) <= TOL[be.precision]
+        d.dec.graph(P, False)
+    finally:
+        d.free()

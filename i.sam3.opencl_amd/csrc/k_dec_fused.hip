@@ -992,3 +992,92 @@ extern "C" int launch_t2i_fused(const float *keys, const float *pe,
                        Z, Wv, wv_dt, bv, o, P);
     return hipGetLastError();
 }
+
+/* ------------------------------------------------------------------ */
+/* Hypernetwork MLPs and IoU head                                      */
+/* ------------------------------------------------------------------ */
+
+/* Workgroup (prompt p, head k): k = 0 the IoU head on token 1 (4 raw
+ * outputs into iou [P][4]), k = 1..3 the hypernetwork MLP of mask token
+ * k on token 2 + k (32 outputs into hyper [P][3][32]); three Linear
+ * layers 256 -> 256 (ReLU) -> 256 (ReLU) -> nout, the layer input in LDS,
+ * thread o one output. W*[k] are [256][256], [256][256], [nout][256]. */
+struct dec_heads_w {
+    const void *w0[4], *w1[4], *w2[4];
+    const float *b0[4], *b1[4], *b2[4];
+    int dt;
+};
+
+/* Output o = thread: its weight row as 16-byte loads, all independent
+ * (bf16 rows: 32 loads of 8; fp32 rows: 64 loads of 4), against the layer
+ * input in LDS. */
+__device__ __forceinline__ float row_dot(const void *W, int dt, int o,
+                                         const float *x)
+{
+    float acc = 0.0f;
+
+    if (dt == DT_BF16) {
+        const bf16x8 *r = (const bf16x8 *)((const uint16_t *)W + (long)o * 256);
+
+#pragma unroll 8
+        for (int c = 0; c < 32; c++) {
+            const bf16x8 v = r[c];
+
+            for (int e = 0; e < 8; e++)
+                acc = fmaf((float)v[e], x[8 * c + e], acc);
+        }
+    }
+    else
+        for (int i = 0; i < 256; i++)
+            acc = fmaf(wld(W, dt, (long)o * 256 + i), x[i], acc);
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void k_dec_heads(const float *__restrict__ qry,
+                                                   dec_heads_w hw,
+                                                   float *__restrict__ hyper,
+                                                   float *__restrict__ iou)
+{
+    __shared__ float xa[256], xb[256];
+    const int p = blockIdx.x, k = blockIdx.y, t = threadIdx.x;
+    const int tok = k ? 2 + k : 1, nout = k ? 32 : 4;
+
+    xa[t] = qry[((long)p * 8 + tok) * 256 + t];
+    __syncthreads();
+    xb[t] = fmaxf(row_dot(hw.w0[k], hw.dt, t, xa) + hw.b0[k][t], 0.0f);
+    __syncthreads();
+    xa[t] = fmaxf(row_dot(hw.w1[k], hw.dt, t, xb) + hw.b1[k][t], 0.0f);
+    __syncthreads();
+    if (t < nout) {
+        const float v = row_dot(hw.w2[k], hw.dt, t, xa) + hw.b2[k][t];
+
+        if (k)
+            hyper[(long)p * 96 + (k - 1) * 32 + t] = v;
+        else
+            iou[(long)p * 4 + t] = v;
+    }
+}
+
+extern "C" int launch_dec_heads(const float *qry, const void *const w0[4],
+                                const void *const w1[4], const void *const w2[4],
+                                const float *const b0[4], const float *const b1[4],
+                                const float *const b2[4], int dt, float *hyper,
+                                float *iou, int P, void *stream)
+{
+    dec_heads_w hw;
+
+    for (int k = 0; k < 4; k++) {
+        hw.w0[k] = w0[k];
+        hw.w1[k] = w1[k];
+        hw.w2[k] = w2[k];
+        hw.b0[k] = b0[k];
+        hw.b1[k] = b1[k];
+        hw.b2[k] = b2[k];
+    }
+    hw.dt = dt;
+    if (P < 1)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dec_heads, dim3(P, 4), dim3(256), 0, (hipStream_t)stream,
+                       qry, hw, hyper, iou);
+    return hipGetLastError();
+}

@@ -433,25 +433,48 @@ static void dec_kernels(struct sam_model *m, int P)
               ACT_NONE);
 
     /* Hypernetwork MLPs of mask tokens 1..3 (into d->hyper [P][3][32])
-     * and the IoU head as GEMMs over the P prompts' token rows (row
-     * stride NTOK x 256), the hidden layers in d->sq / d->sk, the IoU
-     * head's 4 outputs in d->sv. */
-    for (i = 0; i <= 3; i++) {
-        hipb_mem const *W = i ? d->hyper_w[i] : d->iou_w;
-        hipb_mem const *B = i ? d->hyper_b[i] : d->iou_b;
-        const int tok_row = i ? 2 + i : 1, nout = i ? 32 : 4;
+     * and the IoU head (4 raw outputs into d->sv): on the bf16 path one
+     * kernel for all four; else GEMMs over the P prompts' token rows (row
+     * stride NTOK x 256) with the hidden layers in d->sq / d->sk. */
+    if (d->fold_w && d->iou_w[0]->dtype == d->hyper_w[1][0]->dtype) {
+        const void *w0[4], *w1[4], *w2[4];
+        const float *b0[4], *b1[4], *b2[4];
 
-        gemm(m, P, SAM_DIM, SAM_DIM, mat(d->qry, (long)tok_row * SAM_DIM,
-                                         NTOK * SAM_DIM),
-             mat(W[0], 0, SAM_DIM), 1, mat(d->sq, 0, SAM_DIM), 1, 1, B[0],
-             NULL, 0, 1.0f, ACT_RELU);
-        gemm(m, P, SAM_DIM, SAM_DIM, mat(d->sq, 0, SAM_DIM),
-             mat(W[1], 0, SAM_DIM), 1, mat(d->sk, 0, SAM_DIM), 1, 1, B[1],
-             NULL, 0, 1.0f, ACT_RELU);
-        gemm(m, P, nout, SAM_DIM, mat(d->sk, 0, SAM_DIM),
-             mat(W[2], 0, SAM_DIM), 1,
-             i ? mat(d->hyper, (long)(i - 1) * 32, 96) : mat(d->sv, 0, 4), 1,
-             1, B[2], NULL, 0, 1.0f, ACT_NONE);
+        for (i = 0; i <= 3; i++) {
+            hipb_mem const *W = i ? d->hyper_w[i] : d->iou_w;
+            hipb_mem const *B = i ? d->hyper_b[i] : d->iou_b;
+
+            w0[i] = W[0]->ptr;
+            w1[i] = W[1]->ptr;
+            w2[i] = W[2]->ptr;
+            b0[i] = B[0]->ptr;
+            b1[i] = B[1]->ptr;
+            b2[i] = B[2]->ptr;
+        }
+        hipb_run_begin(m->hip);
+        err = launch_dec_heads(d->qry->ptr, w0, w1, w2, b0, b1, b2,
+                               d->iou_w[0]->dtype, d->hyper->ptr, d->sv->ptr,
+                               P, m->hip->stream);
+        hipb_run_end(m->hip, err, "dec_heads", 0.0);
+    }
+    else {
+        for (i = 0; i <= 3; i++) {
+            hipb_mem const *W = i ? d->hyper_w[i] : d->iou_w;
+            hipb_mem const *B = i ? d->hyper_b[i] : d->iou_b;
+            const int tok_row = i ? 2 + i : 1, nout = i ? 32 : 4;
+
+            gemm(m, P, SAM_DIM, SAM_DIM, mat(d->qry, (long)tok_row * SAM_DIM,
+                                             NTOK * SAM_DIM),
+                 mat(W[0], 0, SAM_DIM), 1, mat(d->sq, 0, SAM_DIM), 1, 1, B[0],
+                 NULL, 0, 1.0f, ACT_RELU);
+            gemm(m, P, SAM_DIM, SAM_DIM, mat(d->sq, 0, SAM_DIM),
+                 mat(W[1], 0, SAM_DIM), 1, mat(d->sk, 0, SAM_DIM), 1, 1, B[1],
+                 NULL, 0, 1.0f, ACT_RELU);
+            gemm(m, P, nout, SAM_DIM, mat(d->sk, 0, SAM_DIM),
+                 mat(W[2], 0, SAM_DIM), 1,
+                 i ? mat(d->hyper, (long)(i - 1) * 32, 96) : mat(d->sv, 0, 4), 1,
+                 1, B[2], NULL, 0, 1.0f, ACT_NONE);
+        }
     }
     if (hipb_failed())
         return;

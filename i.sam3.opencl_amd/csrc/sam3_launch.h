@@ -234,6 +234,16 @@ int launch_t2i_fused(const float *keys, const float *pe, const void *U16,
                      const float *bv, float *o, int T, int P, int nsplit,
                      void *stream);
 
+/* The decoder's IoU head (head 0, token 1, 4 raw outputs into iou [P][4])
+ * and hypernetwork MLPs (heads 1..3, tokens 3..5, into hyper [P][3][32])
+ * on qry [P][8][256]: three Linear layers each, weights of element type
+ * dt. */
+int launch_dec_heads(const float *qry, const void *const w0[4],
+                     const void *const w1[4], const void *const w2[4],
+                     const float *const b0[4], const float *const b1[4],
+                     const float *const b2[4], int dt, float *hyper,
+                     float *iou, int P, void *stream);
+
 /* fp32 -> bf16 / half conversion of count elements (weight uploads). */
 int launch_convert(const float *src, void *dst, int dst_dt, size_t count,
                    void *stream);

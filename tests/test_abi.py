@@ -40,12 +40,16 @@ def test_struct_layouts_match_header(hip):
     src = open(HEADER).read()
     for cls, cname in ((hip.HipbBuf, "hipb_buf"), (hip.Opnd, "opnd"),
                        (hip.HipbBackend, "hipb_backend"),
-                       (hip.VitBlock, "vit_block"), (hip.SamModel, "sam_model")):
+                       (hip.VitBlock, "vit_block"), (hip.SamModel, "sam_model"),
+                       (hip.SamAttnW, "sam_attn_w"),
+                       (hip.SamDecLayer, "sam_dec_layer"),
+                       (hip.SamDecoder, "sam_decoder")):
         body = re.search(r"struct %s \{(.*?)\};" % cname, src, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
-        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_]*)\s*(?:\[[^\]]*\])?\s*[,;]",
+        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_]*)\s*(?:\[[^\]]*\])*\s*[,;]",
                             body)
-        assert [f[0] for f in cls._fields_] == fields
+        # "self" is a Python keyword-like name the mirror spells "self_".
+        assert [f[0].rstrip("_") for f in cls._fields_] == fields, cname
 
 
 def _has_gpu():

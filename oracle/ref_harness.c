@@ -12,7 +12,10 @@
  * sam3_model.c:314-330, softmax_rows() sam3_model.c:332-341,
  * window_partition() / window_unpartition_add() sam3_model.c:360-392,
  * mha() sam3_model.c:413-451, rope_apply() sam3_model.c:965-978,
- * run1d() sam3_model.c:209-214, softmax_ext in attend() sam3_text.c:320-335.
+ * run1d() sam3_model.c:209-214, softmax_ext in attend() sam3_text.c:320-335,
+ * convt_scatter() sam3_model.c:394-411, mask_logits in sam_decode()
+ * sam3_model.c:1387-1398, mask_post in sam_postprocess()
+ * sam3_model.c:1500-1515.
  */
 #define CL_TARGET_OPENCL_VERSION 120
 #define CL_USE_DEPRECATED_OPENCL_1_2_APIS
@@ -494,6 +497,135 @@ int ref_mha(int P, int Nq, int Nk, int dint, const float *Q, long qlen,
     clReleaseMemObject(dK);
     clReleaseMemObject(dV);
     clReleaseMemObject(dO);
+    clReleaseKernel(k);
+    return rc;
+}
+
+/* convt_scatter (host convt_scatter, sam3_model.c:394-411): G [(P H W)]
+ * [Co 4], out [P][2H][2W][Co], add may be NULL. */
+int ref_convt_scatter(const float *G, float *out, const float *bias,
+                      const float *add, int P, int H, int W, int Co, int act)
+{
+    cl_int err, cH = H, cW = W, cCo = Co, cact = act;
+    cl_int total = P * 4 * H * W * Co;
+    cl_mem dG, dO, dB, dA;
+    cl_kernel k = clCreateKernel(prog, "convt_scatter", &err);
+    int rc;
+
+    CHECK(err, "clCreateKernel");
+    dG = buf_in(G, (size_t)total * 4, &err);
+    CHECK(err, "G");
+    dO = buf_in(out, (size_t)total * 4, &err);
+    CHECK(err, "out");
+    dB = buf_in(bias, (size_t)Co * 4, &err);
+    CHECK(err, "bias");
+    dA = buf_in(add, (size_t)4 * H * W * Co * 4, &err);
+    CHECK(err, "add");
+    ARG(k, 0, dG);
+    ARG(k, 1, dO);
+    ARG(k, 2, dB);
+    ARG(k, 3, dA);
+    ARG(k, 4, cH);
+    ARG(k, 5, cW);
+    ARG(k, 6, cCo);
+    ARG(k, 7, total);
+    ARG(k, 8, cact);
+    rc = run1d(k, (size_t)total, "convt_scatter");
+    if (rc == 0)
+        CHECK(clEnqueueReadBuffer(q, dO, CL_TRUE, 0, (size_t)total * 4, out, 0,
+                                  NULL, NULL),
+              "read out");
+    clReleaseMemObject(dG);
+    clReleaseMemObject(dO);
+    clReleaseMemObject(dB);
+    if (dA)
+        clReleaseMemObject(dA);
+    clReleaseKernel(k);
+    return rc;
+}
+
+/* mask_logits as sam_decode launches it (sam3_model.c:1387-1398): U
+ * [P][npix][32], hyper [P][96], out [P][3][npix]. */
+int ref_mask_logits(const float *U, const float *hyper, float *out, int P,
+                    int npix)
+{
+    cl_int err, cn = npix, total = P * npix;
+    cl_mem dU, dH, dO;
+    cl_kernel k = clCreateKernel(prog, "mask_logits", &err);
+    int rc;
+
+    CHECK(err, "clCreateKernel");
+    dU = buf_in(U, (size_t)total * 32 * 4, &err);
+    CHECK(err, "U");
+    dH = buf_in(hyper, (size_t)P * 96 * 4, &err);
+    CHECK(err, "hyper");
+    dO = buf_in(out, (size_t)P * 3 * npix * 4, &err);
+    CHECK(err, "out");
+    ARG(k, 0, dU);
+    ARG(k, 1, dH);
+    ARG(k, 2, dO);
+    ARG(k, 3, cn);
+    ARG(k, 4, total);
+    rc = run1d(k, (size_t)total, "mask_logits");
+    if (rc == 0)
+        CHECK(clEnqueueReadBuffer(q, dO, CL_TRUE, 0, (size_t)P * 3 * npix * 4,
+                                  out, 0, NULL, NULL),
+              "read out");
+    clReleaseMemObject(dU);
+    clReleaseMemObject(dH);
+    clReleaseMemObject(dO);
+    clReleaseKernel(k);
+    return rc;
+}
+
+/* mask_post as sam_postprocess launches it (sam3_model.c:1500-1515):
+ * 16 x 16 groups over (out_w, out_h) rounded up, one plane per z; stats
+ * [n][6] hold the initial values on entry. */
+int ref_mask_post(const float *lowres, int planes, const int *sel, int n,
+                  int L, int out_h, int out_w, float offset,
+                  unsigned char *mask, int *stats)
+{
+    cl_int err, cL = L, coh = out_h, cow = out_w;
+    cl_float coff = offset;
+    cl_mem dL, dS, dM, dT;
+    cl_kernel k = clCreateKernel(prog, "mask_post", &err);
+    size_t g[3], l[3] = {16, 16, 1};
+    int rc;
+
+    CHECK(err, "clCreateKernel");
+    dL = buf_in(lowres, (size_t)planes * L * L * 4, &err);
+    CHECK(err, "lowres");
+    dS = buf_in(sel, (size_t)n * 4, &err);
+    CHECK(err, "sel");
+    dM = clCreateBuffer(ctx, CL_MEM_READ_WRITE, (size_t)n * out_h * out_w,
+                        NULL, &err);
+    CHECK(err, "mask");
+    dT = buf_in(stats, (size_t)n * 6 * 4, &err);
+    CHECK(err, "stats");
+    ARG(k, 0, dL);
+    ARG(k, 1, dS);
+    ARG(k, 2, cL);
+    ARG(k, 3, coh);
+    ARG(k, 4, cow);
+    ARG(k, 5, coff);
+    ARG(k, 6, dM);
+    ARG(k, 7, dT);
+    g[0] = (size_t)(out_w + 15) / 16 * 16;
+    g[1] = (size_t)(out_h + 15) / 16 * 16;
+    g[2] = n;
+    rc = launch(k, 3, g, l, "mask_post");
+    if (rc == 0) {
+        CHECK(clEnqueueReadBuffer(q, dM, CL_TRUE, 0, (size_t)n * out_h * out_w,
+                                  mask, 0, NULL, NULL),
+              "read mask");
+        CHECK(clEnqueueReadBuffer(q, dT, CL_TRUE, 0, (size_t)n * 6 * 4, stats,
+                                  0, NULL, NULL),
+              "read stats");
+    }
+    clReleaseMemObject(dL);
+    clReleaseMemObject(dS);
+    clReleaseMemObject(dM);
+    clReleaseMemObject(dT);
     clReleaseKernel(k);
     return rc;
 }

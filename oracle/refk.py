@@ -42,6 +42,9 @@ def lib():
         L.ref_window_partition.argtypes = [p, p, i, i, i, i]
         L.ref_window_unpartition_add.argtypes = [p, p, i, i, i, i]
         L.ref_mha.argtypes = [i, i, i, i, p, l, l, p, l, l, p, l, l, p]
+        L.ref_convt_scatter.argtypes = [p, p, p, p, i, i, i, i, i]
+        L.ref_mask_logits.argtypes = [p, p, p, i, i]
+        L.ref_mask_post.argtypes = [p, i, p, i, i, i, i, f, p, p]
         if L.ref_init(CO.encode()) != 0:
             raise RuntimeError("reference OpenCL init: " + L.ref_error().decode())
         _lib = L
@@ -135,3 +138,35 @@ def mha(P, Nq, Nk, dint, Q, sq, K, sk, V, sv):
                       K.ctypes.data, K.size, sk, V.ctypes.data, V.size, sv,
                       O.ctypes.data))
     return O
+
+
+def convt_scatter(G, bias, add, P, H, W, Co, act):
+    G, bias = _c(G), _c(bias)
+    add = None if add is None else _c(add)
+    out = np.zeros((P, 2 * H, 2 * W, Co), np.float32)
+    _ok(lib().ref_convt_scatter(G.ctypes.data, out.ctypes.data,
+                                bias.ctypes.data,
+                                None if add is None else add.ctypes.data, P, H,
+                                W, Co, act))
+    return out
+
+
+def mask_logits(U, hyper, P, npix):
+    U, hyper = _c(U), _c(hyper)
+    out = np.zeros((P, 3, npix), np.float32)
+    _ok(lib().ref_mask_logits(U.ctypes.data, hyper.ctypes.data,
+                              out.ctypes.data, P, npix))
+    return out
+
+
+def mask_post(lowres, sel, L, out_h, out_w, offset):
+    lowres = _c(lowres)
+    sel = np.ascontiguousarray(sel, np.int32)
+    n = len(sel)
+    mask = np.zeros((n, out_h, out_w), np.uint8)
+    stats = np.tile(np.array([0, 0, 0x7fffffff, 0x7fffffff, -1, -1], np.int32),
+                    (n, 1))
+    _ok(lib().ref_mask_post(lowres.ctypes.data, lowres.shape[0], sel.ctypes.data,
+                            n, L, out_h, out_w, offset, mask.ctypes.data,
+                            stats.ctypes.data))
+    return mask, stats

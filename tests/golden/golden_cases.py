@@ -139,6 +139,39 @@ def _attend_case(Nq, Nk, heads, hd, mode, seed, W=0):
             "mode": mode, "W": W, "inputs": inputs}
 
 
+def _convt_case(P, H, W, Co, add, act, seed):
+    """convt_scatter (sam3_kernels.cl:762-786) of a [P H W][Co 4] GEMM
+    result, with the shared add map and the activation or without."""
+    g = rng(seed)
+    inputs = [g.standard_normal((P * H * W, Co * 4)).astype(np.float32),
+              g.standard_normal(Co).astype(np.float32)]
+    if add:
+        inputs.append(g.standard_normal((2 * H, 2 * W, Co)).astype(np.float32))
+    return {"kind": "convt", "P": P, "H": H, "W": W, "Co": Co, "act": act,
+            "inputs": inputs}
+
+
+def _logits_case(P, npix, seed):
+    """mask_logits (sam3_kernels.cl:789-805): U [P npix][32], hyper [P][96]."""
+    g = rng(seed)
+    return {"kind": "logits", "P": P, "npix": npix,
+            "inputs": [g.standard_normal((P * npix, 32)).astype(np.float32),
+                       g.standard_normal((P, 96)).astype(np.float32)]}
+
+
+def _mask_post_case(L, out_h, out_w, dyadic, seed):
+    """mask_post (sam3_kernels.cl:807-883) of planes 3, 0, 4 of five L x L
+    logit planes; dyadic: logits in multiples of 1/8 with 2x / 0.5x
+    resizes, so every bilinear value is exact."""
+    g = rng(seed)
+    if dyadic:
+        low = (g.integers(-40, 41, (5, L, L)) / 8.0).astype(np.float32)
+    else:
+        low = (2 * g.standard_normal((5, L, L))).astype(np.float32)
+    return {"kind": "mask_post", "L": L, "out_h": out_h, "out_w": out_w,
+            "offset": 0.5, "inputs": [low, np.array([3, 0, 4], np.int32)]}
+
+
 CASES = {
     "gemm_t": lambda: _gemm_case(GEMM, 1, 1),
     "gemm_n": lambda: _gemm_case(GEMM, 0, 2),
@@ -167,6 +200,11 @@ CASES = {
     "attend_box_hd32": lambda: _attend_case(21, 144, 8, 32, "box", 24, W=12),
     "attend_causal_hd64": lambda: _attend_case(33, 33, 4, 64, "causal", 25),
     "attend_self_hd32": lambda: _attend_case(200, 200, 8, 32, "plain", 26),
+    "convt_plain": lambda: _convt_case(3, 4, 4, 64, False, 0, 27),
+    "convt_add_gelu": lambda: _convt_case(2, 5, 7, 32, True, 1, 28),
+    "mask_logits": lambda: _logits_case(2, 300, 29),
+    "mask_post_dyadic": lambda: _mask_post_case(24, 48, 12, True, 30),
+    "mask_post_random": lambda: _mask_post_case(24, 50, 37, False, 31),
 }
 
 
@@ -245,6 +283,16 @@ def run_reference(name, case, impl):
                                       case["nh"])}
     if k == "attend":
         return {"O": _attend(impl, case)}
+    if k == "convt":
+        add = x[2] if len(x) > 2 else None
+        return {"out": impl.convt_scatter(x[0], x[1], add, case["P"], case["H"],
+                                          case["W"], case["Co"], case["act"])}
+    if k == "logits":
+        return {"out": impl.mask_logits(x[0], x[1], case["P"], case["npix"])}
+    if k == "mask_post":
+        mask, stats = impl.mask_post(x[0], x[1], case["L"], case["out_h"],
+                                     case["out_w"], case["offset"])
+        return {"mask": mask, "stats": stats}
     raise ValueError(k)
 
 
@@ -317,3 +365,12 @@ class OracleImpl:
 
     def mha(self, P, Nq, Nk, dint, Q, sq, K, sk, V, sv):
         return self.o.mha(P, Nq, Nk, dint, Q, sq, K, sk, V, sv)
+
+    def convt_scatter(self, G, bias, add, P, H, W, Co, act):
+        return self.o.convt_scatter(G, bias, add, P, H, W, Co, act)
+
+    def mask_logits(self, U, hyper, P, npix):
+        return self.o.mask_logits(U, hyper, P, npix)
+
+    def mask_post(self, lowres, sel, L, out_h, out_w, offset):
+        return self.o.mask_post(lowres, sel, L, out_h, out_w, offset)

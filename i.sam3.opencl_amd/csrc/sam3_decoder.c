@@ -514,12 +514,7 @@ static void dec_kernels(struct sam_model *m, int P)
              1.0f, ACT_NONE);
         convt_scatter(m, d->g2, d->u2, d->up3b, d->feat_s0, P, 2 * G, 2 * G,
                       32, ACT_GELU);
-        if (hipb_failed())
-            return;
-        hipb_run_begin(m->hip);
-        err = launch_mask_logits(d->u2->ptr, d->hyper->ptr, d->lowres->ptr, P,
-                                 (int)(16 * T), m->hip->stream);
-        hipb_run_end(m->hip, err, "mask_logits", 0.0);
+        mask_logits(m, d->u2, d->hyper, d->lowres, P, (int)(16 * T));
     }
 }
 
@@ -579,6 +574,27 @@ void sam_dec_graph(struct sam_model *m, int P, int enable)
     d->graph_exec = x;
     d->graph_P = P;
     d->graph_scratch = scratch;
+}
+
+void mask_logits(struct sam_model *m, hipb_mem U, hipb_mem hyper,
+                 hipb_mem out, int P, int npix)
+{
+    struct hipb_backend *be = m->hip;
+    int err;
+
+    if (P < 1 || npix < 1 || !U || !hyper || !out ||
+        hipb_count(U) < (size_t)P * npix * 32 ||
+        hipb_count(hyper) < (size_t)P * 96 ||
+        hipb_count(out) < (size_t)P * 3 * npix || U->dtype != HIPB_F32 ||
+        hyper->dtype != HIPB_F32 || out->dtype != HIPB_F32) {
+        hipb_fatal("mask_logits: invalid shape P=%d npix=%d or operand", P,
+                   npix);
+        return;
+    }
+    hipb_run_begin(be);
+    err = launch_mask_logits(U->ptr, hyper->ptr, out->ptr, P, npix,
+                             be->stream);
+    hipb_run_end(be, err, "mask_logits", 0.0);
 }
 
 void sam_decode(struct sam_model *m, int P, const float *points, float *iou)

@@ -37,7 +37,7 @@ EXPORTS = [
     "sam_trunk_graph", "softmax_ext", "attend", "sam_dec_init",
     "sam_dec_free", "sam_dec_prepare", "sam_decode", "t2i_attention",
     "i2t_attention", "convt_scatter", "sam_postprocess", "sam_read_mask",
-    "sam_dec_graph",
+    "sam_dec_graph", "mask_logits",
 ]
 
 
@@ -223,6 +223,7 @@ def lib():
     L.sam_dec_prepare.argtypes = [MP]
     L.sam_decode.argtypes = [MP, c_int, vp, vp]
     L.sam_dec_graph.argtypes = [MP, c_int, c_int]
+    L.mask_logits.argtypes = [MP, Mem, Mem, Mem, c_int, c_int]
     L.t2i_attention.argtypes = [MP, c_int, ctypes.POINTER(SamAttnW)]
     L.i2t_attention.argtypes = [MP, c_int, c_int]
     L.convt_scatter.argtypes = [MP, Mem, Mem, Mem, Mem, c_int, c_int, c_int,
@@ -686,3 +687,7 @@ def i2t_attention(m, layer, P):
 
 def convt_scatter(m, G, out, bias, add, P, H, W, Co, act=ACT_NONE):
     _call(_lib.convt_scatter, m.ptr, G, out, bias, add, P, H, W, Co, act)
+
+
+def mask_logits(m, U, hyper, out, P, npix):
+    _call(_lib.mask_logits, m.ptr, U, hyper, out, P, npix)

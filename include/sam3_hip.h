@@ -464,6 +464,12 @@ void convt_scatter(struct sam_model *m, hipb_mem G, hipb_mem out,
                    hipb_mem bias, hipb_mem add, int P, int H, int W, int Co,
                    int act);
 
+/* Low-resolution logits out [P][3][npix] = hyper [P][3][32] .
+ * U [P][npix][32] (the mask_logits kernel, sam3_kernels.cl:789-805, as
+ * sam_decode launches it, sam3_model.c:1387-1398). */
+void mask_logits(struct sam_model *m, hipb_mem U, hipb_mem hyper,
+                 hipb_mem out, int P, int npix);
+
 /* sam_postprocess (sam3_model.c:1445-1517): optional hole filling (host)
  * of the n selected planes sel[] of d->lowres, bilinear resize to out_h x
  * out_w binary masks in d->mask and stats [n][6] = count(logit >

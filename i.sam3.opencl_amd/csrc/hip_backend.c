@@ -297,6 +297,12 @@ void hipb_free(struct hipb_backend *b)
         hipStreamSynchronize((hipStream_t)b->stream);
     if (b->scratch)
         hipFree(b->scratch);
+    for (int i = 0; i < 2; i++) {
+        if (b->stage[i])
+            hipHostFree(b->stage[i]);
+        if (b->stage_ev[i])
+            hipEventDestroy((hipEvent_t)b->stage_ev[i]);
+    }
     if (b->ev[0])
         hipEventDestroy((hipEvent_t)b->ev[0]);
     if (b->ev[1])

@@ -193,6 +193,15 @@ int launch_mask_post(const float *lowres, const int *sel, int n, int L,
                      int out_h, int out_w, float offset, unsigned char *mask,
                      int *stats, void *stream);
 
+/* Checkpoint tensor from its raw storage span src (element type sdt:
+ * enum pth_dtype, 3 = complex64) to n C-order elements of type ddt at
+ * dst (complex64 only to DT_F32, two floats per element); element i of
+ * a non-contiguous tensor is at storage element sum_d idx_d stride[d]
+ * of src. */
+int launch_pth_convert(const void *src, int sdt, void *dst, int ddt,
+                       long long n, int ndim, const long *shape,
+                       const long *stride, int contiguous, void *stream);
+
 /* Image -> token attention folded per prompt (bf16 path): k_i2t_fold
  * builds Wt16 [P][64][K] (bf16), bt [P][64] and YT16 [P][256][64] from
  * the token keys / values sk, sv [P][8][128], the image-query projection

@@ -37,7 +37,14 @@ EXPORTS = [
     "sam_trunk_graph", "softmax_ext", "attend", "sam_dec_init",
     "sam_dec_free", "sam_dec_prepare", "sam_decode", "t2i_attention",
     "i2t_attention", "convt_scatter", "sam_postprocess", "sam_read_mask",
-    "sam_dec_graph", "mask_logits",
+    "sam_dec_graph", "mask_logits", "pth_upload", "load_dev", "load_dev_w",
+    "load_dev_fmt", "load_dev_w_fmt", "load_host", "load_host_into",
+    "sam_load", "sam_free",
+]
+# include/pth_loader.h
+PTH_EXPORTS = [
+    "pth_open", "pth_find", "pth_require", "pth_numel", "pth_bytes",
+    "pth_read_f32", "pth_read_c64", "pth_read_row_f32", "pth_close",
 ]
 
 
@@ -62,7 +69,9 @@ class HipbBackend(ctypes.Structure):
                 ("bf16", ctypes.c_int), ("profile", ctypes.c_int),
                 ("stream", ctypes.c_void_p), ("ev", ctypes.c_void_p * 2),
                 ("scratch", ctypes.c_void_p),
-                ("scratch_bytes", ctypes.c_size_t)]
+                ("scratch_bytes", ctypes.c_size_t),
+                ("stage", ctypes.c_void_p * 2), ("stage_ev", ctypes.c_void_p * 2),
+                ("stage_next", ctypes.c_int)]
 
 
 class Opnd(ctypes.Structure):
@@ -91,7 +100,8 @@ class SamModel(ctypes.Structure):
                             "mlpbuf", "mlp16")] + \
         [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
          ("trunk_gen", ctypes.c_ulong), ("abias", Mem),
-         ("apart", Mem), ("dec", ctypes.c_void_p)]
+         ("apart", Mem), ("dec", ctypes.c_void_p),
+         ("owns_weights", ctypes.c_int)]
 
 
 _FP = ctypes.POINTER(ctypes.c_float)
@@ -135,6 +145,26 @@ class SamDecoder(ctypes.Structure):
                             "up_w2t", "t2i_part", "t2i_z")] + \
         [("graph", ctypes.c_void_p), ("graph_exec", ctypes.c_void_p),
          ("graph_P", ctypes.c_int), ("graph_scratch", ctypes.c_void_p)]
+
+
+# enum pth_dtype (pth_loader.h)
+PTH_F32, PTH_F16, PTH_BF16, PTH_C64 = 0, 1, 2, 3
+PTH_MAX_DIMS = 8
+
+
+class PthTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("ndim", ctypes.c_int),
+                ("shape", ctypes.c_long * PTH_MAX_DIMS),
+                ("stride", ctypes.c_long * PTH_MAX_DIMS),
+                ("storage_offset", ctypes.c_long), ("dtype", ctypes.c_int),
+                ("data_offset", ctypes.c_long),
+                ("storage_bytes", ctypes.c_size_t)]
+
+
+class PthFile(ctypes.Structure):
+    _fields_ = [("map", ctypes.c_void_p), ("map_bytes", ctypes.c_size_t),
+                ("path", ctypes.c_char_p), ("ntensors", ctypes.c_int),
+                ("tensors", ctypes.POINTER(PthTensor))]
 
 
 _lib = None
@@ -232,6 +262,34 @@ def lib():
                                   vp]
     L.sam_read_mask.argtypes = [MP, c_int, c_int, c_int, c_int, c_int, c_int,
                                 c_int, vp]
+    FP = ctypes.POINTER(PthFile)
+    TP = ctypes.POINTER(PthTensor)
+    LP = ctypes.POINTER(c_long)
+    L.pth_open.argtypes = [FP, cp]
+    L.pth_find.argtypes = [FP, cp]
+    L.pth_find.restype = TP
+    L.pth_require.argtypes = [FP, cp, c_int, LP]
+    L.pth_require.restype = TP
+    L.pth_numel.argtypes = [TP]
+    L.pth_numel.restype = c_long
+    L.pth_bytes.argtypes = [FP, cp]
+    L.pth_bytes.restype = ctypes.c_double
+    L.pth_read_f32.argtypes = [FP, TP]
+    L.pth_read_f32.restype = vp
+    L.pth_read_c64.argtypes = [FP, TP]
+    L.pth_read_c64.restype = vp
+    L.pth_read_row_f32.argtypes = [FP, TP, c_long, vp]
+    L.pth_close.argtypes = [FP]
+    L.pth_upload.argtypes = [BP, FP, TP, c_int, cp]
+    L.pth_upload.restype = Mem
+    for n in ("load_dev", "load_dev_w"):
+        getattr(L, n).argtypes = [MP, FP, cp, c_int, LP]
+        getattr(L, n).restype = Mem
+    L.load_host.argtypes = [FP, cp, c_int, LP]
+    L.load_host.restype = vp
+    L.load_host_into.argtypes = [FP, cp, c_int, LP, vp]
+    L.sam_load.argtypes = [MP, BP, FP, c_int, c_int]
+    L.sam_free.argtypes = [MP]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
     return L
@@ -388,8 +446,126 @@ class Model:
     def ptr(self):
         return ctypes.byref(self.m)
 
+    @classmethod
+    def load(cls, backend, ckpt, batch=1, point_head=False):
+        """sam_load: the trunk (and with point_head the decoder, for batch
+        prompts) of the open Checkpoint ckpt, owned by the model."""
+        self = cls.__new__(cls)
+        self.backend = backend
+        self.m = SamModel()
+        self._blocks = None
+        _lib.sam_load(ctypes.byref(self.m), backend.ptr, ckpt.ptr, batch,
+                      int(bool(point_head)))
+        msg = _lib.hipb_last_error()
+        if msg:
+            _lib.hipb_clear_error()
+            _lib.sam_free(self.ptr)
+            raise Sam3HipError(msg.decode())
+        return self
+
+    @property
+    def blocks(self):
+        return [self.m.blocks[i] for i in range(self.m.depth)]
+
+    def decoder(self):
+        """The decoder sam_load attached (a Decoder view owned by the
+        model: sam_free releases it)."""
+        if not self.m.dec:
+            raise Sam3HipError("model has no decoder")
+        return Decoder.attached(self)
+
     def free(self):
-        _lib.sam_path_free(self.ptr)
+        _lib.sam_free(self.ptr)
+
+
+_libc = ctypes.CDLL(None)
+_libc.free.argtypes = [ctypes.c_void_p]
+
+
+class Checkpoint:
+    """An open PyTorch checkpoint (pth_open / pth_close of pth_loader.h)."""
+
+    def __init__(self, path):
+        lib()
+        self.f = PthFile()
+        _lib.pth_open(ctypes.byref(self.f), os.fsencode(path))
+        _check()
+
+    @property
+    def ptr(self):
+        return ctypes.byref(self.f)
+
+    def names(self):
+        return [self.f.tensors[i].name.decode()
+                for i in range(self.f.ntensors)]
+
+    def find(self, name):
+        """pth_find: the tensor record (PthTensor) or None."""
+        t = _lib.pth_find(self.ptr, name.encode())
+        return t.contents if t else None
+
+    def require(self, name, ndim, shape=None):
+        arr = None if shape is None else (ctypes.c_long * ndim)(*shape)
+        t = _lib.pth_require(self.ptr, name.encode(), ndim, arr)
+        _check()
+        return t.contents
+
+    @staticmethod
+    def shape(t):
+        return tuple(t.shape[d] for d in range(t.ndim))
+
+    def numel(self, t):
+        return _lib.pth_numel(ctypes.byref(t))
+
+    def bytes(self, prefix):
+        return _lib.pth_bytes(self.ptr, prefix.encode())
+
+    def _get(self, name):
+        t = self.find(name)
+        if t is None:
+            raise Sam3HipError("Tensor <%s> not found in checkpoint <%s>" %
+                               (name, self.f.path.decode()))
+        return t
+
+    @staticmethod
+    def _take(p, count):
+        """count floats of a malloc'd array, which is then freed."""
+        _check()
+        a = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)),
+                                  (count,)).copy()
+        _libc.free(p)
+        return a
+
+    def read_f32(self, name):
+        """pth_read_f32: the tensor as float32, C order."""
+        t = self._get(name)
+        p = _lib.pth_read_f32(self.ptr, ctypes.byref(t))
+        return self._take(p, self.numel(t)).reshape(self.shape(t))
+
+    def read_c64(self, name):
+        """pth_read_c64: the tensor as complex64, C order."""
+        t = self._get(name)
+        p = _lib.pth_read_c64(self.ptr, ctypes.byref(t))
+        a = self._take(p, 2 * self.numel(t))
+        return a.view(np.complex64).reshape(self.shape(t))
+
+    def read_row_f32(self, name, r):
+        t = self._get(name)
+        out = np.zeros(t.shape[1] if t.ndim == 2 else 0, np.float32)
+        _lib.pth_read_row_f32(self.ptr, ctypes.byref(t), r, out.ctypes.data)
+        _check()
+        return out
+
+    def upload(self, backend, name, dtype=F32):
+        """pth_upload of tensor name into a new device buffer."""
+        t = self._get(name)
+        m = _lib.pth_upload(backend.ptr, self.ptr, ctypes.byref(t), dtype,
+                            name.encode())
+        _check()
+        return m
+
+    def close(self):
+        _lib.pth_close(self.ptr)
 
 
 def mat(buf, off, ld):
@@ -617,6 +793,18 @@ class Decoder:
         self.grid = model.m.grid
         self.batch = batch
 
+    @classmethod
+    def attached(cls, model):
+        """A view of the decoder sam_load attached to model."""
+        self = cls.__new__(cls)
+        self.model, self.be = model, model.backend
+        self.d = ctypes.cast(model.m.dec, ctypes.POINTER(SamDecoder)).contents
+        self._mems = []
+        self._owned = False
+        self.grid = model.m.grid
+        self.batch = self.d.batch
+        return self
+
     @property
     def T(self):
         return self.grid * self.grid
@@ -667,6 +855,8 @@ class Decoder:
         return out
 
     def free(self):
+        if not getattr(self, "_owned", True):
+            return  # the model's sam_free releases it
         _lib.sam_dec_free(self.model.ptr)
         for mem in self._mems + [getattr(self.d, n) for n in ("emb", "feat_s0",
                                                              "feat_s1")]:

@@ -83,6 +83,11 @@ struct hipb_backend {
     void *ev[2];  /* hipEvent_t pair of the region timer */
     void *scratch;          /* backend-owned device scratch (split-K partials) */
     size_t scratch_bytes;
+    /* Pinned host staging of checkpoint uploads (pth_upload): two
+     * buffers and the events that mark the end of their last copy. */
+    void *stage[2];
+    void *stage_ev[2];
+    int stage_next;
 };
 
 /* Select a device and create its stream (ocl_init, ocl_backend.h:57-59).
@@ -211,6 +216,9 @@ struct sam_model {
     hipb_mem apart;
     /* The point-prompt mask decoder (sam_dec_init), or NULL. */
     struct sam_decoder *dec;
+    /* Set by sam_load: the blocks array, the weights, the rope tables and
+     * the decoder are the model's own, and sam_free releases them. */
+    int owns_weights;
 };
 
 /* Set up m for the attention path (mlp = 0) or the whole trunk (mlp =
@@ -480,6 +488,53 @@ void sam_postprocess(struct sam_model *m, int n, const int *sel, int out_h,
  * (sam3_model.c:1519-1530). */
 void sam_read_mask(struct sam_model *m, int k, int out_h, int out_w, int x0,
                    int y0, int x1, int y1, unsigned char *dst);
+
+/* ------------------------------------------------------------------ */
+/* Checkpoint weights (pth_loader.h files into device memory)          */
+/* ------------------------------------------------------------------ */
+
+struct pth_file;
+struct pth_tensor;
+
+/* Tensor t of an open checkpoint as a new device buffer of the given
+ * HIPB_* type, C order: the storage span it covers is copied through
+ * pinned staging and converted / gathered on the device (float32, half
+ * and bfloat16 storage to any of the three, rounding to nearest even;
+ * complex64 only to HIPB_F32 as (real, imaginary) pairs). No counterpart:
+ * the reference reads to host floats and uploads (sam3_model.c:52-76). */
+hipb_mem pth_upload(struct hipb_backend *b, const struct pth_file *pf,
+                    const struct pth_tensor *t, int dtype, const char *what);
+
+/* The reference's load helpers (sam3_ops.h:26-38): pth_require then a
+ * float32 device buffer (load_dev) or a weight matrix in the backend's
+ * weight type (load_dev_w: half with precision=fp16, bf16 with
+ * precision=bf16, else float32); the _fmt forms format the name;
+ * load_host returns malloc'd host floats, load_host_into copies them. */
+hipb_mem load_dev(struct sam_model *m, const struct pth_file *pf,
+                  const char *name, int ndim, const long *shape);
+hipb_mem load_dev_w(struct sam_model *m, const struct pth_file *pf,
+                    const char *name, int ndim, const long *shape);
+hipb_mem load_dev_fmt(struct sam_model *m, const struct pth_file *pf,
+                      int ndim, const long *shape, const char *fmt, ...);
+hipb_mem load_dev_w_fmt(struct sam_model *m, const struct pth_file *pf,
+                        int ndim, const long *shape, const char *fmt, ...);
+float *load_host(const struct pth_file *pf, const char *name, int ndim,
+                 const long *shape);
+void load_host_into(const struct pth_file *pf, const char *name, int ndim,
+                    const long *shape, float *dst);
+
+/* sam_load (sam3_model.c:918-962) without the necks: the image encoder
+ * trunk of a SAM 3 checkpoint (sizes, depth, window and grid from its
+ * tensors, sam3_model.c:473-583; the grid is the global blocks' rope
+ * extent) with its work buffers, and with point_head the point-prompt
+ * decoder's weights (sam3_model.c:657-758) and sam_dec_init(m, d, batch).
+ * The image features of the decoder (emb, feat_s0, feat_s1) stay the
+ * caller's to provide. */
+void sam_load(struct sam_model *m, struct hipb_backend *b,
+              const struct pth_file *pf, int batch, int point_head);
+/* Release a model (sam3_model.c:1532): with owns_weights (sam_load) its
+ * weights, rope tables, blocks and decoder too; else sam_path_free. */
+void sam_free(struct sam_model *m);
 
 #ifdef __cplusplus
 }

@@ -12,8 +12,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "sam3_hip.h")
 
 
-def declared_functions():
-    src = open(HEADER).read()
+PTH_HEADER = os.path.join(ROOT, "include", "pth_loader.h")
+
+
+def declared_functions(header=HEADER):
+    src = open(header).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{]*\)\s*;", src)
     return sorted(set(n for n in names if n not in ("if", "sizeof")))
@@ -33,6 +36,19 @@ def test_every_declared_symbol_is_exported(hip):
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
     assert sorted(hip.EXPORTS) == names
+
+
+def test_checkpoint_reader_symbols_are_exported(hip):
+    names = declared_functions(PTH_HEADER)
+    lib = ctypes.CDLL(hip.LIB_PATH)
+    assert not [n for n in names if not hasattr(lib, n)]
+    assert sorted(hip.PTH_EXPORTS) == names
+    src = re.sub(r"/\*.*?\*/", "", open(PTH_HEADER).read(), flags=re.S)
+    for cls, cname in ((hip.PthTensor, "pth_tensor"), (hip.PthFile, "pth_file")):
+        body = re.search(r"struct %s \{(.*?)\};" % cname, src, re.S).group(1)
+        fields = re.findall(r"([A-Za-z_][A-Za-z0-9_]*)\s*(?:\[[^\]]*\])*\s*;",
+                            body)
+        assert [f[0] for f in cls._fields_] == fields, cname
 
 
 def test_struct_layouts_match_header(hip):

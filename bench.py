@@ -432,6 +432,126 @@ def mask_decoder_cpu(P=2, grid=72):
                                       % P}
 
 
+def checkpoint_load(hip, precisions=("bf16", "fp32"), depth=8, reps=3):
+    """Checkpoint weights into HBM. A SAM 3-named float32 checkpoint of
+    the trunk's first `depth` blocks at their real shapes (E 1024, MLP
+    4736, 16 heads; blocks 0-6 windowed 24 x 24, block 7 global 72 x 72
+    with their complex64 rope tables; patch embedding, 24 x 24 + 1
+    position embedding, ln_pre) and the point decoder, random values,
+    written by torch.save to a temporary file that is read once before
+    timing (page cache warm: memory -> HBM, not disk). Per precision:
+    - upload: every tensor of the file by pth_upload into the element
+      type the model keeps (weight matrices bf16 / f32, the rest f32),
+      GB/s of file storage bytes;
+    - reference_path: the reference's sequence for the same tensors
+      (pth_read_f32 to host floats, host rounding of weight matrices,
+      upload; sam3_model.c:52-76);
+    - sam_load: the whole sam_load (weights, tiled position embedding,
+      work buffers, decoder set-up for 64 prompts), ms."""
+    import ctypes
+    import tempfile
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import pth_case as pc
+
+    g = np.random.default_rng(41)
+    E, M = 1024, 4736
+
+    def rnd(*shape):
+        return (0.02 * g.standard_normal(shape, dtype=np.float32))
+
+    win = [24] * (depth - 1) + [0]
+    blocks = [{"n1w": rnd(E), "n1b": rnd(E), "qkvw": rnd(3 * E, E),
+               "qkvb": rnd(3 * E), "projw": rnd(E, E), "projb": rnd(E),
+               "n2w": rnd(E), "n2b": rnd(E), "l1w": rnd(M, E), "l1b": rnd(M),
+               "l2w": rnd(E, M), "l2b": rnd(E), "window": w} for w in win]
+    ropes = [rope_table(w if w else 72) for w in win]
+    tw = dict(E=E, patch=14, pe_w=rnd(E, 3 * 14 * 14),
+              pos_embed=rnd(1, 577, E), lnpw=rnd(E), lnpb=rnd(E),
+              blocks=blocks, ropes=ropes)
+    sd = pc.sam3_names(tw, hip.random_decoder_weights(41))
+    tmp = tempfile.mkdtemp(prefix="sam3ck_")
+    path = os.path.join(tmp, "sam3_part.pt")
+    pc.save_torch(path, sd)
+    with open(path, "rb") as f:
+        while f.read(1 << 26):
+            pass
+    nbytes = os.path.getsize(path)
+    mats = {k for k, a in sd.items() if a.ndim >= 2 and "freqs" not in k and
+            "pos_embed" not in k and "prompt_encoder" not in k and
+            "_token" not in k and "tokens" not in k}
+    out = {"workload": "SAM 3 checkpoint, trunk blocks 0-%d + point decoder, "
+                       "float32 storage, %d tensors, %.0f MB" %
+                       (depth - 1, len(sd), nbytes / 1e6)}
+    ck = hip.Checkpoint(path)
+    L = hip.lib()
+    store = ck.bytes("")
+    try:
+        for p in precisions:
+            be = hip.Backend(precision=p)
+            wdt = hip.BF16 if p == "bf16" else hip.F32
+
+            def upload():
+                mems = []
+                for k in sd:
+                    dt = wdt if k in mats else hip.F32
+                    mems.append(ck.upload(be, k, dt))
+                be.finish()
+                return mems
+
+            def reference_path():
+                mems = []
+                for k in sd:
+                    t = ck.find(k)
+                    if t.dtype == hip.PTH_C64:
+                        ptr = L.pth_read_c64(ck.ptr, ctypes.byref(t))
+                        n = 2 * ck.numel(t)
+                    else:
+                        ptr = L.pth_read_f32(ck.ptr, ctypes.byref(t))
+                        n = ck.numel(t)
+                    if k in mats:
+                        m = L.hipb_upload_weight(be.ptr, ptr, n, k.encode())
+                    else:
+                        m = L.hipb_upload(be.ptr, ptr, 4 * n, k.encode())
+                    hip._libc.free(ptr)
+                    mems.append(m)
+                be.finish()
+                return mems
+
+            res = {}
+            for name, fn in (("upload", upload),
+                             ("reference_path", reference_path)):
+                best = None
+                for _ in range(reps):
+                    t0 = time.perf_counter()
+                    mems = fn()
+                    dt_s = time.perf_counter() - t0
+                    for mm in mems:
+                        be.release(mm)
+                    best = dt_s if best is None else min(best, dt_s)
+                res[name] = {"ms": round(1e3 * best, 1),
+                             "GB/s": round(store / best / 1e9, 2)}
+            best = None
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                m = hip.Model.load(be, ck, batch=64, point_head=True)
+                be.finish()
+                dt_s = time.perf_counter() - t0
+                m.free()
+                best = dt_s if best is None else min(best, dt_s)
+            res["sam_load_ms"] = round(1e3 * best, 1)
+            res["speedup_vs_reference_path"] = round(
+                res["reference_path"]["ms"] / res["upload"]["ms"], 2)
+            out[p] = res
+            be.free()
+    finally:
+        ck.close()
+        os.remove(path)
+        os.rmdir(tmp)
+    out["storage_bytes"] = int(store)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -450,6 +570,8 @@ def main():
                     help="only the image encoder trunk (profiling)")
     ap.add_argument("--text-only", action="store_true",
                     help="only the text path's attend() shapes (profiling)")
+    ap.add_argument("--checkpoint-only", action="store_true",
+                    help="only the checkpoint upload timings")
     ap.add_argument("--precision", choices=("bf16", "fp32"),
                     help="with --backbone-only: that path alone")
     args = ap.parse_args()
@@ -469,6 +591,10 @@ def main():
         prec = (args.precision,) if args.precision else ("bf16", "fp32")
         print(json.dumps({"mask_decoder": mask_decoder(
             hip, args.steps, min(args.warmup, 5), prec)}))
+        return
+    if args.checkpoint_only:
+        prec = (args.precision,) if args.precision else ("bf16", "fp32")
+        print(json.dumps({"checkpoint": checkpoint_load(hip, prec)}))
         return
     if args.text_only:
         print(json.dumps({"text_attention": text_attention(

@@ -69,7 +69,7 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([os.path.join(ROCM, "bin", "hipcc"), "--offload-arch=gfx950",
           "-shared", "-fPIC", "-o", tmp] + objs +
-         ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64",
+         ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lpthread",
           "-Wl,-rpath," + os.path.join(ROCM, "lib")])
     os.replace(tmp, LIB)
     return LIB

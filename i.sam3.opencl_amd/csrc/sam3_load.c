@@ -25,6 +25,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <math.h>
+#include <pthread.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -33,7 +34,10 @@
 #include <sys/mman.h>
 #include <unistd.h>
 
-#define STAGE_BYTES ((size_t)16 << 20)
+#define STAGE_BYTES ((size_t)32 << 20)
+/* Host threads of one staging copy, and the least bytes per thread. */
+#define COPY_THREADS 8
+#define COPY_MIN ((size_t)2 << 20)
 
 #define TRUNK "detector.backbone.vision_backbone.trunk"
 #define DEC "tracker.sam_mask_decoder"
@@ -63,6 +67,51 @@ static int stage_ready(struct hipb_backend *b)
     return 1;
 }
 
+struct part {
+    void *dst;
+    const void *src;
+    size_t n;
+};
+
+static void *copy_part(void *arg)
+{
+    const struct part *p = arg;
+
+    memcpy(p->dst, p->src, p->n);
+    return NULL;
+}
+
+/* memcpy split over up to COPY_THREADS threads: one core's copy from the
+ * page cache into pinned memory runs far below the DMA rate. */
+static void copy_wide(void *dst, const void *src, size_t n)
+{
+    struct part parts[COPY_THREADS];
+    pthread_t th[COPY_THREADS];
+    int started[COPY_THREADS] = {0};
+    size_t per, off = 0;
+    int k, nt = (int)(n / COPY_MIN);
+
+    nt = nt < 1 ? 1 : nt > COPY_THREADS ? COPY_THREADS : nt;
+    per = (n / (size_t)nt + 4095) & ~(size_t)4095;
+    for (k = 0; k < nt; k++) {
+        const size_t len = off >= n ? 0 : n - off < per ? n - off : per;
+
+        parts[k].dst = (char *)dst + off;
+        parts[k].src = (const char *)src + off;
+        parts[k].n = len;
+        off += len;
+        if (k > 0 && len)
+            started[k] = !pthread_create(&th[k], NULL, copy_part, &parts[k]);
+    }
+    copy_part(&parts[0]);
+    for (k = 1; k < nt; k++) {
+        if (started[k])
+            pthread_join(th[k], NULL);
+        else if (parts[k].n)
+            copy_part(&parts[k]);
+    }
+}
+
 /* n bytes of host memory to device address dst on the backend stream,
  * through the staging buffers in turn. */
 static void h2d(struct hipb_backend *b, char *dst, const unsigned char *src,
@@ -81,7 +130,7 @@ static void h2d(struct hipb_backend *b, char *dst, const unsigned char *src,
         b->stage_next ^= 1;
         hipb_check(hipEventSynchronize((hipEvent_t)b->stage_ev[k]),
                    "hipEventSynchronize (checkpoint staging)");
-        memcpy(b->stage[k], src + off, len);
+        copy_wide(b->stage[k], src + off, len);
         hipb_check(hipMemcpyAsync(dst + off, b->stage[k], len,
                                   hipMemcpyHostToDevice,
                                   (hipStream_t)b->stream),

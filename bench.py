@@ -655,6 +655,7 @@ def main():
         mdec["cpu_oracle"] = mask_decoder_cpu()
     bb = backbone(hip, 5, 2)
     text = text_attention(hip, sub_steps, sub_warm)
+    ckpt = checkpoint_load(hip)
 
     qkv_flops = 2.0 * 5184 * 1024 * 3072
     result = {
@@ -697,6 +698,7 @@ def main():
         "mask_decoder": mdec,
         "backbone": bb,
         "text_attention": text,
+        "checkpoint": ckpt,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": PEAK_BF16, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16, 4),

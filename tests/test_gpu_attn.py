@@ -89,6 +89,30 @@ def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
     assert report("ragged N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
 
 
+def test_many_units(hip, be, orc):
+    """80 units of 1024 tokens (5 images x 16 heads, RoPE): 640 query
+    tiles, more workgroups than one per CU on a 256-CU device, every row
+    against the oracle."""
+    N, H, E, imgs = 1024, 16, 1024, 5
+    m = hip.Model(be, embed=E, heads=H)
+    table = orc.rope_table(32)
+    qkv = np.random.default_rng(77).standard_normal((imgs * N, 3 * E), np.float32)
+    dq, dt = be.upload(qkv), be.upload(table)
+    do = be.alloc(imgs * N * E * 4)
+    st = N * 3 * E
+    print("many units N=%d units=%d %s" % (N, imgs * H, be.precision), flush=True)
+    hip.attn_fused(m, N, imgs * H, H, hip.bmat(dq, 0, 3 * E, st, 64),
+                   hip.bmat(dq, E, 3 * E, st, 64),
+                   hip.bmat(dq, 2 * E, 3 * E, st, 64),
+                   hip.bmat(do, 0, E, N * E, 64), dt, N, 0.125)
+    got = be.read(do).reshape(imgs * N, E)
+    want = _oracle_units(orc, qkv, N, imgs, H, E, table)
+    assert report("many units %s" % be.precision, got, want) <= TOL[be.precision]
+    be.release(dq)
+    be.release(dt)
+    be.release(do)
+
+
 @pytest.mark.parametrize("ooff,ldo", [(1, 131), (4, 132), (8, 136)])
 def test_output_offsets(hip, be, orc, ooff, ldo):
     """Output rows at an offset and stride that break 16-byte alignment

@@ -435,11 +435,17 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
      * traffic per product) only for long reductions that still give
      * (nearly) every CU a tile. Measured at M = 5184: K = 1024 runs at
      * 646 vs 691 TFLOP/s (N = 3072) and 460 vs 585 (N = 4096), K = 4096
-     * at 1145 vs 1070 (N = 3072). */
+     * at 1145 vs 1070 (N = 3072). 128 x 64 tiles (4 waves of 64 x 32)
+     * where 128 x 128 tiles would give fewer than two per CU: at M = 5184,
+     * N = 1024 they run 518 vs 408 TFLOP/s (K = 1024) and 810 vs 732
+     * (K = 4096); everywhere else they are slower. */
     t256 = (long)((d->M + 255) / 256) * ((d->N + 255) / 256);
     /* The packed-operand store exists for 128 x 128 tiles only. */
     bm = t256 >= cu_count() * 9 / 10 && d->K >= 2048 && d->pack_N == 0 ? 256 : 128;
     bn = bm;
+    if (bm == 128 && d->pack_N == 0 &&
+        (long)((d->M + 127) / 128) * ((d->N + 127) / 128) < 2L * cu_count())
+        bn = 64;
     {
         const long tiles = (long)((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn);
         const long grid = (tiles + NT_NXCD - 1) / NT_NXCD * NT_NXCD;
@@ -449,6 +455,9 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
         if (bm == 256)
             hipLaunchKernelGGL((k_gemm_nt<256, 256, 128, 64>),
                                dim3((unsigned)grid), dim3(512), 0, s, *d);
+        else if (bn == 64)
+            hipLaunchKernelGGL((k_gemm_nt<128, 64, 64, 32>),
+                               dim3((unsigned)grid), dim3(256), 0, s, *d);
         else
             hipLaunchKernelGGL((k_gemm_nt<128, 128, 64, 64>),
                                dim3((unsigned)grid), dim3(256), 0, s, *d);

@@ -161,6 +161,29 @@ __device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0
     }
 }
 
+/* Epilogue activation of the bf16 products: GELU with erf from
+ * Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7, far below the bf16
+ * rounding of fc1's stored output), whose short straight-line code leaves
+ * the K loop more registers than the library erff. */
+__device__ __forceinline__ float nt_act(float v, int act)
+{
+    if (act == ACT_GELU_K) {
+        const float z = fabsf(v) * 0.70710678118654752f;
+        const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+        float poly = fmaf(1.061405429f, t, -1.453152027f);
+
+        poly = fmaf(poly, t, 1.421413741f);
+        poly = fmaf(poly, t, -0.284496736f);
+        poly = fmaf(poly, t, 0.254829592f);
+        poly *= t;
+        const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
+        const float erf_abs = fmaf(-poly, e, 1.0f);
+
+        return 0.5f * v * (1.0f + copysignf(erf_abs, v));
+    }
+    return act == ACT_RELU_K ? fmaxf(v, 0.0f) : v;
+}
+
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt(gemm_desc d)
@@ -314,7 +337,7 @@ k_gemm_nt(gemm_desc d)
 #pragma clang loop unroll(full)
                 for (int r = 0; r < 16; r++)
                     E[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * LD + col] =
-                        act_k(d.alpha * cv[r] + bn, d.act);
+                        nt_act(d.alpha * cv[r] + bn, d.act);
             }
         }
         __syncthreads();

@@ -603,6 +603,13 @@ static void release_decoder(struct sam_decoder *d)
 
 /* ------------------------------------------------- sam_load / sam_free */
 
+int sam_is_sam3(const struct pth_file *pf)
+{
+    return pth_find(pf, TRUNK ".pos_embed") &&
+           pth_find(pf, DEC ".iou_token.weight") &&
+           pth_find(pf, "detector.backbone.vision_backbone.sam2_convs.0.conv_1x1.weight");
+}
+
 void sam_load(struct sam_model *m, struct hipb_backend *b,
               const struct pth_file *pf, int batch, int point_head)
 {

@@ -39,7 +39,7 @@ EXPORTS = [
     "i2t_attention", "convt_scatter", "sam_postprocess", "sam_read_mask",
     "sam_dec_graph", "mask_logits", "pth_upload", "load_dev", "load_dev_w",
     "load_dev_fmt", "load_dev_w_fmt", "load_host", "load_host_into",
-    "sam_load", "sam_free",
+    "sam_load", "sam_free", "sam_is_sam3",
 ]
 # include/pth_loader.h
 PTH_EXPORTS = [
@@ -290,6 +290,7 @@ def lib():
     L.load_host_into.argtypes = [FP, cp, c_int, LP, vp]
     L.sam_load.argtypes = [MP, BP, FP, c_int, c_int]
     L.sam_free.argtypes = [MP]
+    L.sam_is_sam3.argtypes = [FP]
     L.hipb_set_error_mode(ERR_RECORD)
     _lib = L
     return L
@@ -555,6 +556,10 @@ class Checkpoint:
         _lib.pth_read_row_f32(self.ptr, ctypes.byref(t), r, out.ctypes.data)
         _check()
         return out
+
+    def is_sam3(self):
+        """sam_is_sam3: the SAM 3 trunk, mask decoder and point neck."""
+        return bool(_lib.sam_is_sam3(self.ptr))
 
     def upload(self, backend, name, dtype=F32):
         """pth_upload of tensor name into a new device buffer."""

@@ -523,6 +523,11 @@ float *load_host(const struct pth_file *pf, const char *name, int ndim,
 void load_host_into(const struct pth_file *pf, const char *name, int ndim,
                     const long *shape, float *dst);
 
+/* Non-zero if pf holds the SAM 3 trunk, the tracker's mask decoder and
+ * the point-prompt neck (sam_is_sam3, sam3_model.c:41-46; main.c:537-550
+ * refuses other checkpoints with it). */
+int sam_is_sam3(const struct pth_file *pf);
+
 /* sam_load (sam3_model.c:918-962) without the necks: the image encoder
  * trunk of a SAM 3 checkpoint (sizes, depth, window and grid from its
  * tensors, sam3_model.c:473-583; the grid is the global blocks' rope

@@ -183,6 +183,29 @@ def test_reference_fixture_form(hip, tmp_path):
         ck.close()
 
 
+def test_sam3_detection(hip, tmp_path):
+    """sam_is_sam3 (sam3_model.c:41-46) on the reference test's kinds of
+    fixture: a SAM 3 checkpoint, SAM 1 and SAM 2 checkpoints (which
+    main.c:537-550 refuses by their own markers), and a SAM 3 file
+    without the point-prompt neck."""
+    sam3 = {pc.TRUNK + ".pos_embed": (1, 5, 8),
+            pc.DEC + ".iou_token.weight": (1, 256),
+            "detector.backbone.vision_backbone.sam2_convs.0.conv_1x1.weight":
+                (256, 8, 1, 1)}
+    cases = {"sam3": (sam3, True),
+             "sam1": ({"image_encoder.pos_embed": (1, 4, 4, 8)}, False),
+             "sam2": ({"image_encoder.trunk.pos_embed": (1, 8, 7, 7)}, False),
+             "noneck": (dict(list(sam3.items())[:2]), False)}
+    for name, (shapes, want) in cases.items():
+        path = str(tmp_path / (name + ".pt"))
+        pc.zeros_checkpoint(path, shapes)
+        ck = hip.Checkpoint(path)
+        try:
+            assert ck.is_sam3() == want, name
+        finally:
+            ck.close()
+
+
 def test_assembled_strided_tensor(hip, tmp_path):
     """A hand-assembled view (offset 3, strides (1, 4)) of one storage
     shared by two tensors, under a folder with another name."""

@@ -403,7 +403,9 @@ static struct val *tuple_from(struct vm *m, long h)
 
 static void memo_set(struct vm *m, uint64_t idx, struct val *v)
 {
-    if (idx > (uint64_t)1 << 30)
+    /* torch.save memoizes a few values per tensor; 2^24 slots (128 MiB of
+     * pointers) bound what a corrupt index can make this allocate. */
+    if (idx >= (uint64_t)1 << 24)
         die(m->c, "Invalid pickle memo index in <%s>", m->c->path);
     if ((long)idx >= m->memocap) {
         long old = m->memocap;

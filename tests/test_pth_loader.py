@@ -384,6 +384,7 @@ def test_structural_errors(hip, tmp_path):
         ("nomark", b"\x80\x02}" + pc.p_str("a") + pc.p_int(1) + b"u.", {},
          "Pickle mark not found"),
         ("memo", b"\x80\x02h\x05.", {}, "Invalid pickle memo reference 5"),
+        ("memoidx", b"\x80\x02}r\xff\xff\xff\x7f.", {}, "Invalid pickle memo index"),
         ("persid", b"\x80\x02}(" + pc.p_str("a") + pc.p_str("x") + b"Qu.", {},
          "Unsupported persistent id in checkpoint"),
     ]

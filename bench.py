@@ -576,9 +576,10 @@ def main():
                     help="with --backbone-only: that path alone")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU; the attention path "
-              "shards by image/crop with no exchange, see DESIGN.md. "
-              "Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the attention path shards by image "
+              "or crop (data parallel, no exchange between GPUs), so a "
+              "multi-GPU figure is N independent copies of this one. Run "
+              "with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     hip = load_hip()

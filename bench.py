@@ -570,6 +570,8 @@ def main():
                     help="only the image encoder trunk (profiling)")
     ap.add_argument("--text-only", action="store_true",
                     help="only the text path's attend() shapes (profiling)")
+    ap.add_argument("--window-only", action="store_true",
+                    help="only the windowed bf16 attention kernel (profiling)")
     ap.add_argument("--checkpoint-only", action="store_true",
                     help="only the checkpoint upload timings")
     ap.add_argument("--precision", choices=("bf16", "fp32"),
@@ -607,6 +609,14 @@ def main():
                                                   args.warmup)}))
         return
     be = hip.Backend(precision="bf16")
+    if args.window_only:
+        win = Block(hip, be, 24, seed=2)
+        win.region()
+        be.finish()
+        ms = timed(be, win.attn, args.steps, args.warmup)
+        print(json.dumps({"kernel": "attn_bf16 windowed 9x576", "ms": ms,
+                          "TFLOP/s": win.flops() / ms / 1e9}))
+        return
     glob = Block(hip, be, 0, seed=3)
     glob.region()          # LN -> QKV -> pack -> attention; packs operands
     be.finish()

@@ -486,10 +486,12 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * score could leave [m - SAFE_SPAN, m + SAFE_SPAN]. |q . k| <= |q| |k|,
  * and the packing kernel records each block's largest |k|, so a wave
  * first checks the bound |q| max|k| - m <= SAFE_SPAN for all its lanes
- * (three VALU operations); only blocks it cannot clear, and the first
- * block (which also guards against a row whose scores all lie far below
- * 0), take the exact block max with its cross-lane exchange. While every
- * m of the wave is 0 the scores feed exp2 directly. */
+ * (three VALU operations); only blocks it cannot clear take the exact
+ * block max with its cross-lane exchange. In the first block (m = 0) the
+ * bound also keeps every score >= -SAFE_SPAN, so a row cannot start with
+ * all its weights underflowed; where the first block takes the exact max,
+ * m may also move down to a row's maximum far below 0. While every m of
+ * the wave is 0 the scores feed exp2 directly. */
 template <bool EXT>
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
@@ -613,7 +615,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         f32x16 s0, s1;
         /* Can this block's scores exceed m + SAFE_SPAN for some lane? */
         const bool check =
-            __ballot(fresh || brow || qn * kn_next - st.m > SAFE_SPAN) != 0;
+            __ballot(brow || qn * kn_next - st.m > SAFE_SPAN) != 0;
 
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -699,8 +701,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 st.m += mx;
                 shifted = true;
             }
-            fresh = false;
         }
+        fresh = false;
         for (int r = 0; r < 16; r++) {
             s0[r] = __builtin_amdgcn_exp2f(s0[r]);
             s1[r] = __builtin_amdgcn_exp2f(s1[r]);

@@ -7,8 +7,9 @@ against models built from the same weights by host uploads.
   .half() and .bfloat16() of the tensor bit for bit (round to nearest
   even, overflow to infinity, subnormals; NaN-free inputs), and complex64
   rope tables arrive as their (real, imaginary) float pairs;
-- sam_load of a SAM 3-named checkpoint holds exactly the buffers the
-  host-built model holds (patch embedding, tiled position embedding,
+- sam_load of a SAM 3-named checkpoint (on the fp32, bf16 and fp16
+  backends: weight matrices float, bfloat16 or half) holds exactly the
+  buffers the host-built model holds (patch embedding, tiled position embedding,
   ln_pre, every block's weights, both rope tables, the decoder's weights
   and prompt tables), and the trunk and the decoder then give identical
   results, bit for bit.
@@ -28,7 +29,7 @@ def hip():
     return sam3_hip
 
 
-@pytest.fixture(scope="module", params=["fp32", "bf16"])
+@pytest.fixture(scope="module", params=["fp32", "bf16", "fp16"])
 def be(hip, request):
     b = hip.Backend(precision=request.param)
     b.precision = request.param

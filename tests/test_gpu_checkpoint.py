@@ -134,15 +134,15 @@ def same(be, a, b, what):
     assert ga.tobytes() == gb.tobytes(), what
 
 
-@pytest.mark.parametrize("storage", ["float32", "bfloat16"])
+@pytest.mark.parametrize("storage", ["float32", "bfloat16", "float16"])
 def test_sam_load_equals_host_built_model(hip, be, orc, tmp_path, storage):
     import torch
     tw = trunk_weights(orc)
     dw = hip.random_decoder_weights(7)
-    if storage == "bfloat16":
-        # The host-built model gets the same bf16-rounded values.
+    if storage != "float32":
+        # The host-built model gets the same values rounded to the storage.
         rnd = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)) \
-            .bfloat16().float().numpy()
+            .to(getattr(torch, storage)).float().numpy()
         tw = dict(tw, pe_w=rnd(tw["pe_w"]), pos=rnd(tw["pos"]),
                   pos_embed=rnd(tw["pos_embed"]), lnpw=rnd(tw["lnpw"]),
                   lnpb=rnd(tw["lnpb"]),

@@ -880,13 +880,15 @@ __global__ __launch_bounds__(256) void k_attn_merge_few(attn_desc d,
 /* Merge of key-split partials (k_attn_bf16 with 8 < nsplit <= 64): a
  * wave per (unit, query). Lane s holds split s's (m, l): M = the largest m
  * over splits that saw a key, weights w_s = 2^(m_s - M), L = sum w_s l_s
- * (wave reductions); then lane c sums w_s o_s[c] over the splits (each
- * split's 64 channels one coalesced 256-byte read) and stores O = that / L
- * like the kernel's own epilogue (hd columns, fp32 or bf16). */
+ * (wave reductions). The wave then reads four splits at a time: lane
+ * group g = l / 16 takes splits g, g + 4, ..., each lane four channels
+ * (one coalesced 256-byte row per split and group), and the groups' sums
+ * meet by two cross-lane exchanges; O = sum / L is stored like the
+ * kernel's own epilogue (hd columns, fp32 or bf16). */
 __global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__restrict__ part,
                                                     int nsplit, int Np)
 {
-    const int l = threadIdx.x & 63;
+    const int l = threadIdx.x & 63, grp = l >> 4, c4 = (l & 15) * 4;
     const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
 
     if (g >= (long)d.nb * d.N)
@@ -905,20 +907,31 @@ __global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__
     const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
     const float wt = ls > 0.0f ? __builtin_amdgcn_exp2f(ms - M) : 0.0f;
     const float L = wave_sum(wt * ls);
-    const float *o = part + ((unit * nsplit) * Np + q) * 64 + l;
-    float acc = 0.0f;
+    const float *o = part + ((unit * nsplit) * Np + q) * 64 + c4;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll 8
-    for (int sp = 0; sp < nsplit; sp++)
-        acc = fmaf(__shfl(wt, sp, 64), o[(long)sp * Np * 64], acc);
-    if (l < d.hd) {
+#pragma unroll 4
+    for (int sp = grp; sp < nsplit; sp += 4) {
+        const float w_s = __shfl(wt, sp, 64);
+        const f32x4 v = *(const f32x4 *)(o + (long)sp * Np * 64);
+
+        acc += w_s * v;
+    }
+    for (int e = 0; e < 4; e++) {
+        acc[e] += __shfl_xor(acc[e], 16, 64);
+        acc[e] += __shfl_xor(acc[e], 32, 64);
+    }
+    if (grp == 0 && c4 < d.hd) {
         const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-        const long oi = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + l;
+        const long oi = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + c4;
+        const float inv = 1.0f / L;
 
-        if (d.odt == DT_F32)
-            ((float *)d.O)[oi] = acc / L;
-        else
-            ((uint16_t *)d.O)[oi] = f2bf(acc / L);
+        for (int e = 0; e < 4 && c4 + e < d.hd; e++) {
+            if (d.odt == DT_F32)
+                ((float *)d.O)[oi + e] = acc[e] * inv;
+            else
+                ((uint16_t *)d.O)[oi + e] = f2bf(acc[e] * inv);
+        }
     }
 }
 

@@ -492,7 +492,7 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * all its weights underflowed; where the first block takes the exact max,
  * m may also move down to a row's maximum far below 0. While every m of
  * the wave is 0 the scores feed exp2 directly. */
-template <bool EXT>
+template <bool EXT, bool H32>
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
@@ -626,17 +626,21 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             load_block(kb + 1, slot ^ 1);
         if (idle)
             return;
+        /* Head width 32 (H32): channels 32..63 of the packed operands are
+         * zero, so only the first two 16-channel steps of Q K^T and the
+         * first 32 output channels of P V carry work. */
         for (int c = 0; c < 2; c++)
-            for (int ds = 0; ds < 4; ds++)
+            for (int ds = 0; ds < (H32 ? 2 : 4); ds++)
                 kf[4 * c + ds] = *(const bf16x8 *)(Kb + 8192 * slot + 4096 * c + kro[ds]);
         for (int t4 = 0; t4 < 4; t4++) {
             vf[2 * t4] = *(const bf16x8 *)(Vb + 8192 * slot + vro[t4]);
-            vf[2 * t4 + 1] = *(const bf16x8 *)(Vb + 8192 * slot + 4096 + vro[t4]);
+            if (!H32)
+                vf[2 * t4 + 1] = *(const bf16x8 *)(Vb + 8192 * slot + 4096 + vro[t4]);
         }
         /* Both 32-key halves at once: two independent Q K^T chains. */
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qb[0], zero16, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4], qb[0], zero16, 0, 0, 0);
-        for (int ds = 1; ds < 4; ds++) {
+        for (int ds = 1; ds < (H32 ? 2 : 4); ds++) {
             s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s0, 0, 0, 0);
             s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4 + ds], qb[ds], s1, 0, 0, 0);
         }
@@ -714,7 +718,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             }
         for (int t4 = 0; t4 < 4; t4++) {
             st.o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4], pb[t4], st.o0, 0, 0, 0);
-            st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4 + 1], pb[t4], st.o1, 0, 0, 0);
+            if (!H32)
+                st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4 + 1], pb[t4], st.o1, 0, 0, 0);
         }
         for (int a = 0; a < 4; a++)
             for (int e = 0; e < 4; e++) {
@@ -948,16 +953,16 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk || nsplit > 64 ||
         (nsplit > 1 && !part))
         return hipErrorInvalidConfiguration;
-    if (d->bias || d->causal)
-        hipLaunchKernelGGL(k_attn_bf16<true>, dim3((unsigned)grid), dim3(256), 0,
-                           (hipStream_t)stream, *d,
+    {
+        auto kern = d->bias || d->causal ? (d->hd == 32 ? k_attn_bf16<true, true>
+                                                        : k_attn_bf16<true, false>)
+                                         : (d->hd == 32 ? k_attn_bf16<false, true>
+                                                        : k_attn_bf16<false, false>);
+
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
                            (const uint16_t *)vt16, knorm, part, nsplit);
-    else
-        hipLaunchKernelGGL(k_attn_bf16<false>, dim3((unsigned)grid), dim3(256), 0,
-                           (hipStream_t)stream, *d,
-                           (const uint16_t *)q16, (const uint16_t *)k16,
-                           (const uint16_t *)vt16, knorm, part, nsplit);
+    }
     err = hipGetLastError();
     if (err != hipSuccess || nsplit == 1)
         return err;

@@ -487,11 +487,13 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * and the packing kernel records each block's largest |k|, so a wave
  * first checks the bound |q| max|k| - m <= SAFE_SPAN for all its lanes
  * (three VALU operations); only blocks it cannot clear take the exact
- * block max with its cross-lane exchange. In the first block (m = 0) the
- * bound also keeps every score >= -SAFE_SPAN, so a row cannot start with
- * all its weights underflowed; where the first block takes the exact max,
- * m may also move down to a row's maximum far below 0. While every m of
- * the wave is 0 the scores feed exp2 directly. */
+ * block max with its cross-lane exchange. Each query then moves its own
+ * m: up to a block max above m + SAFE_SPAN (O and l shrink), or, while
+ * it has no weight yet, down to a block max below m - SAFE_SPAN. Hence
+ * every query's largest score so far stays within SAFE_SPAN of its m:
+ * no weight exceeds 2^SAFE_SPAN and the largest is >= 2^-SAFE_SPAN, at
+ * any score magnitude. While every m of the wave is 0 the scores feed
+ * exp2 directly. */
 template <bool EXT, bool H32>
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
@@ -548,7 +550,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     bf16x8 qb[4];
     SoftState st;
     float qn; /* |q| of this lane's query, rounded up */
-    bool fresh = true, shifted = false; /* shifted: some lane's m != 0 */
+    bool shifted = false; /* some lane's m != 0 */
 
     /* Async copy of block kb into `slot`: wave w, pass j fills LDS rows
      * 8 (2 w + j) .. +7; lane i lands on row + i / 8, physical chunk
@@ -684,29 +686,36 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                 s1[r] += key + 32 > qi ? -INFINITY : 0.0f;
             }
         if (check) {
-            /* Exact block max relative to m; move m (rescaling O, l and
-             * this block's scores) if it leaves the safe span. A lane
-             * whose keys are all masked in this block stays put. */
+            /* Exact block max relative to m, decided per query (lanes l
+             * and l ^ 32 share it): m moves up to a block max past
+             * m + SAFE_SPAN, rescaling O and l by at most 1; it moves down
+             * only while the query has no weight yet (l = 0, so O = 0 and
+             * nothing is rescaled) and its block max lies below
+             * m - SAFE_SPAN, so that its first weights do not underflow. A
+             * query whose keys are all masked in this block stays put. */
             float mx = max16(s1, max16(s0, -INFINITY));
 
             mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-            if (mx == -INFINITY)
-                mx = 0.0f;
-            if (__ballot(mx > SAFE_SPAN || (fresh && mx < -SAFE_SPAN)) != 0) {
-                const float corr = __builtin_amdgcn_exp2f(-mx);
+            const bool empty = st.l + __shfl_xor(st.l, 32, 64) == 0.0f;
+            const float mv = mx > SAFE_SPAN ||
+                                     (empty && mx < -SAFE_SPAN && mx != -INFINITY)
+                                 ? mx
+                                 : 0.0f;
+
+            if (__ballot(mv != 0.0f) != 0) {
+                const float corr = __builtin_amdgcn_exp2f(-__builtin_fmaxf(mv, 0.0f));
 
                 st.l *= corr;
                 for (int r = 0; r < 16; r++) {
                     st.o0[r] *= corr;
                     st.o1[r] *= corr;
-                    s0[r] -= mx;
-                    s1[r] -= mx;
+                    s0[r] -= mv;
+                    s1[r] -= mv;
                 }
-                st.m += mx;
+                st.m += mv;
                 shifted = true;
             }
         }
-        fresh = false;
         for (int r = 0; r < 16; r++) {
             s0[r] = __builtin_amdgcn_exp2f(s0[r]);
             s1[r] = __builtin_amdgcn_exp2f(s1[r]);

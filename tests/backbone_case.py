@@ -30,15 +30,18 @@ def block_weights(g, E, mlp, window):
     }
 
 
-def trunk_case(seed, grid, ps, E, mlp, windows):
+def trunk_case(seed, grid, ps, E, mlp, windows, pt=None):
     """Image (ImageNet-style (u - 0.5) / 0.5 of U(0, 1)), patch weight
-    [E, 3 ps^2], tiled position embedding [grid^2, E], ln_pre and one
-    weight dict per entry of `windows` (window side, 0 = global)."""
+    [E, 3 ps^2], position embedding of a pt x pt pretraining grid tiled
+    over the grid [grid^2, E] (pt 2, or 1 for an odd grid, unless given),
+    ln_pre and one weight dict per entry of `windows` (window side, 0 =
+    global)."""
     g = np.random.default_rng(seed)
     side = grid * ps
     img = ((g.random((3, side, side), dtype=np.float32) - 0.5) / 0.5)
     pe_w = xavier(g, E, 3 * ps * ps)
-    pt = 2 if grid % 2 == 0 else 1   # pretraining grid, tiled over the grid
+    if pt is None:
+        pt = 2 if grid % 2 == 0 else 1
     pe = (0.02 * g.standard_normal((pt * pt, E))).astype(np.float32)
     yy, xx = np.divmod(np.arange(grid * grid), grid)
     pos = pe[(yy % pt) * pt + xx % pt]

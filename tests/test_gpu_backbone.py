@@ -120,6 +120,70 @@ def test_trunk_prologue_full_size(hip, be, orc):
                   want) <= TOL[be.precision]
 
 
+# The 1008 x 1008 trunk: 32 blocks, global at 0-based 7, 15, 23, 31,
+# 24 x 24 windows elsewhere (sam3_model.c:1112-1135, model.c:541-548).
+FULL_WINDOWS = [0 if i in (7, 15, 23, 31) else 24 for i in range(32)]
+_full_oracle = {}
+
+
+def full_trunk_case():
+    """Inputs of the full trunk and the oracle's output (computed once per
+    session: the reference's profile=cpu sequence over 4.96 TFLOP)."""
+    if "case" not in _full_oracle:
+        from oracle import oracle as orc
+        case = bc.trunk_case(97, 72, 14, 1024, 4096, FULL_WINDOWS, pt=24)
+        img, pe_w, pos, lnpw, lnpb, blocks = case
+        print("oracle: full trunk, 32 blocks", flush=True)
+        want = orc.encode_trunk(img, 72, 14, 1024, 16, 64, 4096, pe_w, pos,
+                                lnpw, lnpb, blocks, orc.rope_table(24),
+                                orc.rope_table(72))
+        print("oracle: done", flush=True)
+        _full_oracle["case"] = (case, want)
+    return _full_oracle["case"]
+
+
+def test_trunk_full_size(hip, be, orc):
+    """The whole image encoder trunk of a 1008 x 1008 image: patch 14 ->
+    72 x 72 tokens of width 1024, 32 blocks of 16 heads x 64 with MLP
+    4096, axial RoPE, position embedding tiled from the 24 x 24
+    pretraining grid. The eager run against the oracle, then two replays
+    of the captured trunk graph (another image between them) bit for bit
+    against the eager run."""
+    (img, pe_w, pos, lnpw, lnpb, blocks), want = full_trunk_case()
+    grid, E = 72, 1024
+    blks = [upload_block(hip, be, w) for w in blocks]
+    m = hip.Model(be, grid=grid, embed=E, heads=16, blocks=blks, mlp=4096)
+    m.m.patch = 14
+    m.m.pe_w = be.upload_weight(pe_w)
+    m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(lnpw), be.upload(lnpb)
+    m.m.rope_win = be.upload(orc.rope_table(24))
+    m.m.rope_glob = be.upload(orc.rope_table(grid))
+    try:
+        def run(x):
+            hip.sam_encode_trunk(m, x)
+            be.finish()
+            return be.read(m.m.x, grid * grid * E).reshape(grid * grid, E)
+
+        print("trunk full 32 blocks %s: eager" % be.precision, flush=True)
+        eager = run(img)
+        assert np.isfinite(eager).all()
+        assert report("trunk full %s" % be.precision, eager,
+                      want) <= TOL[be.precision]
+        other = np.ascontiguousarray(img[:, ::-1, :])
+        print("trunk full 32 blocks %s: graph replays" % be.precision, flush=True)
+        hip.sam_trunk_graph(m)
+        assert m.m.trunk_exec
+        first = run(img)
+        flipped = run(other)
+        again = run(img)
+        assert np.array_equal(first, eager)
+        assert np.array_equal(again, eager)
+        assert not np.array_equal(flipped, eager)
+        hip.sam_trunk_graph(m, False)
+    finally:
+        m.free()
+
+
 def test_trunk_graph_replay(hip, be, orc):
     """HIP-graph replay of the trunk (sam_trunk_graph): every replay, with
     alternating images and eager work plus synchronisations between

@@ -29,7 +29,10 @@ def p_str(s):
 
 
 def p_int(i):
-    return b"J" + struct.pack("<i", i)
+    """BININT for 32-bit values, else LONG1 with eight bytes."""
+    if -2**31 <= i < 2**31:
+        return b"J" + struct.pack("<i", i)
+    return b"\x8a\x08" + struct.pack("<q", i)
 
 
 def p_tuple(items):

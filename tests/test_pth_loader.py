@@ -394,6 +394,32 @@ def test_structural_errors(hip, tmp_path):
         expect_open_error(hip, p, pattern)
 
 
+def test_view_extent_overflow(hip, tmp_path):
+    """Views whose extent arithmetic would overflow 64 bits (huge offset,
+    shape x stride, an expanded shape whose element count overflows) or
+    that reach before the storage are refused, not wrapped."""
+    big = 2 ** 62
+    cases = [
+        ("offset", 0, (4,), (1,)),
+        ("offset_big", big, (4,), (1,)),
+        ("negative_offset", -1, (4,), (1,)),
+        ("shape_stride", 0, (2 ** 33, 2 ** 33), (2 ** 33, 1)),
+        ("reach_wraps", 3, (2, 2), (big, big)),
+        ("numel", 0, (2 ** 40, 2 ** 40), (0, 0)),
+        ("negative_stride", 3, (4,), (-1,)),
+    ]
+    for name, off, shape, stride in cases:
+        p = tmp_path / (name + ".pt")
+        pkl = pc.p_state([("a", pc.p_tensor("0", "FloatStorage", off, shape,
+                                            stride, 4))])
+        pc.write_archive(str(p), pkl, {"0": bytes(16)})
+        if name == "offset":
+            ck = hip.Checkpoint(str(p))
+            ck.close()
+            continue
+        expect_open_error(hip, p, "Tensor <a> exceeds its storage in")
+
+
 def test_truncated_zip(hip, tmp_path):
     import torch
     src = tmp_path / "ok.pt"

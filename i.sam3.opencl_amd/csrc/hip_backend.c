@@ -6,6 +6,7 @@
  * one device, one in-order stream, device-resident buffers.
  */
 #include "hipb_internal.h"
+#include "sam3_launch.h"
 
 #include <hip/hip_runtime_api.h>
 
@@ -267,6 +268,10 @@ void hipb_init(struct hipb_backend *b, const char *device_opt,
                    prop.name, prop.gcnArchName);
         return;
     }
+    /* Address of this device's static scratch (mha_noalloc). */
+    hipb_check(dec_scratch_init(dev), "hipGetSymbolAddress (device scratch)");
+    if (hipb_failed())
+        return;
     b->global_mem = prop.totalGlobalMem;
     b->max_alloc = prop.totalGlobalMem / 4 * 3;
     b->cu_count = prop.multiProcessorCount;

@@ -556,6 +556,38 @@ static int many_chunk(int P, int Nq, int Nk)
     return (int)(chunk < MANY_STEP ? MANY_STEP : chunk);
 }
 
+/* Static device scratch of mha_noalloc: the split-K partial records of
+ * the many-keys kernel, for callers that cannot allocate (HIP graph
+ * capture, serving loops). Every GPU the library runs on holds its own
+ * copy, at its own address, until the process ends. The host refers to
+ * it only through the address hipGetSymbolAddress returns on each
+ * device (the array's name is a host-side stand-in). */
+static __device__ __align__(256) float scratch[MHA_NOALLOC_BYTES / sizeof(float)];
+
+#define SCRATCH_DEVICES 64
+static void *scratch_at[SCRATCH_DEVICES];
+
+extern "C" int dec_scratch_init(int device)
+{
+    void *p = NULL;
+    int err;
+
+    if (device < 0 || device >= SCRATCH_DEVICES)
+        return hipErrorInvalidDevice;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess)
+        return err;
+    __atomic_store_n(&scratch_at[device], p, __ATOMIC_RELEASE);
+    return hipSuccess;
+}
+
+extern "C" void *dec_scratch(int device)
+{
+    if (device < 0 || device >= SCRATCH_DEVICES)
+        return NULL;
+    return __atomic_load_n(&scratch_at[device], __ATOMIC_ACQUIRE);
+}
+
 extern "C" size_t mha_manykeys_scratch(int P, int Nq, int Nk)
 {
     const int chunk = many_chunk(P, Nq, Nk);

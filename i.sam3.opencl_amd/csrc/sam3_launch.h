@@ -172,6 +172,14 @@ int launch_mha_few32x4(const float *Q, long sq, const float *K, long sk,
  * partial results, mha_manykeys_scratch() bytes (0 when the key range is
  * not split: scratch may then be NULL). */
 size_t mha_manykeys_scratch(int P, int Nq, int Nk);
+/* Bytes of the static device scratch mha_noalloc uses for those partials
+ * (8 MiB: more than the many-keys split rule ever asks, about 4.7 MB at
+ * most); dec_scratch_init(device), with that device current, resolves
+ * its address on that device (hipb_init calls it), dec_scratch(device)
+ * returns it (NULL before). */
+#define MHA_NOALLOC_BYTES ((size_t)8 << 20)
+int dec_scratch_init(int device);
+void *dec_scratch(int device);
 int launch_mha_manykeys(const float *Q, long sq, const float *K, long sk,
                         const float *V, long sv, float *O, int P, int Nq,
                         int Nk, int dint, float scale, void *scratch,

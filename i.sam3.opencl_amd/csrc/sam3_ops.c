@@ -358,18 +358,24 @@ static size_t dec_extent(int P, long s, int rows, int dint)
     return (size_t)((long)(P - 1) * s + (long)rows * dint);
 }
 
-void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
-         long sq, hipb_mem kp, long sk, hipb_mem vp, long sv, hipb_mem o)
+/* mha and mha_noalloc: the many-keys split partials in the backend's
+ * scratch (grown on demand) or, with noalloc, in the library's static
+ * device scratch (no allocation, no profiling events). */
+static void mha_run(struct sam_model *m, const char *who, int noalloc, int P,
+                    int Nq, int Nk, int dint, hipb_mem qp, long sq, hipb_mem kp,
+                    long sk, hipb_mem vp, long sv, hipb_mem o)
 {
     struct hipb_backend *be = m->hip;
     const int c = dint / DEC_HEADS;
     const float scale = 1.0f / sqrtf((float)c);
     const int many = Nk > 64;
+    const char *what;
+    double flops;
     int err;
 
     if (P < 1 || Nq < 1 || Nk < 1 || dint < DEC_HEADS || sq < 0 || sk < 0 ||
         sv < 0) {
-        hipb_fatal("mha: invalid shape P=%d Nq=%d Nk=%d dint=%d", P, Nq, Nk,
+        hipb_fatal("%s: invalid shape P=%d Nq=%d Nk=%d dint=%d", who, P, Nq, Nk,
                    dint);
         return;
     }
@@ -381,42 +387,74 @@ void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
     }
     /* The many-keys kernel reads rows as 16-byte vectors. */
     if (many && (sq % 4 || sk % 4 || sv % 4)) {
-        hipb_fatal("mha: per-prompt strides must be multiples of 4 floats "
-                   "with many keys (sq=%ld sk=%ld sv=%ld)", sq, sk, sv);
+        hipb_fatal("%s: per-prompt strides must be multiples of 4 floats "
+                   "with many keys (sq=%ld sk=%ld sv=%ld)", who, sq, sk, sv);
         return;
     }
-    if (!buf_ok("mha", "q", qp, dec_extent(P, sq, Nq, dint), HIPB_F32) ||
-        !buf_ok("mha", "k", kp, dec_extent(P, sk, Nk, dint), HIPB_F32) ||
-        !buf_ok("mha", "v", vp, dec_extent(P, sv, Nk, dint), HIPB_F32) ||
-        !buf_ok("mha", "o", o, (size_t)P * Nq * dint, HIPB_F32))
+    if (!buf_ok(who, "q", qp, dec_extent(P, sq, Nq, dint), HIPB_F32) ||
+        !buf_ok(who, "k", kp, dec_extent(P, sk, Nk, dint), HIPB_F32) ||
+        !buf_ok(who, "v", vp, dec_extent(P, sv, Nk, dint), HIPB_F32) ||
+        !buf_ok(who, "o", o, (size_t)P * Nq * dint, HIPB_F32))
         return;
-    hipb_run_begin(be);
+    flops = 4.0 * P * DEC_HEADS * (double)Nq * Nk * c;
+    if (!noalloc)
+        hipb_run_begin(be);
     if (many) {
         const size_t need = mha_manykeys_scratch(P, Nq, Nk);
-        void *scr = need ? hipb_scratch(be, need) : NULL;
+        void *scr = NULL;
 
-        if (need && !scr)
-            return;
+        if (need && noalloc) {
+            if (need > MHA_NOALLOC_BYTES) {
+                hipb_fatal("%s: %zu bytes of split partials exceed the static "
+                           "scratch of %zu bytes", who, need, MHA_NOALLOC_BYTES);
+                return;
+            }
+            scr = dec_scratch(be->device);
+            if (!scr) {
+                hipb_fatal("%s: no device scratch on device %d (hipb_init "
+                           "resolves it)", who, be->device);
+                return;
+            }
+        }
+        else if (need) {
+            scr = hipb_scratch(be, need);
+            if (!scr)
+                return;
+        }
         err = launch_mha_manykeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
                                   o->ptr, P, Nq, Nk, dint, scale, scr,
                                   be->stream);
-        hipb_run_end(be, err, "attn_manykeys",
-                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+        what = "attn_manykeys";
     }
     else if (be->bf16 && c == 32 && Nk <= 8 && (sq | sk | sv) % 4 == 0) {
         /* precision=bf16: the decoder's token self-attention, four lanes
          * per (query, head) instead of the reference's one. */
         err = launch_mha_few32x4(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
                                  o->ptr, P, Nq, Nk, dint, scale, be->stream);
-        hipb_run_end(be, err, "attn_fewkeys",
-                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+        what = "attn_fewkeys";
     }
     else {
         err = launch_mha_fewkeys(qp->ptr, sq, kp->ptr, sk, vp->ptr, sv,
                                  o->ptr, P, Nq, Nk, dint, scale, be->stream);
-        hipb_run_end(be, err, "attn_fewkeys",
-                     4.0 * P * DEC_HEADS * (double)Nq * Nk * c);
+        what = "attn_fewkeys";
     }
+    if (!noalloc)
+        hipb_run_end(be, err, what, flops);
+    else if (err != hipSuccess)
+        hipb_fatal("HIP: %s failed: %s (%d)", what, hipb_errstr(err), err);
+}
+
+void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
+         long sq, hipb_mem kp, long sk, hipb_mem vp, long sv, hipb_mem o)
+{
+    mha_run(m, "mha", 0, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o);
+}
+
+void mha_noalloc(struct sam_model *m, int P, int Nq, int Nk, int dint,
+                 hipb_mem qp, long sq, hipb_mem kp, long sk, hipb_mem vp,
+                 long sv, hipb_mem o)
+{
+    mha_run(m, "mha_noalloc", 1, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o);
 }
 
 /* ------------------------------------------------------------ attention */

@@ -32,7 +32,8 @@ EXPORTS = [
     "hipb_prof_print", "hipb_timer_start", "hipb_timer_stop",
     "sam_path_init", "sam_path_free", "mat", "bmat", "gemm", "linear",
     "layernorm", "add_bcast", "softmax_rows", "rope_apply",
-    "window_partition", "window_unpartition_add", "mha", "attn_fused",
+    "window_partition", "window_unpartition_add", "mha", "mha_noalloc",
+    "attn_fused",
     "attn_packed", "vit_attention", "vit_block", "sam_encode_trunk",
     "sam_trunk_graph", "softmax_ext", "attend", "sam_dec_init",
     "sam_dec_free", "sam_dec_prepare", "sam_decode", "t2i_attention",
@@ -240,6 +241,7 @@ def lib():
                                          c_int]
     L.mha.argtypes = [MP, c_int, c_int, c_int, c_int, Mem, c_long, Mem,
                       c_long, Mem, c_long, Mem]
+    L.mha_noalloc.argtypes = L.mha.argtypes
     L.attn_fused.argtypes = [MP, c_int, c_int, c_int, Opnd, Opnd, Opnd, Opnd,
                              Mem, c_int, c_float]
     L.attn_packed.argtypes = [MP, c_int, c_int, c_int, Opnd]
@@ -637,6 +639,10 @@ def window_unpartition_add(m, X, Wd, H, C, ws, nwx):
 
 def mha(m, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o):
     _call(_lib.mha, m.ptr, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o)
+
+
+def mha_noalloc(m, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o):
+    _call(_lib.mha_noalloc, m.ptr, P, Nq, Nk, dint, qp, sq, kp, sk, vp, sv, o)
 
 
 def attn_fused(m, N, nb, nb1, Q, K, V, O, rope=None, npos=1, scale=0.125):

@@ -301,6 +301,19 @@ void window_unpartition_add(struct sam_model *m, hipb_mem X, hipb_mem Wd,
 void mha(struct sam_model *m, int P, int Nq, int Nk, int dint, hipb_mem qp,
          long sq, hipb_mem kp, long sk, hipb_mem vp, long sv, hipb_mem o);
 
+/* mha without allocating: no counterpart in the reference. For callers
+ * that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). Same arguments,
+ * results and errors as mha; the token -> image (Nk > 64) split-K
+ * partials go to a static device scratch of 8 MiB per GPU, held from
+ * hipb_init until the process ends, instead of the backend's scratch; a
+ * shape needing more is a fatal error. The call queues kernels only (no
+ * hipMalloc / hipFree, no profiling events). Calls that overlap on one
+ * GPU (several streams or backends) share that scratch and race. */
+void mha_noalloc(struct sam_model *m, int P, int Nq, int Nk, int dint,
+                 hipb_mem qp, long sq, hipb_mem kp, long sk, hipb_mem vp,
+                 long sv, hipb_mem o);
+
 /* Fused softmax attention of nb independent (window, head) units of N
  * tokens and head width 64: O = softmax(scale * rope(Q) rope(K)^T) V.
  * Q, K, V and O use the operand addressing of gemm (batch b split as

@@ -160,6 +160,9 @@ hipb_mem pth_upload(struct hipb_backend *b, const struct pth_file *pf,
                    t->name);
         return NULL;
     }
+    /* pth_open accepted the view only if storage_offset + span elements
+     * lie inside the storage and the element count stays below 2^56, so
+     * none of this overflows. */
     for (d = t->ndim - 1; d >= 0; d--) {
         if (t->shape[d] != 1 && t->stride[d] != expect)
             contiguous = 0;

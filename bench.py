@@ -41,11 +41,13 @@ COPY_BYTES = 256 << 20
 
 # HBM bytes per k_attn_bf16 launch (global, 5184 tokens x 16 heads), from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --kernel-only`
-# (KiB per dispatch), each scaled by what the counter reads for the
-# runtime's 256 MiB copy in the same run (FETCH_SIZE 2.0, WRITE_SIZE 1.0).
-# Summary and commands: profiles/attn_bf16_global_5184.md.
-ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15641.0, 20736.0
-FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+# (KiB per dispatch), each scaled by what the counter reads for the same
+# run's LayerNorm, whose bytes are known exactly (5184 x 1024 fp32 read with
+# gamma and beta, 20744 KiB, against FETCH_SIZE 10470 KiB; 5184 x 1024 bf16
+# written, 10368 KiB, against WRITE_SIZE 10370 KiB). Summary and commands:
+# profiles/attn_bf16_global_5184.md.
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15650.0, 20740.0
+FETCH_SCALE, WRITE_SCALE = 20744.0 / 10470.0, 10368.0 / 10370.0
 
 
 def load_hip():

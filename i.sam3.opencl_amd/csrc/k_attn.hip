@@ -30,43 +30,72 @@
 /* ------------------------------------------------------------ fp32 path */
 
 /* fp32 operands in the reference row layout (Q/K/V/O opnds of
- * sam3_model.c:1004-1011), v_mfma_f32_32x32x2_f32, 32-key blocks.
- * RoPE and the scale are applied on the loads. The contraction index of
- * Q K^T is ordered d = step + 32 h, so a lane's Q registers are one
- * contiguous half row and RoPE pairs stay in one lane. */
-__global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
+ * sam3_model.c:1004-1011, or the Q, K, V, O rows of the text path's
+ * attend, sam3_text.c:305-343), v_mfma_f32_32x32x2_f32, 32-key blocks:
+ * the exact path. N queries over Nk keys per unit, head width HD (64, or
+ * 32 for the text path's heads). RoPE (HD 64) and the scale are applied
+ * on the loads. The contraction index of Q K^T is ordered
+ * d = step + (HD / 2) h, so a lane's Q registers are one contiguous half
+ * row and RoPE pairs stay in one lane.
+ *
+ * EXT adds softmax_ext's terms (sam3_kernels.cl:885-921) the way it adds
+ * them: the causal mask (key j > query i: -inf), or an additive table
+ * [unit][N][Nk padded to 64] of dy + dx already summed (k_box_bias with
+ * scale 1), added to the scaled score as softmax_ext adds it.
+ *
+ * With nsplit > 1 the workgroup takes key blocks [kb0, kb1) of split sp
+ * (blockIdx.x = tile nsplit + sp) and leaves the unnormalised O, its
+ * reference point m (in log2 units) and l in `part`, in k_attn_bf16's
+ * record layout, for k_attn_merge(_few). A query none of whose keys the
+ * split sees (causal) keeps l = 0 and drops out of the merge. */
+template <int HD, bool EXT>
+__global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict__ part,
+                                                  int nsplit)
 {
-    __shared__ float Kt[2][64][33]; /* K^T block: [d][key] */
-    __shared__ float Vs[2][32][72]; /* V block:   [key][d] */
+    __shared__ float Kt[2][HD][33]; /* K^T block: [d][key] */
+    __shared__ float Vs[2][32][HD + 8]; /* V block:   [key][d] */
+    constexpr int HH = HD / 2;          /* channels per lane half */
+    constexpr int LPR = HD / 8;         /* loader threads per key row */
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
-    const int N = d.N;
-    const long b0 = blockIdx.y / d.nb1, b1 = blockIdx.y % d.nb1;
+    const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64,
+              Npk = (Nk + 63) / 64 * 64;
+    const int tile = blockIdx.x / nsplit, sp = blockIdx.x - tile * nsplit;
+    const long unit = blockIdx.y;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
     const float *Qb = (const float *)d.Q + d.qoff + b0 * d.sq0 + b1 * d.sq1;
     const float *Kb = (const float *)d.K + d.koff + b0 * d.sk0 + b1 * d.sk1;
     const float *Vb = (const float *)d.V + d.voff + b0 * d.sv0 + b1 * d.sv1;
     const float2 *cs = (const float2 *)d.rope;
-    const int qi = blockIdx.x * 128 + w * 32 + l32;
-    const int nblk = (N + 31) / 32;
-    /* Loader role: key row kr of a block, 8 channels from dc. */
-    const int kr = t >> 3, dc = (t & 7) * 8;
-    float qreg[32], kpre[8], vpre[8];
+    const int qi = tile * 128 + w * 32 + l32;
+    const int nblk = (Nk + 31) / 32;
+    const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
+    /* This lane's row of the bias table, if any (queries past N read the
+     * last row, never stored). */
+    const float *brow = EXT && d.bias
+                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * Npk
+                            : nullptr;
+    /* Loader role: key row kr of a block, 8 channels from dc; with HD 32
+     * the upper half of the threads loads nothing. */
+    const int kr = t / LPR, dc = (t % LPR) * 8;
+    const bool loader = t < 32 * LPR;
+    float qreg[HH], kpre[8], vpre[8];
     f32x16 o0, o1;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    /* Q: lane holds channels 32 h .. 32 h + 31 of query qi, rotated and
-     * scaled. */
-    for (int i = 0; i < 32; i++)
+    /* Q: lane holds channels HH h .. HH h + HH - 1 of query qi, rotated
+     * and scaled. */
+    for (int i = 0; i < HH; i++)
         qreg[i] = 0.0f;
     if (qi < N) {
-        const float *qr = Qb + (long)qi * d.ldq + 32 * h;
+        const float *qr = Qb + (long)qi * d.ldq + HH * h;
 
-        for (int i = 0; i < 32; i++)
+        for (int i = 0; i < HH; i++)
             qreg[i] = qr[i];
-        if (cs) {
+        if (HD == 64 && cs) {
             const float2 *rot = cs + (long)(qi % d.npos) * 32 + 16 * h;
 
-            for (int j = 0; j < 16; j++) {
+            for (int j = 0; j < HH / 2; j++) {
                 const float a = qreg[2 * j], b = qreg[2 * j + 1];
                 const float2 r = rot[j];
 
@@ -84,7 +113,7 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
     auto fetch = [&](int kb) {
         const int key = kb * 32 + kr;
 
-        if (key < N) {
+        if (loader && key < Nk) {
             const float *kp = Kb + (long)key * d.ldk + dc;
             const float *vp = Vb + (long)key * d.ldv + dc;
 
@@ -92,7 +121,7 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
                 kpre[e] = kp[e];
                 vpre[e] = vp[e];
             }
-            if (cs) {
+            if (HD == 64 && cs) {
                 const float2 *rot = cs + (long)(key % d.npos) * 32 + dc / 2;
 
                 for (int j = 0; j < 4; j++) {
@@ -111,48 +140,69 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
             }
     };
     auto stage = [&](int buf) {
-        for (int e = 0; e < 8; e++) {
-            Kt[buf][dc + e][kr] = kpre[e];
-            Vs[buf][kr][dc + e] = vpre[e];
-        }
+        if (loader)
+            for (int e = 0; e < 8; e++) {
+                Kt[buf][dc + e][kr] = kpre[e];
+                Vs[buf][kr][dc + e] = vpre[e];
+            }
     };
 
-    fetch(0);
+    fetch(kb0);
     stage(0);
     __syncthreads();
-    for (int kb = 0; kb < nblk; kb++) {
-        const int buf = kb & 1;
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int buf = (kb - kb0) & 1;
         f32x16 s;
-        float mx, m_new, corr, rs = 0.0f;
+        float mx, m_new, mref, corr, rs = 0.0f;
 
-        if (kb + 1 < nblk)
+        if (kb + 1 < kb1)
             fetch(kb + 1);
         for (int r = 0; r < 16; r++)
             s[r] = 0.0f;
 #pragma unroll
-        for (int st = 0; st < 32; st++)
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[buf][st + 32 * h][l32],
+        for (int st = 0; st < HH; st++)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[buf][st + HH * h][l32],
                                                      qreg[st], s, 0, 0, 0);
-        /* Scale, mask keys past N, online softmax. */
-        mx = -INFINITY;
+        /* Scale, mask keys past Nk, the causal mask or the bias, online
+         * softmax. Register r holds key kb 32 + 8 (r / 4) + 4 h + r % 4. */
         for (int r = 0; r < 16; r++) {
             const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
 
-            s[r] = key < N ? s[r] * d.scale : -INFINITY;
-            mx = fmaxf(mx, s[r]);
+            s[r] = key < Nk ? s[r] * d.scale : -INFINITY;
         }
+        if (EXT && d.causal)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+
+                if (key > qi)
+                    s[r] = -INFINITY;
+            }
+        else if (EXT && brow)
+            for (int g = 0; g < 4; g++) {
+                const f32x4 bv = *(const f32x4 *)(brow + kb * 32 + 8 * g + 4 * h);
+
+                for (int e = 0; e < 4; e++)
+                    s[4 * g + e] += bv[e];
+            }
+        mx = -INFINITY;
+        for (int r = 0; r < 16; r++)
+            mx = fmaxf(mx, s[r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         m_new = fmaxf(m_run, mx);
-        corr = __builtin_amdgcn_exp2f((m_run - m_new) * LOG2E_F);
+        /* No key seen yet (all masked so far): nothing to rescale, and
+         * every weight of this block is 0. */
+        mref = m_new == -INFINITY ? 0.0f : m_new;
+        corr = m_run == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m_run - mref) * LOG2E_F);
         for (int r = 0; r < 16; r++) {
-            s[r] = __builtin_amdgcn_exp2f((s[r] - m_new) * LOG2E_F);
+            s[r] = __builtin_amdgcn_exp2f((s[r] - mref) * LOG2E_F);
             rs += s[r];
         }
         l_run = l_run * corr + rs;
         m_run = m_new;
         for (int r = 0; r < 16; r++) {
             o0[r] *= corr;
-            o1[r] *= corr;
+            if (HD == 64)
+                o1[r] *= corr;
         }
         /* O^T += V^T P^T: step st contracts key 8 (st / 4) + 4 h + st % 4,
          * the key of this lane's score register st. */
@@ -162,16 +212,40 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
 
             o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][l32], s[st],
                                                       o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][32 + l32],
-                                                      s[st], o1, 0, 0, 0);
+            if (HD == 64)
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][32 + l32],
+                                                          s[st], o1, 0, 0, 0);
         }
-        if (kb + 1 < nblk)
+        if (kb + 1 < kb1)
             stage(buf ^ 1);
         __syncthreads();
     }
 
     l_run += __shfl_xor(l_run, 32, 64);
-    if (qi < N) {
+    if (qi >= N)
+        return;
+    if (nsplit > 1) {
+        /* Partial record: O rows of 64 floats (HD columns used), then
+         * (m in log2 units, l). */
+        const long pidx = (unit * nsplit + sp) * (long)Np + qi;
+        float *orow = part + pidx * 64;
+
+        for (int r = 0; r < 16; r++) {
+            const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+
+            orow[dd] = o0[r];
+            if (HD == 64)
+                orow[32 + dd] = o1[r];
+        }
+        if (h == 0) {
+            float *ml = part + (long)d.nb * nsplit * Np * 64 + pidx * 2;
+
+            ml[0] = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
+            ml[1] = l_run;
+        }
+        return;
+    }
+    {
         const float inv = 1.0f / l_run;
         const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
 
@@ -180,23 +254,16 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d)
 
             if (d.odt == DT_F32) {
                 ((float *)d.O)[orow + dd] = o0[r] * inv;
-                ((float *)d.O)[orow + 32 + dd] = o1[r] * inv;
+                if (HD == 64)
+                    ((float *)d.O)[orow + 32 + dd] = o1[r] * inv;
             }
             else {
                 ((uint16_t *)d.O)[orow + dd] = f2bf(o0[r] * inv);
-                ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(o1[r] * inv);
+                if (HD == 64)
+                    ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(o1[r] * inv);
             }
         }
     }
-}
-
-extern "C" int launch_attn_f32(const attn_desc *d, void *stream)
-{
-    if (d->nb > 65535)
-        return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(k_attn_f32, dim3((d->N + 127) / 128, d->nb), dim3(256),
-                       0, (hipStream_t)stream, *d);
-    return hipGetLastError();
 }
 
 /* ------------------------------------------------------------ packing */
@@ -339,16 +406,18 @@ extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
     return hipGetLastError();
 }
 
-/* Additive bias of the bf16 attention in its exp2 domain,
- * out[unit][i][j] = log2(e) (dy[(i H + j / W) nh + h] + dx[(i W + j % W)
+/* Additive bias table of the fused attention kernels,
+ * out[unit][i][j] = unit_scale (dy[(i H + j / W) nh + h] + dx[(i W + j % W)
  * nh + h]) for keys j < Nk and -inf for the padding up to Npk (unit = head
  * h, H = Nk / W): the box relative position bias of softmax_ext
- * (sam3_kernels.cl:904-906) for every (head, query, key). */
+ * (sam3_kernels.cl:904-906) for every (head, query, key), with unit_scale
+ * log2(e) for the bf16 kernel's exp2 domain and 1 for the exact path (the
+ * sum dy + dx then has softmax_ext's own rounding). */
 __global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
                                                   const float *__restrict__ dy,
                                                   const float *__restrict__ dx,
                                                   int heads, int Nq, int Nk, int Npk,
-                                                  int W, int nh)
+                                                  int W, int nh, float unit_scale)
 {
     /* Workgroup: one (head, query) row; its H dy and W dx values go to
      * LDS once, then the row is written as 16-byte runs of four keys. */
@@ -368,7 +437,7 @@ __global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
         for (int k = 0; k < 4; k++) {
             const unsigned j = j0 + k, y = j / (unsigned)W;
 
-            v[k] = j < (unsigned)Nk ? (sy[y] + sx[j - y * W]) * LOG2E_F : -INFINITY;
+            v[k] = j < (unsigned)Nk ? (sy[y] + sx[j - y * W]) * unit_scale : -INFINITY;
         }
         *(f32x4 *)(orow + j0) = v;
     }
@@ -376,7 +445,7 @@ __global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
 
 extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
                                int heads, int Nq, int Nk, int W, int nh,
-                               void *stream)
+                               float unit_scale, void *stream)
 {
     const int Npk = (Nk + 63) / 64 * 64;
     const long rows = (long)heads * Nq;
@@ -387,7 +456,8 @@ extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
     if (rows > 0x7fffffffL || W < 1 || lds > 65536)
         return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_box_bias, dim3((unsigned)rows), dim3(256), lds,
-                       (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh);
+                       (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh,
+                       unit_scale);
     return hipGetLastError();
 }
 
@@ -971,6 +1041,38 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
                            (const uint16_t *)vt16, knorm, part, nsplit);
+    }
+    err = hipGetLastError();
+    if (err != hipSuccess || nsplit == 1)
+        return err;
+    if (nsplit <= 8)
+        hipLaunchKernelGGL(k_attn_merge_few, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
+                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
+                           nsplit, Np);
+    else
+        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 3) / 4)),
+                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
+                           nsplit, Np);
+    return hipGetLastError();
+}
+
+extern "C" int launch_attn_f32(const attn_desc *d, float *part, int nsplit, void *stream)
+{
+    const int nblk = (d->Nk + 31) / 32, Np = (d->N + 63) / 64 * 64;
+    const long gx = (long)((d->N + 127) / 128) * nsplit;
+    const bool ext = d->causal || d->bias;
+    int err;
+
+    if (d->nb > 65535 || gx > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > 64 ||
+        nsplit > nblk || (nsplit > 1 && !part) || (d->hd != 64 && d->hd != 32) ||
+        (d->hd == 32 && d->rope))
+        return hipErrorInvalidConfiguration;
+    {
+        auto kern = d->hd == 32 ? (ext ? k_attn_f32<32, true> : k_attn_f32<32, false>)
+                                : (ext ? k_attn_f32<64, true> : k_attn_f32<64, false>);
+
+        hipLaunchKernelGGL(kern, dim3((unsigned)gx, d->nb), dim3(256), 0,
+                           (hipStream_t)stream, *d, part, nsplit);
     }
     err = hipGetLastError();
     if (err != hipSuccess || nsplit == 1)

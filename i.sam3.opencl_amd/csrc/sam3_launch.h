@@ -134,8 +134,13 @@ struct attn_desc {
     int causal;
 };
 
-/* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads. */
-int launch_attn_f32(const struct attn_desc *d, void *stream);
+/* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads; N
+ * queries over Nk keys, head width 64 or 32 (no RoPE), the causal mask or
+ * an additive bias table in natural units (d->bias, as launch_box_bias
+ * with unit_scale 1 writes it). With 1 < nsplit <= 64 the 32-key blocks
+ * are split nsplit ways, `part` (nb nsplit Np 66 floats) holds the
+ * partials and the bf16 path's merge kernels combine them into O. */
+int launch_attn_f32(const struct attn_desc *d, float *part, int nsplit, void *stream);
 
 /* Packed bf16 staging of the fast path, Np = N rounded up to 64:
  * q16/k16 [nb][Np][64] (RoPE applied, q scaled), vt16 [nb][64][Np],
@@ -152,12 +157,13 @@ int launch_attn_bf16(const struct attn_desc *d, const void *q16,
                      const void *k16, const void *vt16, const float *knorm,
                      float *part, int nsplit, void *stream);
 
-/* Additive bias table of the bf16 attention from the box relative
+/* Additive bias table of the fused attention from the box relative
  * position bias of softmax_ext: out [heads][Nq][Nk padded to 64] =
- * log2(e) (dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h]), -inf in
- * the padding (H = Nk / W). */
+ * unit_scale (dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h]), -inf in
+ * the padding (H = Nk / W); unit_scale log2(e) for the bf16 kernel, 1 for
+ * the exact path. */
 int launch_box_bias(float *out, const float *dy, const float *dx, int heads,
-                    int Nq, int Nk, int W, int nh, void *stream);
+                    int Nq, int Nk, int W, int nh, float unit_scale, void *stream);
 
 /* Decoder attention (8 heads, head width c = dint / 8). */
 int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,

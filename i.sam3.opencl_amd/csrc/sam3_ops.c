@@ -24,6 +24,7 @@
 #define ENC_EPS 1e-5f   /* ViT LayerNorm eps (sam3_model.c:30) */
 #define SAM_PATCH 14    /* ViT patch side (sam3_model.h:10) */
 #define DEC_HEADS 8     /* decoder heads (sam3_model.c:36) */
+#define LOG2E_HOST 1.4426950408889634f /* the bf16 kernel scores in log2 units */
 
 struct opnd mat(hipb_mem buf, long off, int ld)
 {
@@ -532,12 +533,8 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
                    Nk, nb, nb1, npos);
         return;
     }
-    if (!(hd == 64 || (hd == 32 && b->bf16 && !rope))) {
+    if (!(hd == 64 || (hd == 32 && !rope))) {
         hipb_fatal("%s: unsupported head width %d", who, hd);
-        return;
-    }
-    if (!b->bf16 && (Nk != N || causal || bias)) {
-        hipb_fatal("%s: key count, mask and bias need the bf16 path", who);
         return;
     }
     if (N == 0 || Nk == 0)
@@ -585,13 +582,14 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
     d.Nk = Nk;
     d.causal = causal != 0;
     d.bias = bias ? (const float *)bias->ptr : NULL;
+    if (bias && !buf_ok(who, "bias table", bias,
+                        (size_t)nb * N * (((size_t)Nk + 63) / 64 * 64), HIPB_F32))
+        return;
     if (b->bf16) {
         const size_t np = ((size_t)N + 63) / 64 * 64;
         const size_t npk = ((size_t)Nk + 63) / 64 * 64;
 
-        if ((bias && !buf_ok(who, "bias table", bias, (size_t)nb * N * npk,
-                             HIPB_F32)) ||
-            !ensure_bf16(b, &m->q16, (size_t)nb * np * 64, "packed q") ||
+        if (!ensure_bf16(b, &m->q16, (size_t)nb * np * 64, "packed q") ||
             !ensure_bf16(b, &m->k16, (size_t)nb * npk * 64, "packed k") ||
             !ensure_bf16(b, &m->vt16, (size_t)nb * npk * 64, "packed v^T") ||
             !ensure_typed(b, &m->knorm, (size_t)nb * (npk / 64), HIPB_F32,
@@ -617,9 +615,16 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         }
         return;
     }
-    hipb_run_begin(b);
-    err = launch_attn_f32(&d, b->stream);
-    hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)N * hd * nb);
+    {
+        const int ns = attn_splits(b, N, Nk, nb);
+        float *part = attn_part(m, N, nb, ns);
+
+        if (ns > 1 && !part)
+            return;
+        hipb_run_begin(b);
+        err = launch_attn_f32(&d, part, ns, b->stream);
+        hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)Nk * hd * nb);
+    }
 }
 
 void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
@@ -705,12 +710,11 @@ void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
             hipb_fatal("attend: box bias needs dy, dx and W dividing Nk");
         return;
     }
-    /* Fused: the bf16 path for head width 64 or 32 with any mask or bias
-     * (the bias as a table in the kernel's exp2 domain), the fp32 path
-     * for head width 64 self-attention without either. Heads are the
-     * units, head h at column h hd of every operand. */
-    if ((b->bf16 && (hd == 64 || hd == 32)) ||
-        (hd == 64 && Nq == Nk && !causal && !dy)) {
+    /* Fused for head width 64 or 32 with any mask or bias, on both paths
+     * (the bias as a table: in the bf16 kernel's exp2 domain, or as the
+     * sums dy + dx for the exact path). Heads are the units, head h at
+     * column h hd of every operand. */
+    if (hd == 64 || hd == 32) {
         if (dy) {
             const size_t npk = ((size_t)Nk + 63) / 64 * 64;
             int err;
@@ -721,7 +725,7 @@ void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
             hipb_run_begin(b);
             err = launch_box_bias((float *)m->abias->ptr, (const float *)dy->ptr,
                                   (const float *)dx->ptr, heads, Nq, Nk, W,
-                                  heads, b->stream);
+                                  heads, b->bf16 ? LOG2E_HOST : 1.0f, b->stream);
             hipb_run_end(b, err, "box_bias", 0.0);
             if (hipb_failed())
                 return;

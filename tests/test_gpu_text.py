@@ -10,10 +10,10 @@ P V), at the shapes the text path runs:
 - text encoder self-attention: 32 tokens, 16 heads x 64, causal
   (sam3_text.c:489-490).
 
-The bf16 path runs all three in the fused kernel (bias as an additive
-table, causal mask, head width 32 packed to 64); the fp32 path runs the
-reference's chunked gemm / softmax_ext / gemm for all three (head width
-32, the mask and the bias are outside its fused kernel).
+Both paths run all three in a fused kernel (bias as an additive table,
+causal mask, head width 32): bf16 MFMA with the bias in the exp2 domain,
+or f32 MFMA with the sums dy + dx added as softmax_ext adds them; other
+head widths take the reference's chunked gemm / softmax_ext / gemm.
 
 Bars: rel-L2 <= 2e-5 (fp32), <= 2e-2 (bf16); max-abs printed.
 """
@@ -105,27 +105,36 @@ def test_text_encoder_causal(hip, be, orc):
         assert np.array_equal(got[0], V[0])
 
 
-def test_score_chunks_and_capacity(hip, be):
-    """One head per score chunk gives the result of all heads at once (the
-    chunk offset reaches the bias and the operand columns); on the fp32
-    path, which runs the reference's chunked sequence for biased
-    attention, a buffer that cannot hold one head's scores is the
-    reference's fatal error (the bf16 path's fused kernel needs none)."""
-    Nq, W, heads, hd = 30, 6, 4, 32
+def test_score_chunks_and_capacity(hip, be, orc):
+    """Head widths the fused kernels do not take (16 here) run the
+    reference's chunked sequence on both paths: one head per score chunk
+    gives the result of all heads at once (the chunk offset reaches the
+    bias and the operand columns), matching the oracle, and a buffer that
+    cannot hold one head's scores is the reference's fatal error. At head
+    width 32 the fused kernel needs no score buffer: the capacity leaves
+    its result unchanged."""
+    Nq, W, heads = 30, 6, 4
     Nk = W * 5
     g = np.random.default_rng(34)
-    Q = g.standard_normal((Nq, heads * hd + 8)).astype(np.float32)
-    K, V = (g.standard_normal((Nk, heads * hd)).astype(np.float32) for _ in range(2))
-    dy = g.standard_normal((Nq, 5, heads)).astype(np.float32)
-    dx = g.standard_normal((Nq, W, heads)).astype(np.float32)
-    a = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
-    b = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W, score_cap=Nq * Nk)
-    assert np.array_equal(a, b)
-    if be.precision != "fp32":
-        return
-    with pytest.raises(hip.Sam3HipError):
-        _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
-             score_cap=Nq * Nk - 1)
+    for hd in (16, 32):
+        Q = g.standard_normal((Nq, heads * hd + 8)).astype(np.float32)
+        K, V = (g.standard_normal((Nk, heads * hd)).astype(np.float32)
+                for _ in range(2))
+        dy = g.standard_normal((Nq, 5, heads)).astype(np.float32)
+        dx = g.standard_normal((Nq, W, heads)).astype(np.float32)
+        a = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+        b = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W, score_cap=Nq * Nk)
+        assert np.array_equal(a, b)
+        want = orc.attend(Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+        assert report("chunks hd=%d %s" % (hd, be.precision), a, want) <= TOL[be.precision]
+        if hd == 16:
+            with pytest.raises(hip.Sam3HipError):
+                _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
+                     score_cap=Nq * Nk - 1)
+        else:
+            c = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W,
+                     score_cap=Nq * Nk - 1)
+            assert np.array_equal(a, c)
 
 
 def test_long_causal_split_keys(hip, be, orc):

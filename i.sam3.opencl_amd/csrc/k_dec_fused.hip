@@ -163,7 +163,12 @@ __device__ __forceinline__ unsigned swz_off(int row, int chunk, int rowbytes)
  * XCD-contiguous order, blocked as described at the item decode. X rows of K floats (per-prompt
  * stride xs, 0 = shared), plus PE rows when pe != NULL; residual R
  * (stride rs, 0 = shared); out [P][T][256] may alias R. */
-template <int K>
+/* RX: the residual R is the input X itself (layer 1: R = keys, X = keys +
+ * PE added on load). The S^T loop then drops each token's loaded keys
+ * into the output accumulators U^T in their channel layout (an exchange
+ * with lane l ^ 32 per step), so the U^T product adds onto the residual and
+ * the keys are read from HBM once instead of twice. */
+template <int K, bool RX>
 __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     const float *X, long xs, const float *__restrict__ pe,
     const uint16_t *__restrict__ Wt16, const float *__restrict__ bt,
@@ -215,15 +220,38 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     const float *xr = X + (long)p * xs + (long)(valid ? j : 0) * K;
     const float *per = pe ? pe + (long)(valid ? j : 0) * K : nullptr;
     f32x16 s0 = {}, s1 = {};
+    /* U^T accumulators (8 tiles of 32 channels x 32 tokens): register r of
+     * tile c is channel 32 c + 8 (r / 4) + 4 hh + r % 4 of token l32. With
+     * RX they start as the residual. */
+    f32x16 u[8];
+
+    for (int c = 0; c < 8; c++)
+        u[c] = (f32x16){};
 
     /* S^T = Wt X^T over K / 16 steps; the lane's B operand is 8
      * consecutive inputs of its token, converted to bf16. */
-#pragma unroll 4
+#pragma unroll(RX ? K / 16 : 4)
     for (int st = 0; st < K / 16; st++) {
         const int c0 = 16 * st + 8 * hh;
         f32x4 a0 = *(const f32x4 *)(xr + c0), a1 = *(const f32x4 *)(xr + c0 + 4);
         bf16x8 bx;
 
+        if constexpr (RX) {
+            /* Lane hh holds channels 16 st + 8 hh .. +7 of its token; U^T
+             * wants channels 16 st + 4 hh .. +3 and 16 st + 8 + 4 hh .. +3
+             * in lane hh: lane 0 keeps a0 and takes lane 1's a0, lane 1
+             * keeps a1 and takes lane 0's a1. */
+            f32x4 give = hh ? a0 : a1, got;
+
+            for (int e = 0; e < 4; e++)
+                got[e] = __shfl_xor(give[e], 32, 64);
+            const f32x4 lo = hh ? got : a0, hi = hh ? a1 : got;
+
+            for (int e = 0; e < 4; e++) {
+                u[st / 2][8 * (st & 1) + e] = lo[e];
+                u[st / 2][8 * (st & 1) + 4 + e] = hi[e];
+            }
+        }
         if (per) {
             const f32x4 p0 = *(const f32x4 *)(per + c0), p1 = *(const f32x4 *)(per + c0 + 4);
 
@@ -273,10 +301,6 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
 
     /* U^T = Y^T A^T: 8 channel tiles x 4 k steps; the B operand of step st
      * is registers 8 (st % 2) .. + 7 of score tile st / 2. */
-    f32x16 u[8];
-
-    for (int c = 0; c < 8; c++)
-        u[c] = (f32x16){};
     for (int st = 0; st < 4; st++) {
         const f32x16 &sc = st < 2 ? s0 : s1;
         bf16x8 pb;
@@ -309,6 +333,18 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
 
 #pragma unroll
     for (int c = 0; c < 8; c++) {
+        if constexpr (RX) {
+            /* The residual is already in u. */
+            for (int q = 0; q < 4; q++) {
+                const f32x4 b4 = *(const f32x4 *)(bo + 32 * c + 8 * q + 4 * hh);
+
+                for (int i = 0; i < 4; i++) {
+                    u[c][4 * q + i] += b4[i];
+                    sum += u[c][4 * q + i];
+                }
+            }
+            continue;
+        }
         for (int k = 0; k < 4; k++) {
             /* Rows past T read row T - 1 (no branch around the load). */
             const int tok = 8 * k + (l >> 3), ck = l & 7;
@@ -379,13 +415,18 @@ extern "C" int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
           (uintptr_t)g | (uintptr_t)b | (uintptr_t)(pe ? pe : X) |
           (uintptr_t)Wt16 | (uintptr_t)YT16) & 15))
         return hipErrorInvalidValue;
-    if (K == 256)
-        hipLaunchKernelGGL(k_i2t_fused<256>, dim3((unsigned)grid), dim3(256), 0,
+    if (K == 256 && R == X && rs == xs)
+        hipLaunchKernelGGL((k_i2t_fused<256, true>), dim3((unsigned)grid), dim3(256), 0,
+                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
+                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
+                           eps);
+    else if (K == 256)
+        hipLaunchKernelGGL((k_i2t_fused<256, false>), dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
                            bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
                            eps);
     else
-        hipLaunchKernelGGL(k_i2t_fused<128>, dim3((unsigned)grid), dim3(256), 0,
+        hipLaunchKernelGGL((k_i2t_fused<128, false>), dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
                            bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
                            eps);

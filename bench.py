@@ -740,6 +740,16 @@ def main():
     ms = timed(be, glob.attn, args.steps, args.warmup)
     tflops = glob.flops() / ms / 1e9
     wms = timed(be, win.attn, args.steps, args.warmup)
+    # Config 1: one 576-token window (16 heads), the shape the reference's
+    # own CPU run takes; and its exact path.
+    one = Block(hip, be, 24, seed=1, grid=24)
+    one.region()
+    be.finish()
+    one_ms = timed(be, one.attn, sub_steps, sub_warm)
+    one32 = Block(hip, be32, 24, seed=1, grid=24)
+    one32.region()
+    be32.finish()
+    one32_ms = timed(be32, one32.attn_f32, sub_steps, sub_warm)
     region_ms = timed(be, glob.region, sub_steps, sub_warm)
     qkv_ms = timed(be, glob.qkv_gemm, sub_steps, sub_warm)
     w_region = timed(be, win.region, sub_steps, sub_warm)
@@ -771,6 +781,11 @@ def main():
                      "pct_bf16_peak": round(100 * win.flops() / wms / 1e9 /
                                             PEAK_BF16, 2),
                      "region_ms": round(w_region, 4)},
+        "single_window": {"workload": "1 window x 576 tokens, 16 heads x 64",
+                          "bf16_ms": round(one_ms, 5),
+                          "bf16_TFLOP/s": round(one.flops() / one_ms / 1e9, 2),
+                          "fp32_ms": round(one32_ms, 5),
+                          "fp32_TFLOP/s": round(one.flops() / one32_ms / 1e9, 2)},
         "global_region_ms": round(region_ms, 4),
         "qkv_gemm_bf16": {"ms": round(qkv_ms, 4),
                           "TFLOP/s": round(qkv_flops / qkv_ms / 1e9, 1)},

@@ -483,6 +483,20 @@ __device__ __forceinline__ float max16(const f32x16 &s, float m)
     return m;
 }
 
+/* Sum of the 32 weights of a block (pairwise, f32 adds). The row sums of
+ * P are taken from the f32 exponentials with VALU adds rather than with
+ * v_dot2_f32_bf16 on the bf16 weights: on gfx950 that dot product waits
+ * for the MFMA pipe, so it stalls behind every matrix product in flight
+ * on the SIMD, while plain adds issue beside them. */
+__device__ __forceinline__ float sum32(const f32x16 &a, const f32x16 &b)
+{
+    float t[8];
+
+    for (int i = 0; i < 8; i++)
+        t[i] = (a[2 * i] + a[2 * i + 1]) + (b[2 * i] + b[2 * i + 1]);
+    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
 /* LDS rows of K [key][d] and V^T [d][key] blocks are 64 bf16 (128 B, no
  * padding); the 16-byte chunk c of row r is stored at chunk
  * c ^ ((r >> 1) & 7). A 16-lane group of 16-byte reads then touches 16
@@ -615,7 +629,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                             ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * Npk
                             : nullptr;
     const int krow = kperm(l32);
-    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
     const f32x16 zero16 = {};
     bf16x8 qb[4];
     SoftState st;
@@ -800,14 +813,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             if (!H32)
                 st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4 + 1], pb[t4], st.o1, 0, 0, 0);
         }
-        for (int a = 0; a < 4; a++)
-            for (int e = 0; e < 4; e++) {
-                bf16x2 p2;
-
-                p2.x = pb[a][2 * e];
-                p2.y = pb[a][2 * e + 1];
-                st.l = __builtin_amdgcn_fdot2_f32_bf16(p2, ones, st.l, false);
-            }
+        st.l += sum32(s0, s1);
     };
     for (int kb = kb0; kb < kb1; kb += 2) {
         block(kb, std::integral_constant<int, 0>());

@@ -124,13 +124,14 @@ __device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0
             for (int e = 0; e < 4; e++) {
                 pk[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
                 if (third == 1) {
-                    /* Built element-wise: a bit-cast of pk[e] here was
-                     * compiled to reads of stale registers. */
-                    bf16x2 b2;
+                    /* Squares of the two bf16 values as floats, with FMAs:
+                     * v_dot2_f32_bf16 would wait for the MFMA pipe, busy
+                     * with the other workgroup's K loop. */
+                    const uint32_t u = pk[e];
+                    const float lo = __builtin_bit_cast(float, u << 16),
+                                hi = __builtin_bit_cast(float, u & 0xffff0000u);
 
-                    b2.x = (__bf16)v[2 * e];
-                    b2.y = (__bf16)v[2 * e + 1];
-                    ps = __builtin_amdgcn_fdot2_f32_bf16(b2, b2, ps, false);
+                    ps = fmaf(hi, hi, fmaf(lo, lo, ps));
                 }
             }
             *(u32x4 *)(dst + (long)row * 64) = pk;
@@ -319,9 +320,10 @@ k_gemm_nt(gemm_desc d)
             nt_pack_rope(d, m0, n0, t, rot);
     }
 
-    __syncthreads();
-#pragma clang loop unroll(full)
-    for (int c = 0; c < BM / CR; c++) {
+    /* The activation is chosen once, outside the element loops: a
+     * per-element switch on d.act costs more than the K loop's tail. */
+    auto stage_out = [&](int c, auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
 #pragma clang loop unroll(full)
         for (int i = 0; i < NA; i++) {
             const int rb = wm * WM + 32 * i - c * CR; /* block row in chunk */
@@ -337,9 +339,20 @@ k_gemm_nt(gemm_desc d)
 #pragma clang loop unroll(full)
                 for (int r = 0; r < 16; r++)
                     E[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * LD + col] =
-                        nt_act(d.alpha * cv[r] + bn, d.act);
+                        nt_act(d.alpha * cv[r] + bn, ACT);
             }
         }
+    };
+
+    __syncthreads();
+#pragma clang loop unroll(full)
+    for (int c = 0; c < BM / CR; c++) {
+        if (d.act == ACT_GELU_K)
+            stage_out(c, std::integral_constant<int, ACT_GELU_K>());
+        else if (d.act == ACT_RELU_K)
+            stage_out(c, std::integral_constant<int, ACT_RELU_K>());
+        else
+            stage_out(c, std::integral_constant<int, ACT_NONE_K>());
         __syncthreads();
         if constexpr (BM == 128 && BN == 128) {
             if (d.pack_N > 0) {
@@ -347,69 +360,95 @@ k_gemm_nt(gemm_desc d)
                 return;
             }
         }
-        for (int it = 0; it < CR / RPI; it++) {
-            const int row = it * RPI + t / (BN / 4), col = (t % (BN / 4)) * 4;
-            const int m = m0 + c * CR + row, n = n0 + col;
-            long crow = m;
-            bool keep = m < d.M && n < d.N;
+        /* Output type, residual and window remap chosen once per chunk. */
+        auto store_rows = [&](auto f32_c, auto res_c, auto unpart_c) {
+            constexpr bool F32 = decltype(f32_c)::value, RES = decltype(res_c)::value,
+                           UNPART = decltype(unpart_c)::value;
 
-            if (d.unpart_ws > 0) {
-                const int ws = d.unpart_ws, wsz = ws * ws;
-                const int w = m / wsz, p = m - w * wsz;
-                const int py = p / ws, wy = w / d.unpart_nwx;
-                const int y = wy * ws + py;
-                const int x = (w - wy * d.unpart_nwx) * ws + (p - py * ws);
+            for (int it = 0; it < CR / RPI; it++) {
+                const int row = it * RPI + t / (BN / 4), col = (t % (BN / 4)) * 4;
+                const int m = m0 + c * CR + row, n = n0 + col;
+                long crow = m;
+                bool keep = m < d.M && n < d.N;
 
-                keep = keep && y < d.unpart_H && x < d.unpart_H;
-                crow = (long)y * d.unpart_H + x;
-            }
-            if (!keep)
-                continue;
-            const f32x4 v4 = *(const f32x4 *)&E[row * LD + col];
-            const long idx = d.coff + crow * d.ldc + n;
-            const long ridx = d.roff + crow * d.ldc + n;
+                if (UNPART) {
+                    const int ws = d.unpart_ws, wsz = ws * ws;
+                    const int w = m / wsz, p = m - w * wsz;
+                    const int py = p / ws, wy = w / d.unpart_nwx;
+                    const int y = wy * ws + py;
+                    const int x = (w - wy * d.unpart_nwx) * ws + (p - py * ws);
 
-            if (vec && n + 3 < d.N) {
-                if (d.cdt == DT_F32) {
-                    f32x4 o = v4;
-
-                    if (d.R)
-                        o += *(const f32x4 *)((const float *)d.R + ridx);
-                    *(f32x4 *)((float *)d.C + idx) = o;
+                    keep = keep && y < d.unpart_H && x < d.unpart_H;
+                    crow = (long)y * d.unpart_H + x;
                 }
-                else {
-                    f32x4 o = v4;
-                    uint2 pk;
+                if (!keep)
+                    continue;
+                const f32x4 v4 = *(const f32x4 *)&E[row * LD + col];
+                const long idx = d.coff + crow * d.ldc + n;
+                const long ridx = d.roff + crow * d.ldc + n;
 
-                    if (d.R) {
-                        const uint2 rv = *(const uint2 *)((const uint16_t *)d.R + ridx);
+                if (vec && n + 3 < d.N) {
+                    if (F32) {
+                        f32x4 o = v4;
 
-                        o.x += __builtin_bit_cast(float, rv.x << 16);
-                        o.y += __builtin_bit_cast(float, rv.x & 0xffff0000u);
-                        o.z += __builtin_bit_cast(float, rv.y << 16);
-                        o.w += __builtin_bit_cast(float, rv.y & 0xffff0000u);
-                    }
-                    pk.x = pack_bf16x2(o.x, o.y);
-                    pk.y = pack_bf16x2(o.z, o.w);
-                    *(uint2 *)((uint16_t *)d.C + idx) = pk;
-                }
-            }
-            else
-                for (int e = 0; e < 4 && n + e < d.N; e++) {
-                    float v = v4[e];
-
-                    if (d.cdt == DT_F32) {
-                        if (d.R)
-                            v += ((const float *)d.R)[ridx + e];
-                        ((float *)d.C)[idx + e] = v;
+                        if (RES)
+                            o += *(const f32x4 *)((const float *)d.R + ridx);
+                        *(f32x4 *)((float *)d.C + idx) = o;
                     }
                     else {
-                        if (d.R)
-                            v += bf2f(((const uint16_t *)d.R)[ridx + e]);
-                        ((uint16_t *)d.C)[idx + e] = f2bf(v);
+                        f32x4 o = v4;
+                        uint2 pk;
+
+                        if (RES) {
+                            const uint2 rv = *(const uint2 *)((const uint16_t *)d.R + ridx);
+
+                            o.x += __builtin_bit_cast(float, rv.x << 16);
+                            o.y += __builtin_bit_cast(float, rv.x & 0xffff0000u);
+                            o.z += __builtin_bit_cast(float, rv.y << 16);
+                            o.w += __builtin_bit_cast(float, rv.y & 0xffff0000u);
+                        }
+                        pk.x = pack_bf16x2(o.x, o.y);
+                        pk.y = pack_bf16x2(o.z, o.w);
+                        *(uint2 *)((uint16_t *)d.C + idx) = pk;
                     }
                 }
-        }
+                else
+                    for (int e = 0; e < 4 && n + e < d.N; e++) {
+                        float v = v4[e];
+
+                        if (F32) {
+                            if (RES)
+                                v += ((const float *)d.R)[ridx + e];
+                            ((float *)d.C)[idx + e] = v;
+                        }
+                        else {
+                            if (RES)
+                                v += bf2f(((const uint16_t *)d.R)[ridx + e]);
+                            ((uint16_t *)d.C)[idx + e] = f2bf(v);
+                        }
+                    }
+            }
+        };
+        using T_ = std::true_type;
+        using F_ = std::false_type;
+        const bool f32 = d.cdt == DT_F32, res = d.R != nullptr, unp = d.unpart_ws > 0;
+
+        if (f32 && res && unp)
+            store_rows(T_(), T_(), T_());
+        else if (f32 && res)
+            store_rows(T_(), T_(), F_());
+        else if (f32 && unp)
+            store_rows(T_(), F_(), T_());
+        else if (f32)
+            store_rows(T_(), F_(), F_());
+        else if (res && unp)
+            store_rows(F_(), T_(), T_());
+        else if (res)
+            store_rows(F_(), T_(), F_());
+        else if (unp)
+            store_rows(F_(), F_(), T_());
+        else
+            store_rows(F_(), F_(), F_());
         __syncthreads();
     }
 }

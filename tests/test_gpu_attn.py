@@ -193,15 +193,32 @@ def test_vit_attention_small(hip, be, orc, grid, ws, unfused):
                   (grid, ws, unfused, be.precision), got, want) <= TOL[be.precision]
 
 
+_FULL_REGION = {}
+
+
+def _full_region_oracle(orc, ws):
+    """Inputs of the full-size region (72 x 72 grid, width 1024, 16 heads)
+    and the oracle's whole output for them, computed once per ws."""
+    if ws not in _FULL_REGION:
+        grid, E, H = 72, 1024, 16
+        x, n1w, n1b, w, b = block_inputs(7 + ws, grid, E)
+        s = ws if ws else grid
+        table = orc.rope_table(s)
+        want = orc.vit_attention(x, grid, E, H, 64, ws, n1w, n1b, w, b, table,
+                                 cpu=True)
+        _FULL_REGION[ws] = (x, n1w, n1b, w, b, table, want)
+    return _FULL_REGION[ws]
+
+
 @pytest.mark.parametrize("ws", [24, 0])
 def test_vit_attention_full_size(hip, be, orc, ws):
     """72 x 72 grid, width 1024, 16 heads: 9 windows of 576 tokens (ws=24)
-    or global attention over 5184 tokens (ws=0)."""
+    or global attention over 5184 tokens (ws=0). The whole output, every
+    row of every (window, head), against the oracle's attention region
+    (LayerNorm, QKV projection, RoPE, the profile=cpu attention sequence):
+    sam3_model.c:981-1013 end to end at the configs' full size."""
     grid, E, H = 72, 1024, 16
-    x, n1w, n1b, w, b = block_inputs(7 + ws, grid, E)
-    s = ws if ws else grid
-    N = s * s
-    table = orc.rope_table(s)
+    x, n1w, n1b, w, b, table, want = _full_region_oracle(orc, ws)
     blk = hip.VitBlock()
     blk.n1w, blk.n1b = be.upload(n1w), be.upload(n1b)
     blk.qkvw, blk.qkvb = be.upload_weight(w), be.upload(b)
@@ -213,36 +230,19 @@ def test_vit_attention_full_size(hip, be, orc, ws):
         m.m.rope_glob = be.upload(table)
     be.write(m.m.x, 0, x)
     hip.vit_attention(m, blk)
-    rows = grid * grid
-    attn = be.read(m.m.attn, rows * E).reshape(rows, E)
-    xn = orc.layernorm(x, n1w, n1b)
-    xw = orc.window_partition(xn, grid, grid, E, s) if ws else xn
-    if be.precision == "fp32":
-        # QKV projection of sampled rows against LayerNorm + linear; the
-        # attention below starts from the device's qkv.
-        qkv = be.read(m.m.qkv, rows * 3 * E).reshape(rows, 3 * E)
-        pick = np.random.default_rng(0).choice(rows, 64, replace=False)
-        want_qkv = orc.linear(xw[pick], w, b, cpu=True)
-        assert report("qkv rows ws=%d %s" % (ws, be.precision), qkv[pick],
-                      want_qkv) <= TOL[be.precision]
-    else:
-        # The bf16 path packs the operands in the projection's store and
-        # writes no fp32 qkv: the attention starts from the oracle's.
-        qkv = orc.linear(xw, w, b, cpu=True)
-
-    # Attention of sampled (unit, head, rows) from the device's qkv.
-    g = np.random.default_rng(1)
-    nunits = rows // N
-    got, want = [], []
-    for trial in range(3):
-        u, h = int(g.integers(nunits)), int(g.integers(H))
-        qrows = np.sort(g.choice(N, 64, replace=False))
-        unit = qkv[u * N:(u + 1) * N]
-        want.append(oracle_attn_rows(unit, E, h, qrows, table))
-        got.append(attn[u * N + qrows, h * 64:(h + 1) * 64])
-    assert report("attention rows ws=%d %s" % (ws, be.precision),
-                  np.concatenate(got), np.concatenate(want)) <= TOL[be.precision]
+    rows = want.shape[0]
+    got = be.read(m.m.attn, rows * E).reshape(rows, E)
     m.free()
+    assert report("attention region ws=%d %s (all %d rows)" % (ws, be.precision, rows),
+                  got, want) <= TOL[be.precision]
+    # Per (unit, head) as well: no block of the output may hide behind the
+    # average over the whole.
+    s = ws if ws else grid
+    N = s * s
+    worst = max(rel_l2(got[u * N:(u + 1) * N, h * 64:(h + 1) * 64],
+                       want[u * N:(u + 1) * N, h * 64:(h + 1) * 64])
+                for u in range(rows // N) for h in range(H))
+    assert worst <= TOL[be.precision], worst
 
 
 @pytest.mark.parametrize("grid,ws", [(16, 8), (24, 8), (16, 0)])

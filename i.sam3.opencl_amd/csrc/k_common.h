@@ -88,4 +88,24 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+/* Compute units of the current device, queried once per library (256 on
+ * MI355X; 256 when the query fails). Used to size persistent grids and to
+ * pick tile shapes; the host launchers call it. */
+static inline int dev_cu_count(void)
+{
+    static int n;
+
+    if (!n) {
+        int dev = 0, c = 0;
+
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess ||
+            c < 1)
+            c = 256;
+        n = c;
+    }
+    return n;
+}
+
 #endif /* K_COMMON_H */

@@ -18,11 +18,19 @@
  *   out_j = Wo (concat_h sum_t a(j,h,t) v_{t,h}) + bo
  *         = sum_{h,t} a(j,h,t) Y[h,t] + bo,   Y[h,t] = Wo_h v_{t,h},
  *
- * with a the softmax over t per head (exp2 domain). k_i2t_fold builds Wt,
- * bt and Y^T per prompt; k_i2t_fused runs a wave per 32 image tokens:
- * S^T = Wt X^T (64 rows (h, t) x 32 tokens), the grouped softmax in
- * registers, U^T = Y^T A^T (256 channels x 32 tokens), then + bo +
- * residual and the LayerNorm over the 256 channels, written once.
+ * with a the softmax over t per head (exp2 domain). In layer 1 the
+ * position encoding enters the scores only through its projection:
+ *
+ *   score(j, h, t) = keys_j . Wt[h,t] + s k_{t,h} . PQ_{j,h} + bt[h,t],
+ *       PQ_j = Wq PE_j (128 wide, head h = columns 16 h .. 16 h + 15),
+ *
+ * so the kernel reads PQ (bf16, 256 bytes per image token, shared by the
+ * prompts) instead of PE (1 KB per token). k_i2t_fold builds Wt, bt, Y^T
+ * and the compact rows Kc[h,t] = s k_{t,h} (16 wide) per prompt;
+ * k_i2t_fused runs a wave per 32 image tokens: S^T = Wt X^T (+ Kc PQ^T,
+ * block diagonal over the heads; 64 rows (h, t) x 32 tokens), the grouped
+ * softmax in registers, U^T = Y^T A^T (256 channels x 32 tokens), then +
+ * bo + residual and the LayerNorm over the 256 channels, written once.
  *
  * MFMA 32x32x16 bf16 lane layouts (l = lane, hh = l / 32): A operand lane
  * l holds A[l % 32][8 hh .. 8 hh + 7 of the k step]; B operand B[same k
@@ -54,7 +62,9 @@ __device__ __forceinline__ int yt_row(int kappa)
  * of the image -> token attention), Wq [128][256] (layer 1) with bias bq,
  * Wo [256][128]. Writes Wt16 [P][64][K] (bf16), bt [P][64] (when bq is
  * given), YT16 [P][256][64] (bf16, columns in yt_row order; when Wo is
- * given). Row r of Wt is (h, t) = (r / 8, r % 8). The token -> image
+ * given) and, in layer 1 when Kc16 is given, Kc16 [P][64][16] (bf16, row
+ * (h, t) = s k_{t,h}: the factor of the projected position encoding's
+ * score term). Row r of Wt is (h, t) = (r / 8, r % 8). The token -> image
  * attention uses the same fold for its queries (sk = projected queries,
  * Wq = the key projection, no bq or Wo). */
 __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
@@ -66,7 +76,8 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
                                                   float s,
                                                   uint16_t *__restrict__ Wt16,
                                                   float *__restrict__ bt,
-                                                  uint16_t *__restrict__ YT16)
+                                                  uint16_t *__restrict__ YT16,
+                                                  uint16_t *__restrict__ Kc16)
 {
     /* Workgroup (p, h): head h's 16 columns of the 8 tokens' keys and
      * values, rows 8 h .. 8 h + 7 of Wt and bt, those columns of Y^T. */
@@ -103,6 +114,9 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
                 acc = fmaf(ks[t][c], bq[16 * h + c], acc);
             bt[p * FOLD_ROWS + 8 * h + t] = s * acc;
         }
+        if (Kc16 && t < 128)
+            Kc16[((long)p * FOLD_ROWS + 8 * h + t / 16) * 16 + t % 16] =
+                f2bf(s * ks[t / 16][t % 16]);
     }
     else {
         /* Block diagonal: row (h, tk) holds s k_{tk,h} on columns 16 h ..
@@ -137,14 +151,14 @@ __global__ __launch_bounds__(256) void k_i2t_fold(const float *__restrict__ sk,
 extern "C" int launch_i2t_fold(const float *sk, const float *sv, int layer,
                                const void *Wq, int wq_dt, const float *bq,
                                const void *Wo, int wo_dt, float s, int P,
-                               void *Wt16, float *bt, void *YT16,
+                               void *Wt16, float *bt, void *YT16, void *Kc16,
                                void *stream)
 {
-    if (P < 1 || (layer && !Wq) || (!layer && !Wo))
+    if (P < 1 || (layer && !Wq) || (!layer && !Wo) || (!layer && Kc16))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_i2t_fold, dim3(P, 8), dim3(256), 0, (hipStream_t)stream,
                        sk, sv, layer, Wq, wq_dt, bq, Wo, wo_dt, s,
-                       (uint16_t *)Wt16, bt, (uint16_t *)YT16);
+                       (uint16_t *)Wt16, bt, (uint16_t *)YT16, (uint16_t *)Kc16);
     return hipGetLastError();
 }
 
@@ -159,18 +173,54 @@ __device__ __forceinline__ unsigned swz_off(int row, int chunk, int rowbytes)
     return (unsigned)(row * rowbytes + 16 * ((chunk ^ sw) & (nch - 1)));
 }
 
-/* Workgroup = 4 waves = 128 image tokens of one prompt; items in
- * XCD-contiguous order, blocked as described at the item decode. X rows of K floats (per-prompt
- * stride xs, 0 = shared), plus PE rows when pe != NULL; residual R
- * (stride rs, 0 = shared); out [P][T][256] may alias R. */
-/* RX: the residual R is the input X itself (layer 1: R = keys, X = keys +
- * PE added on load). The S^T loop then drops each token's loaded keys
- * into the output accumulators U^T in their channel layout (an exchange
- * with lane l ^ 32 per step), so the U^T product adds onto the residual and
- * the keys are read from HBM once instead of twice. */
+/* Work split of the (prompt, 128-token chunk) items over the 8 XCDs
+ * (workgroup b runs on XCD b % 8): XCD x owns prompts [x P / 8, (x + 1) P
+ * / 8) with all C chunks when P >= 8, else all prompts with chunks [x C /
+ * 8, (x + 1) C / 8): pa, np (first prompt, count), ca, nc (first chunk,
+ * count). */
+#ifndef I2T_WAVES
+#define I2T_WAVES 4
+#endif
+#ifndef I2T_BLOCK
+#define I2T_BLOCK 8
+#endif
+#define I2T_TOK (32 * I2T_WAVES)
+__device__ __forceinline__ void i2t_region(int P, int C, int x, int &pa, int &np, int &ca,
+                                           int &nc)
+{
+    if (P >= 8) {
+        pa = x * P / 8;
+        np = (x + 1) * P / 8 - pa;
+        ca = 0;
+        nc = C;
+    }
+    else {
+        pa = 0;
+        np = P;
+        ca = x * C / 8;
+        nc = (x + 1) * C / 8 - ca;
+    }
+}
+
+/* Workgroup = 8 waves = 256 image tokens of one prompt (one workgroup
+ * per CU): workgroup b takes item b / 8 of XCD b % 8's region
+ * (i2t_region), chunk-major, prompt fastest, so the workgroups in flight
+ * on an XCD cover a few chunks of each of its prompts: a prompt's fold
+ * (Wt, Y^T; 256 tokens per fetch of it) stays in that XCD's L2 between
+ * uses, and the rows the prompts share (PQ in layer 1, qp0 and src in
+ * layer 0) of a chunk are read by all of them at nearly the same time. X
+ * rows of K floats (per-prompt stride xs, 0 = shared); residual R (stride
+ * rs, 0 = shared); out [P][T][256] may alias R. */
+/* RX (layer 1): the residual R is the input X itself (the keys), and the
+ * scores take the position term Kc PQ^T (pq [T][128] bf16, kc [P][64][16]
+ * bf16). The S^T loop drops each token's loaded keys into the output
+ * accumulators U^T in their channel layout (an exchange with lane l ^ 32
+ * per step), so the U^T product adds onto the residual and the keys are
+ * read from HBM once. */
 template <int K, bool RX>
-__global__ __launch_bounds__(256, 2) void k_i2t_fused(
-    const float *X, long xs, const float *__restrict__ pe,
+__global__ __launch_bounds__(64 * I2T_WAVES, 8 / I2T_WAVES) void k_i2t_fused(
+    const float *X, long xs, const uint16_t *__restrict__ pq,
+    const uint16_t *__restrict__ kc,
     const uint16_t *__restrict__ Wt16, const float *__restrict__ bt,
     const uint16_t *__restrict__ YT16, const float *__restrict__ bo,
     const float *R, long rs, const float *__restrict__ g,
@@ -181,31 +231,30 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     __shared__ float bts[FOLD_ROWS];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
               l32 = l & 31;
-    const int chunks = (T + 127) / 128;
-    const unsigned total = (unsigned)P * chunks, per_xcd = (total + 7) / 8;
-    const unsigned item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    int pa, np, ca, nc;
 
-    if (item >= total)
+    i2t_region(P, (T + I2T_TOK - 1) / I2T_TOK, (int)(blockIdx.x % 8), pa, np, ca, nc);
+    const unsigned it = blockIdx.x / 8;
+
+    if (it >= (unsigned)np * (unsigned)nc)
         return;
-    /* Blocks of 8 token chunks, prompt next, chunk fastest: one XCD's
-     * workgroups take 8 chunks of a prompt (its Wt / Y^T reused from L2),
-     * then the same 8 chunks of the next prompt (the rows shared by the
-     * prompts, PE or qp0 and src, reused from L2). */
-    const unsigned cb = item / (8u * P), rem = item - cb * 8u * P;
-    const unsigned nin = chunks - 8 * cb < 8 ? chunks - 8 * cb : 8;
-    const int p = (int)(rem / nin), ch0 = (int)(8 * cb + rem % nin) * 128;
+    /* Blocks of I2T_BLOCK chunks x the region's prompts, chunk fastest. */
+    const unsigned blk = it / (I2T_BLOCK * (unsigned)np), r = it % (I2T_BLOCK * (unsigned)np);
+    const unsigned nb = (unsigned)nc - I2T_BLOCK * blk < I2T_BLOCK ? (unsigned)nc - I2T_BLOCK * blk
+                                                                   : I2T_BLOCK;
+    const int p = pa + (int)(r / nb), ch0 = I2T_TOK * (ca + (int)(I2T_BLOCK * blk + r % nb));
 
     /* Stage the prompt's Wt (64 x K) and Y^T (256 x 64) in LDS. */
     {
         const uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
         const uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS;
 
-        for (int i = tid; i < FOLD_ROWS * K / 8; i += 256) {
+        for (int i = tid; i < FOLD_ROWS * K / 8; i += 64 * I2T_WAVES) {
             const int row = i / (K / 8), c = i % (K / 8);
 
             *(u32x4 *)(Ws + swz_off(row, c, 2 * K)) = *(const u32x4 *)(wt + 8 * i);
         }
-        for (int i = tid; i < 256 * FOLD_ROWS / 8; i += 256) {
+        for (int i = tid; i < 256 * FOLD_ROWS / 8; i += 64 * I2T_WAVES) {
             const int row = i / 8, c = i % 8;
 
             *(u32x4 *)(Ys + swz_off(row, c, 2 * FOLD_ROWS)) = *(const u32x4 *)(yt + 8 * i);
@@ -218,7 +267,6 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     const int j = ch0 + 32 * w + l32;
     const bool valid = j < T;
     const float *xr = X + (long)p * xs + (long)(valid ? j : 0) * K;
-    const float *per = pe ? pe + (long)(valid ? j : 0) * K : nullptr;
     f32x16 s0 = {}, s1 = {};
     /* U^T accumulators (8 tiles of 32 channels x 32 tokens): register r of
      * tile c is channel 32 c + 8 (r / 4) + 4 hh + r % 4 of token l32. With
@@ -227,6 +275,28 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
 
     for (int c = 0; c < 8; c++)
         u[c] = (f32x16){};
+
+    if constexpr (RX) {
+        /* S^T = Kc PQ^T first (while U^T holds nothing), one k step per
+         * head: step i of tile T_ contracts head 4 T_ + i's 16 columns of
+         * PQ (B operand: 8 of them for the lane's token), against A rows
+         * (h, t) that are s k_{t,h} where h is that head and zero for the
+         * other heads (rows 8 i .. 8 i + 7 of the tile, lanes l32 / 8 ==
+         * i). */
+        const uint16_t *pr = pq + (long)(valid ? j : 0) * 128 + 8 * hh;
+        const bf16x8 k0 = *(const bf16x8 *)(kc + ((long)p * FOLD_ROWS + l32) * 16 + 8 * hh);
+        const bf16x8 k1 = *(const bf16x8 *)(kc + ((long)p * FOLD_ROWS + 32 + l32) * 16 + 8 * hh);
+        const bf16x8 zero = {};
+
+        for (int i = 0; i < 4; i++) {
+            const bf16x8 b0 = *(const bf16x8 *)(pr + 16 * i);
+            const bf16x8 b1 = *(const bf16x8 *)(pr + 64 + 16 * i);
+            const bool mine = (l32 >> 3) == i;
+
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mine ? k0 : zero, b0, s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(mine ? k1 : zero, b1, s1, 0, 0, 0);
+        }
+    }
 
     /* S^T = Wt X^T over K / 16 steps; the lane's B operand is 8
      * consecutive inputs of its token, converted to bf16. */
@@ -252,12 +322,6 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
                 u[st / 2][8 * (st & 1) + 4 + e] = hi[e];
             }
         }
-        if (per) {
-            const f32x4 p0 = *(const f32x4 *)(per + c0), p1 = *(const f32x4 *)(per + c0 + 4);
-
-            a0 += p0;
-            a1 += p1;
-        }
         for (int e = 0; e < 4; e++) {
             bx[e] = (__bf16)a0[e];
             bx[4 + e] = (__bf16)a1[e];
@@ -268,10 +332,6 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, bx, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, bx, s1, 0, 0, 0);
     }
-
-    /* Every wave's reads of Wt are done past this point: the epilogue
-     * reuses its LDS for staging. */
-    __syncthreads();
 
     /* Grouped softmax: register r of tile T_ is row 32 T_ + 8 (r / 4) +
      * 4 hh + r % 4, i.e. head 4 T_ + r / 4 and prompt token 4 hh + r % 4:
@@ -315,17 +375,18 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     }
 
     /* Epilogue through a per-wave [32 tokens][32 channels] fp32 staging
-     * tile in the (now free) Wt area, so that the residual is read and the
-     * output written as whole 128-byte row segments: in the coalesced
-     * phase lane L takes token 8 k + L / 8, 16-byte chunk L % 8 of the
-     * tile; chunk c of staging row r sits at c ^ (r & 7). Register r of
-     * U^T tile c is channel 32 c + 8 (r / 4) + 4 hh + r % 4, i.e. chunk
-     * 2 (r / 4) + hh of the tile's row l32. The barrier after the S^T
-     * product guarantees every wave is done reading Wt. */
+     * tile in the Y^T area (free once every wave's U^T product is done:
+     * the barrier), so that the residual is read and the output written
+     * as whole 128-byte row segments: in the coalesced phase lane L takes
+     * token 8 k + L / 8, 16-byte chunk L % 8 of the tile; chunk c of
+     * staging row r sits at c ^ (r & 7). Register r of U^T tile c is
+     * channel 32 c + 8 (r / 4) + 4 hh + r % 4, i.e. chunk 2 (r / 4) + hh
+     * of the tile's row l32. */
+    __syncthreads();
     /* Nothing of the epilogue is scheduled into the products above (its
      * loads would stay live across them and spill). */
     __builtin_amdgcn_sched_barrier(0);
-    char *stg = Ws + 4096 * w;
+    char *stg = Ys + 4096 * w;
     const int j0 = ch0 + 32 * w;
     const float *rbase = R + (long)p * rs;
 
@@ -399,37 +460,40 @@ __global__ __launch_bounds__(256, 2) void k_i2t_fused(
     }
 }
 
-extern "C" int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
-                                const void *Wt16, const float *bt,
+extern "C" int launch_i2t_fused(const float *X, long xs, int K, const void *pq16,
+                                const void *Kc16, const void *Wt16, const float *bt,
                                 const void *YT16, const float *bo,
                                 const float *R, long rs, const float *g,
                                 const float *b, float *out, int T, int P,
                                 float eps, void *stream)
 {
-    const long items = (long)P * ((T + 127) / 128);
-    const long grid = (items + 7) / 8 * 8;
+    const long C = T > 0 ? (T + I2T_TOK - 1) / I2T_TOK : 0;
+    /* 8 x the largest region (ceil(P / 8) C or P ceil(C / 8) items of 256
+     * tokens; 64-bit, so that sizes past the grid limit are refused rather
+     * than wrapped). */
+    const long grid = P < 1 ? 0 : 8L * (P >= 8 ? (P + 7L) / 8 * C : P * ((C + 7) / 8));
+    /* K = 256 is layer 1 (residual = input, position term); K = 128 is
+     * layer 0 (shared image queries, separate residual, no position
+     * term). */
+    const bool l1 = K == 256;
 
     if (P < 1 || T < 1 || grid > 0x7fffffffL || (K != 128 && K != 256) ||
-        ((xs | rs) & 3) ||
-        (((uintptr_t)X | (uintptr_t)R | (uintptr_t)out | (uintptr_t)bo |
-          (uintptr_t)g | (uintptr_t)b | (uintptr_t)(pe ? pe : X) |
-          (uintptr_t)Wt16 | (uintptr_t)YT16) & 15))
+        ((xs | rs) & 3) || (l1 && (R != X || rs != xs || !pq16 || !Kc16)) ||
+        (!l1 && (pq16 || Kc16)) ||
+        (((uintptr_t)X | (uintptr_t)R | (uintptr_t)out | (uintptr_t)bo | (uintptr_t)bt |
+          (uintptr_t)g | (uintptr_t)b | (uintptr_t)(l1 ? pq16 : X) |
+          (uintptr_t)(l1 ? Kc16 : X) | (uintptr_t)Wt16 | (uintptr_t)YT16) & 15))
         return hipErrorInvalidValue;
-    if (K == 256 && R == X && rs == xs)
-        hipLaunchKernelGGL((k_i2t_fused<256, true>), dim3((unsigned)grid), dim3(256), 0,
-                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
-                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
-                           eps);
-    else if (K == 256)
-        hipLaunchKernelGGL((k_i2t_fused<256, false>), dim3((unsigned)grid), dim3(256), 0,
-                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
-                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
-                           eps);
+    if (l1)
+        hipLaunchKernelGGL((k_i2t_fused<256, true>), dim3((unsigned)grid), dim3(64 * I2T_WAVES), 0,
+                           (hipStream_t)stream, X, xs, (const uint16_t *)pq16,
+                           (const uint16_t *)Kc16, (const uint16_t *)Wt16, bt,
+                           (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P, eps);
     else
-        hipLaunchKernelGGL((k_i2t_fused<128, false>), dim3((unsigned)grid), dim3(256), 0,
-                           (hipStream_t)stream, X, xs, pe, (const uint16_t *)Wt16,
-                           bt, (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P,
-                           eps);
+        hipLaunchKernelGGL((k_i2t_fused<128, false>), dim3((unsigned)grid), dim3(64 * I2T_WAVES), 0,
+                           (hipStream_t)stream, X, xs, nullptr, nullptr,
+                           (const uint16_t *)Wt16, bt, (const uint16_t *)YT16, bo, R,
+                           rs, g, b, out, T, P, eps);
     return hipGetLastError();
 }
 
@@ -761,17 +825,20 @@ extern "C" int launch_upscale_fused(const float *keys, const void *W1T16,
 /* ------------------------------------------------------------------ */
 
 /* For prompt p, head h, prompt token i (row r = 8 h + i):
- *   score(r, j) = s q_{i,h} . (Wk_h kin_j + bk_h) = U[r] . kin_j + const(r),
+ *   score(r, j) = s q_{i,h} . (Wk_h (keys_j + PE_j) + bk_h)
+ *               = U[r] . keys_j + Qc[r] . PK_{j,h} + const(r),
  *   U[r] = s Wk_h^T q_{i,h} (k_i2t_fold on the projected queries),
- *   o_{i,h} = Wv_h (sum_j a(r, j) keys_j) + bv_h = Wv_h Z[r] + bv_h,
- * with kin_j = keys_j + PE_j formed on the fly; the constant drops out of
- * the softmax. k_t2i_fused: workgroup = (prompt, key split), 4 waves =
- * 2 row tiles x 2 key streams; per 64-key block the workgroup stages Kin
- * [64 keys][256] and keys^T [256][64 keys] in LDS as bf16, and each wave
- * does S^T = Kin U^T (32 keys x 32 rows, rows = lanes), the online
- * softmax, and Z^T += keys^T P^T (256 x 32). The two streams of a row
- * tile merge through LDS; each split leaves (Z, m, l) partials for
- * k_t2i_merge; k_t2i_unfold applies Wv and bv. */
+ *   Qc[r] = s q_{i,h} (16 wide), PK_j = Wk PE_j (128 wide, per image),
+ *   o_{i,h} = Wv_h (sum_j a(r, j) keys_j) + bv_h = Wv_h Z[r] + bv_h;
+ * the constant drops out of the softmax. k_t2i_fused: workgroup =
+ * (prompt, key split), 4 waves = 2 row tiles x 2 key streams; per 64-key
+ * block the workgroup stages keys [64 keys][256] and keys^T [256][64
+ * keys] in LDS as bf16, and each wave does S^T = keys U^T + PK Qc^T (32
+ * keys x 32 rows, rows = lanes; PK straight from global memory, 256 bytes
+ * per key instead of PE's 1 KB), the online softmax, and Z^T += keys^T
+ * P^T (256 x 32). The two streams of a row tile merge through LDS; each
+ * split leaves (Z, m, l) partials for k_t2i_merge; k_t2i_unfold applies
+ * Wv and bv. */
 
 /* Byte offset of keys^T element (dim d, key k) in a [256][64] bf16 tile:
  * rows of 128 B, 16-byte chunk k / 8 at chunk (k / 8) ^ ((d >> 1) & 7). */
@@ -781,23 +848,26 @@ __device__ __forceinline__ unsigned vt_off(int d, int k)
 }
 
 __global__ __launch_bounds__(256, 2) void k_t2i_fused(
-    const float *__restrict__ keys, const float *__restrict__ pe,
-    const uint16_t *__restrict__ U16, float *__restrict__ part, int T,
-    int P, int nsplit)
+    const float *__restrict__ keys, const uint16_t *__restrict__ pk,
+    const uint16_t *__restrict__ U16, const uint16_t *__restrict__ Qc16,
+    float *__restrict__ part, int T, int P, int nsplit)
 {
     __shared__ __attribute__((aligned(16))) char Ks[64 * 512];
     __shared__ __attribute__((aligned(16))) char Vs[256 * 128];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
               l32 = l & 31;
     const int rt = w & 1, kh = w >> 1;
-    /* XCD-contiguous items, prompt fastest: one XCD's workgroups take the
-     * same key range for consecutive prompts and share its PE rows in L2. */
+    /* XCD-contiguous items, split fastest: one XCD's workgroups take
+     * whole prompts (1/8 of them), so the U rows each block re-reads stay
+     * in that XCD's L2 (a few prompts' worth), and the shared PK rows
+     * (256 bytes a key) of a split are read by the XCD's prompts
+     * together. */
     const unsigned total = (unsigned)P * nsplit, per_xcd = (total + 7) / 8;
     const unsigned item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
 
     if (item >= total)
         return;
-    const int p = (int)(item % (unsigned)P), sp = (int)(item / (unsigned)P);
+    const int p = (int)(item / (unsigned)nsplit), sp = (int)(item % (unsigned)nsplit);
     const int nblk = (T + 63) / 64;
     const int kb0 = sp * nblk / nsplit, kb1 = (sp + 1) * nblk / nsplit;
     const float *kp = keys + (long)p * T * 256;
@@ -810,36 +880,49 @@ __global__ __launch_bounds__(256, 2) void k_t2i_fused(
         z[dt] = (f32x16){};
     float m = -INFINITY, lsum = 0.0f;
     const int krow = 32 * kh + ((l32 & ~12) | ((l32 & 4) << 1) | ((l32 & 8) >> 1));
+    /* Qc^T B operands (8 of the 16 values of the lane's row) and whether
+     * the row's head is that of k step i (head 4 rt + i): l32 / 8 == i. */
+    const bf16x8 qc = *(const bf16x8 *)(Qc16 + ((long)p * FOLD_ROWS + row) * 16 + 8 * hh);
+    const int qstep = l32 >> 3;
 
     for (int kb = kb0; kb < kb1; kb++) {
+        /* PK A operands of this wave's 32 keys (kperm order) on the row
+         * tile's four heads; rows past T read row T - 1 (their scores are
+         * masked below). Issued before the staging so the loads overlap
+         * it. */
+        bf16x8 pka[4];
+        {
+            const int key = kb * 64 + krow;
+            const uint16_t *pr = pk + (long)(key < T ? key : T - 1) * 128 + 64 * rt + 8 * hh;
+
+            for (int i = 0; i < 4; i++)
+                pka[i] = *(const bf16x8 *)(pr + 16 * i);
+        }
         /* Stage: task = (8-dim chunk c, key pair) with c fastest, so a
          * wave reads two contiguous 1 KB rows; keys past T are zero. */
         for (int task = tid; task < 32 * 32; task += 256) {
             const int c = task & 31, k0 = 2 * (task >> 5);
-            f32x4 a[2][2], b[2][2];
+            f32x4 a[2][2];
 
             for (int e = 0; e < 2; e++) {
                 const int key = kb * 64 + k0 + e;
 
                 if (key < T) {
                     const float *kr = kp + (long)key * 256 + 8 * c;
-                    const float *pr = pe + (long)key * 256 + 8 * c;
 
                     a[e][0] = *(const f32x4 *)kr;
                     a[e][1] = *(const f32x4 *)(kr + 4);
-                    b[e][0] = *(const f32x4 *)pr;
-                    b[e][1] = *(const f32x4 *)(pr + 4);
                 }
                 else {
-                    a[e][0] = a[e][1] = b[e][0] = b[e][1] = (f32x4){};
+                    a[e][0] = a[e][1] = (f32x4){};
                 }
             }
             for (int e = 0; e < 2; e++) {
                 bf16x8 kin;
 
                 for (int i = 0; i < 4; i++) {
-                    kin[i] = (__bf16)(a[e][0][i] + b[e][0][i]);
-                    kin[4 + i] = (__bf16)(a[e][1][i] + b[e][1][i]);
+                    kin[i] = (__bf16)a[e][0][i];
+                    kin[4 + i] = (__bf16)a[e][1][i];
                 }
                 *(bf16x8 *)(Ks + swz_off(k0 + e, c, 512)) = kin;
             }
@@ -863,6 +946,13 @@ __global__ __launch_bounds__(256, 2) void k_t2i_fused(
             const bf16x8 ub = *(const bf16x8 *)(ur + 16 * st);
 
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, ub, sc, 0, 0, 0);
+        }
+        {
+            const bf16x8 zero = {};
+
+            for (int i = 0; i < 4; i++)
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pka[i], qstep == i ? qc : zero,
+                                                            sc, 0, 0, 0);
         }
         /* Register r of lane half hh is key 32 kh + 16 (r / 8) + 8 hh + r % 8. */
         for (int r = 0; r < 16; r++) {
@@ -1011,22 +1101,24 @@ __global__ __launch_bounds__(128) void k_t2i_unfold(const float *__restrict__ Z,
     o[((long)p * 8 + i) * 128 + 16 * h + c] = acc;
 }
 
-extern "C" int launch_t2i_fused(const float *keys, const float *pe,
-                                const void *U16, float *part, float *Z,
-                                const void *Wv, int wv_dt, const float *bv,
-                                float *o, int T, int P, int nsplit,
-                                void *stream)
+extern "C" int launch_t2i_fused(const float *keys, const void *pk16,
+                                const void *U16, const void *Qc16, float *part,
+                                float *Z, const void *Wv, int wv_dt,
+                                const float *bv, float *o, int T, int P,
+                                int nsplit, void *stream)
 {
     const int nblk = (T + 63) / 64;
     const long n = (long)P * FOLD_ROWS * 256;
 
     if (P < 1 || T < 1 || nsplit < 1 || nsplit > nblk ||
-        (long)P * nsplit > 0x7fffffffL ||
-        (((uintptr_t)keys | (uintptr_t)pe | (uintptr_t)U16 | (uintptr_t)part) & 15))
+        (long)P * nsplit > 0x7fffffffL || !pk16 || !Qc16 ||
+        (((uintptr_t)keys | (uintptr_t)pk16 | (uintptr_t)U16 | (uintptr_t)Qc16 |
+          (uintptr_t)part) & 15))
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_t2i_fused, dim3((unsigned)((P * nsplit + 7) / 8 * 8)),
-                       dim3(256), 0, (hipStream_t)stream, keys, pe,
-                       (const uint16_t *)U16, part, T, P, nsplit);
+                       dim3(256), 0, (hipStream_t)stream, keys,
+                       (const uint16_t *)pk16, (const uint16_t *)U16,
+                       (const uint16_t *)Qc16, part, T, P, nsplit);
     hipLaunchKernelGGL(k_t2i_merge, dim3((unsigned)((n + 255) / 256)), dim3(256),
                        0, (hipStream_t)stream, part, Z, P, nsplit);
     hipLaunchKernelGGL(k_t2i_unfold, dim3(P, 8), dim3(128), 0, (hipStream_t)stream,

@@ -453,21 +453,6 @@ k_gemm_nt(gemm_desc d)
     }
 }
 
-static int cu_count(void)
-{
-    static int n;
-
-    if (!n) {
-        int dev = 0;
-
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
-                                  dev) != hipSuccess || n < 1)
-            n = 256;
-    }
-    return n;
-}
-
 /* The NT kernel applies to unbatched bf16 x bf16 (weights as [N][K])
  * products with K a multiple of 64 and 16-byte aligned rows. */
 extern "C" int gemm_nt_ok(const gemm_desc *d)
@@ -503,10 +488,10 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
      * (K = 4096); everywhere else they are slower. */
     t256 = (long)((d->M + 255) / 256) * ((d->N + 255) / 256);
     /* The packed-operand store exists for 128 x 128 tiles only. */
-    bm = t256 >= cu_count() * 9 / 10 && d->K >= 2048 && d->pack_N == 0 ? 256 : 128;
+    bm = t256 >= dev_cu_count() * 9 / 10 && d->K >= 2048 && d->pack_N == 0 ? 256 : 128;
     bn = bm;
     if (bm == 128 && d->pack_N == 0 &&
-        (long)((d->M + 127) / 128) * ((d->N + 127) / 128) < 2L * cu_count())
+        (long)((d->M + 127) / 128) * ((d->N + 127) / 128) < 2L * dev_cu_count())
         bn = 64;
     {
         const long tiles = (long)((d->M + bm - 1) / bm) * ((d->N + bn - 1) / bn);

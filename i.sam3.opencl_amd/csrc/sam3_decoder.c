@@ -113,6 +113,14 @@ void sam_dec_init(struct sam_model *m, struct sam_decoder *d, int batch)
         d->t2i_part = dalloc(m, (2L * m->hip->cu_count + P) * 64 * 258,
                              "token -> image partials");
         d->t2i_z = dalloc(m, P * 64 * SAM_DIM, "token -> image key sums");
+        d->fold_c = hipb_alloc_typed(m->hip, P * 64 * 16, HIPB_BF16,
+                                     "folded token rows");
+        d->pe_q1 = hipb_alloc_typed(m->hip, T * 128, HIPB_BF16,
+                                    "PE image-query projection");
+        d->pe_k1 = hipb_alloc_typed(m->hip, T * 128, HIPB_BF16,
+                                    "PE key projection");
+        d->pe_kf = hipb_alloc_typed(m->hip, T * 128, HIPB_BF16,
+                                    "PE final key projection");
     }
 }
 
@@ -139,7 +147,8 @@ void sam_dec_free(struct sam_model *m)
                         &d->bk, &d->bv, &d->bo, &d->u1, &d->g2, &d->u2,
                         &d->hyper, &d->lowres, &d->mask, &d->sel, &d->stats,
                         &d->fold_w, &d->fold_b, &d->fold_y, &d->up_w1t,
-                        &d->up_w2t, &d->t2i_part, &d->t2i_z};
+                        &d->up_w2t, &d->t2i_part, &d->t2i_z, &d->fold_c,
+                        &d->pe_q1, &d->pe_k1, &d->pe_kf};
 
     if (m->hip)
         hipb_finish(m->hip);
@@ -182,6 +191,19 @@ void sam_dec_prepare(struct sam_model *m)
            0, ACT_NONE, 0);
     linear(m, (int)T, SAM_DIM, 128, d->srcpe, 0, L0->i2t.qw, L0->i2t.qb,
            d->qp0, 0, ACT_NONE, 0);
+    if (d->fold_w) {
+        /* The position term of the fused layer-1 and final blocks: PE
+         * through the projections that meet it there, without their
+         * biases (the fused blocks add those through the folds). */
+        const struct sam_dec_layer *L1 = &d->layers[1];
+
+        linear(m, (int)T, SAM_DIM, 128, d->pe_img, 0, L1->i2t.qw, NULL,
+               d->pe_q1, 0, ACT_NONE, 0);
+        linear(m, (int)T, SAM_DIM, 128, d->pe_img, 0, L1->t2i.kw, NULL,
+               d->pe_k1, 0, ACT_NONE, 0);
+        linear(m, (int)T, SAM_DIM, 128, d->pe_img, 0, d->final_t2i.kw, NULL,
+               d->pe_kf, 0, ACT_NONE, 0);
+    }
     hipb_finish(m->hip);
     hipb_release(&nm);
 }
@@ -208,7 +230,18 @@ void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a)
         struct hipb_backend *be = m->hip;
         const int nblk = (int)((T + 63) / 64);
         int nsplit = (2 * be->cu_count + P - 1) / P, err;
+        /* The position term needs PE through this block's key projection,
+         * cached per image for the two blocks that attend to per-prompt
+         * keys. */
+        const hipb_mem pk = a == &d->layers[1].t2i ? d->pe_k1
+                            : a == &d->final_t2i   ? d->pe_kf
+                                                   : NULL;
 
+        if (!pk) {
+            hipb_fatal("t2i_attention: precision=bf16 runs the layer-1 and "
+                       "final token -> image blocks only");
+            return;
+        }
         if (nsplit > nblk)
             nsplit = nblk;
 
@@ -220,13 +253,15 @@ void t2i_attention(struct sam_model *m, int P, const struct sam_attn_w *a)
         err = launch_i2t_fold(d->sq->ptr, NULL, 1, a->kw->ptr, a->kw->dtype,
                               NULL, NULL, 0,
                               1.4426950408889634f / sqrtf(16.0f), P,
-                              d->fold_w->ptr, NULL, NULL, be->stream);
+                              d->fold_w->ptr, NULL, NULL, d->fold_c->ptr,
+                              be->stream);
         hipb_run_end(be, err, "t2i_fold", 0.0);
         hipb_run_begin(be);
-        err = launch_t2i_fused(d->keys->ptr, d->pe_img->ptr, d->fold_w->ptr,
-                               d->t2i_part->ptr, d->t2i_z->ptr, a->vw->ptr,
-                               a->vw->dtype, a->vb->ptr, d->so->ptr, (int)T, P,
-                               nsplit, be->stream);
+        err = launch_t2i_fused(d->keys->ptr, pk->ptr, d->fold_w->ptr,
+                               d->fold_c->ptr, d->t2i_part->ptr,
+                               d->t2i_z->ptr, a->vw->ptr, a->vw->dtype,
+                               a->vb->ptr, d->so->ptr, (int)T, P, nsplit,
+                               be->stream);
         hipb_run_end(be, err, "t2i_fused", 4.0 * P * 64.0 * T * SAM_DIM);
         linear(m, P * NTOK, 128, SAM_DIM, d->so, 0, a->ow, a->ob, d->qry, 0,
                ACT_NONE, 1);
@@ -280,12 +315,13 @@ void i2t_attention(struct sam_model *m, int layer, int P)
                               L->i2t.qw->dtype, layer ? L->i2t.qb->ptr : NULL,
                               L->i2t.ow->ptr, L->i2t.ow->dtype, s, P,
                               d->fold_w->ptr, d->fold_b->ptr, d->fold_y->ptr,
-                              be->stream);
+                              layer ? d->fold_c->ptr : NULL, be->stream);
         hipb_run_end(be, err, "i2t_fold", 0.0);
         hipb_run_begin(be);
         err = launch_i2t_fused(layer ? d->keys->ptr : d->qp0->ptr,
                                layer ? T * SAM_DIM : 0, layer ? 256 : 128,
-                               layer ? d->pe_img->ptr : NULL, d->fold_w->ptr,
+                               layer ? d->pe_q1->ptr : NULL,
+                               layer ? d->fold_c->ptr : NULL, d->fold_w->ptr,
                                d->fold_b->ptr, d->fold_y->ptr, L->i2t.ob->ptr,
                                layer ? d->keys->ptr : d->src->ptr,
                                layer ? T * SAM_DIM : 0, L->n4w->ptr,

@@ -220,19 +220,24 @@ int launch_pth_convert(const void *src, int sdt, void *dst, int ddt,
  * builds Wt16 [P][64][K] (bf16), bt [P][64] and YT16 [P][256][64] from
  * the token keys / values sk, sv [P][8][128], the image-query projection
  * Wq [128][256] + bq (layer 1; NULL in layer 0, K = 128) and the output
- * projection Wo [256][128]; s = log2(e) / sqrt(head width). */
+ * projection Wo [256][128]; s = log2(e) / sqrt(head width). In layer 1
+ * Kc16 (optional) receives the compact rows s k_{t,h}, [P][64][16] bf16. */
 int launch_i2t_fold(const float *sk, const float *sv, int layer,
                     const void *Wq, int wq_dt, const float *bq,
                     const void *Wo, int wo_dt, float s, int P, void *Wt16,
-                    float *bt, void *YT16, void *stream);
-/* out [P][T][256] = LayerNorm(R + bo + attention of X (+ pe) over the
- * folded prompt tokens); X rows of K floats with per-prompt stride xs,
- * R with stride rs (0 = shared); out may alias R. */
-int launch_i2t_fused(const float *X, long xs, int K, const float *pe,
-                     const void *Wt16, const float *bt, const void *YT16,
-                     const float *bo, const float *R, long rs, const float *g,
-                     const float *b, float *out, int T, int P, float eps,
-                     void *stream);
+                    float *bt, void *YT16, void *Kc16, void *stream);
+/* out [P][T][256] = LayerNorm(R + bo + attention of X over the folded
+ * prompt tokens). K = 256 (layer 1): X = R = the keys (xs == rs), whose
+ * image queries are keys + PE: the PE part enters as pq16 [T][128] bf16
+ * (PE through the image-query projection, no bias) against Kc16 (the
+ * fold's compact rows). K = 128 (layer 0): X = the shared projected image
+ * queries (xs = 0), R with stride rs (0 = shared), pq16 = Kc16 = NULL.
+ * out may alias R. */
+int launch_i2t_fused(const float *X, long xs, int K, const void *pq16,
+                     const void *Kc16, const void *Wt16, const float *bt,
+                     const void *YT16, const float *bo, const float *R,
+                     long rs, const float *g, const float *b, float *out,
+                     int T, int P, float eps, void *stream);
 
 /* Output upscaling fused with the mask logits (bf16 path): prep writes
  * the permuted bf16 transposes W1T16 [256][256] of up0w [256][64 4] and
@@ -248,14 +253,16 @@ int launch_upscale_fused(const float *keys, const void *W1T16,
                          int G, int P, float eps, int cus, void *stream);
 
 /* Token -> image attention on per-prompt keys (bf16 path): keys [P][T]
- * [256] + pe [T][256] against the folded queries U16 [P][64][256] (bf16,
- * k_i2t_fold on the projected queries with the key projection), nsplit
- * key splits with partials in part (P nsplit 64 258 floats), merged into
- * Z [P][64][256], then o [P][8][128] = Wv Z + bv per head. */
-int launch_t2i_fused(const float *keys, const float *pe, const void *U16,
-                     float *part, float *Z, const void *Wv, int wv_dt,
-                     const float *bv, float *o, int T, int P, int nsplit,
-                     void *stream);
+ * [256] + PE against the folded queries U16 [P][64][256] (bf16,
+ * k_i2t_fold on the projected queries with the key projection), the PE
+ * part as pk16 [T][128] bf16 (PE through the key projection, no bias)
+ * against Qc16 (the fold's compact rows s q_{i,h}), nsplit key splits
+ * with partials in part (P nsplit 64 258 floats), merged into Z [P][64]
+ * [256], then o [P][8][128] = Wv Z + bv per head. */
+int launch_t2i_fused(const float *keys, const void *pk16, const void *U16,
+                     const void *Qc16, float *part, float *Z, const void *Wv,
+                     int wv_dt, const float *bv, float *o, int T, int P,
+                     int nsplit, void *stream);
 
 /* The decoder's IoU head (head 0, token 1, 4 raw outputs into iou [P][4])
  * and hypernetwork MLPs (heads 1..3, tokens 3..5, into hyper [P][3][32])

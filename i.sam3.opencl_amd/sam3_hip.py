@@ -143,7 +143,8 @@ class SamDecoder(ctypes.Structure):
         [(n, Mem) for n in ("mask", "sel", "stats")] + \
         [("mask_cap", ctypes.c_size_t)] + \
         [(n, Mem) for n in ("fold_w", "fold_b", "fold_y", "up_w1t",
-                            "up_w2t", "t2i_part", "t2i_z")] + \
+                            "up_w2t", "t2i_part", "t2i_z", "fold_c", "pe_q1",
+                            "pe_k1", "pe_kf")] + \
         [("graph", ctypes.c_void_p), ("graph_exec", ctypes.c_void_p),
          ("graph_P", ctypes.c_int), ("graph_scratch", ctypes.c_void_p)]
 

@@ -436,6 +436,12 @@ struct sam_decoder {
      * ((2 CUs + batch) records of 64 rows x 258 floats) and the merged
      * weighted key sums Z [batch][64][256]. */
     hipb_mem t2i_part, t2i_z;
+    /* precision=bf16: the folds' compact per-head token rows (s k_{t,h},
+     * or s q_{i,h} for token -> image) [batch][64][16] bf16, and the dense
+     * PE through the layer-1 image-query, layer-1 key and final key
+     * projections (no bias), [grid^2][128] bf16 each, per image: the
+     * position term of the fused blocks' scores. */
+    hipb_mem fold_c, pe_q1, pe_k1, pe_kf;
     /* sam_dec_graph: hipGraph_t, hipGraphExec_t of the device sequence
      * for graph_P prompts, and the backend scratch it was captured with. */
     void *graph, *graph_exec;

@@ -178,39 +178,63 @@ __device__ __forceinline__ unsigned swz_off(int row, int chunk, int rowbytes)
  * / 8) with all C chunks when P >= 8, else all prompts with chunks [x C /
  * 8, (x + 1) C / 8): pa, np (first prompt, count), ca, nc (first chunk,
  * count). */
-#ifndef I2T_WAVES
-#define I2T_WAVES 4
-#endif
-#ifndef I2T_BLOCK
-#define I2T_BLOCK 8
-#endif
-#define I2T_TOK (32 * I2T_WAVES)
-__device__ __forceinline__ void i2t_region(int P, int C, int x, int &pa, int &np, int &ca,
-                                           int &nc)
+/* Item (prompt p, 128-token chunk c) of workgroup b, which runs on XCD
+ * b % 8. Both orders take blocks of 8 chunks x a set of prompts, chunk
+ * fastest, so that the workgroups in flight on an XCD share each prompt's
+ * fold (Wt, Y^T, fetched by the block's first workgroup of the prompt)
+ * and each chunk's shared rows (read by the block's prompts together).
+ * Layer 1 (XR): XCD x owns a region, prompts [x P / 8, (x + 1) P / 8)
+ * with all C chunks when P >= 8 (else all prompts, chunks [x C / 8, (x +
+ * 1) C / 8)), so that its prompts' folds and the whole shared PQ (1.3 MB)
+ * stay in its L2 from block to block: 1.11 x the bytes of keys + PE
+ * fetched at P = 64, against 1.22 x in the order below. Layer 0: XCD x
+ * takes the x-th eighth of all items in block order, which runs ~5 %
+ * faster there (its shared rows, qp0 and src, are 1.5 KB a token). Grid:
+ * 8 x ceil(P / 8) C or 8 x P ceil(C / 8) (layer 1), P C rounded up to a
+ * multiple of 8 (layer 0). */
+template <bool XR>
+__device__ __forceinline__ bool i2t_item(int P, int C, unsigned b, int &p, int &c)
 {
-    if (P >= 8) {
-        pa = x * P / 8;
-        np = (x + 1) * P / 8 - pa;
-        ca = 0;
-        nc = C;
+    unsigned pa, np, ca, nc, s;
+
+    if constexpr (XR) {
+        const int x = (int)(b % 8);
+
+        if (P >= 8) {
+            pa = (unsigned)(x * P / 8);
+            np = (unsigned)((x + 1) * P / 8) - pa;
+            ca = 0;
+            nc = (unsigned)C;
+        }
+        else {
+            pa = 0;
+            np = (unsigned)P;
+            ca = (unsigned)(x * C / 8);
+            nc = (unsigned)((x + 1) * C / 8) - ca;
+        }
+        s = b / 8;
     }
     else {
-        pa = 0;
-        np = P;
-        ca = x * C / 8;
-        nc = (x + 1) * C / 8 - ca;
+        const unsigned total = (unsigned)P * (unsigned)C;
+
+        pa = ca = 0;
+        np = (unsigned)P;
+        nc = (unsigned)C;
+        s = (b % 8) * ((total + 7) / 8) + b / 8;
     }
+    if (s >= np * nc)
+        return false;
+    const unsigned blk = s / (8 * np), r = s % (8 * np);
+    const unsigned nb = nc - 8 * blk < 8 ? nc - 8 * blk : 8;
+
+    p = (int)(pa + r / nb);
+    c = (int)(ca + 8 * blk + r % nb);
+    return true;
 }
 
-/* Workgroup = 8 waves = 256 image tokens of one prompt (one workgroup
- * per CU): workgroup b takes item b / 8 of XCD b % 8's region
- * (i2t_region), chunk-major, prompt fastest, so the workgroups in flight
- * on an XCD cover a few chunks of each of its prompts: a prompt's fold
- * (Wt, Y^T; 256 tokens per fetch of it) stays in that XCD's L2 between
- * uses, and the rows the prompts share (PQ in layer 1, qp0 and src in
- * layer 0) of a chunk are read by all of them at nearly the same time. X
- * rows of K floats (per-prompt stride xs, 0 = shared); residual R (stride
- * rs, 0 = shared); out [P][T][256] may alias R. */
+/* Workgroup = 4 waves = 128 image tokens of one prompt (i2t_item). X rows
+ * of K floats (per-prompt stride xs, 0 = shared); residual R (stride rs,
+ * 0 = shared); out [P][T][256] may alias R. */
 /* RX (layer 1): the residual R is the input X itself (the keys), and the
  * scores take the position term Kc PQ^T (pq [T][128] bf16, kc [P][64][16]
  * bf16). The S^T loop drops each token's loaded keys into the output
@@ -218,7 +242,7 @@ __device__ __forceinline__ void i2t_region(int P, int C, int x, int &pa, int &np
  * per step), so the U^T product adds onto the residual and the keys are
  * read from HBM once. */
 template <int K, bool RX>
-__global__ __launch_bounds__(64 * I2T_WAVES, 8 / I2T_WAVES) void k_i2t_fused(
+__global__ __launch_bounds__(256, 2) void k_i2t_fused(
     const float *X, long xs, const uint16_t *__restrict__ pq,
     const uint16_t *__restrict__ kc,
     const uint16_t *__restrict__ Wt16, const float *__restrict__ bt,
@@ -231,30 +255,23 @@ __global__ __launch_bounds__(64 * I2T_WAVES, 8 / I2T_WAVES) void k_i2t_fused(
     __shared__ float bts[FOLD_ROWS];
     const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, hh = l >> 5,
               l32 = l & 31;
-    int pa, np, ca, nc;
+    int p, c;
 
-    i2t_region(P, (T + I2T_TOK - 1) / I2T_TOK, (int)(blockIdx.x % 8), pa, np, ca, nc);
-    const unsigned it = blockIdx.x / 8;
-
-    if (it >= (unsigned)np * (unsigned)nc)
+    if (!i2t_item<RX>(P, (T + 127) / 128, blockIdx.x, p, c))
         return;
-    /* Blocks of I2T_BLOCK chunks x the region's prompts, chunk fastest. */
-    const unsigned blk = it / (I2T_BLOCK * (unsigned)np), r = it % (I2T_BLOCK * (unsigned)np);
-    const unsigned nb = (unsigned)nc - I2T_BLOCK * blk < I2T_BLOCK ? (unsigned)nc - I2T_BLOCK * blk
-                                                                   : I2T_BLOCK;
-    const int p = pa + (int)(r / nb), ch0 = I2T_TOK * (ca + (int)(I2T_BLOCK * blk + r % nb));
+    const int ch0 = 128 * c;
 
     /* Stage the prompt's Wt (64 x K) and Y^T (256 x 64) in LDS. */
     {
         const uint16_t *wt = Wt16 + (long)p * FOLD_ROWS * K;
         const uint16_t *yt = YT16 + (long)p * 256 * FOLD_ROWS;
 
-        for (int i = tid; i < FOLD_ROWS * K / 8; i += 64 * I2T_WAVES) {
+        for (int i = tid; i < FOLD_ROWS * K / 8; i += 256) {
             const int row = i / (K / 8), c = i % (K / 8);
 
             *(u32x4 *)(Ws + swz_off(row, c, 2 * K)) = *(const u32x4 *)(wt + 8 * i);
         }
-        for (int i = tid; i < 256 * FOLD_ROWS / 8; i += 64 * I2T_WAVES) {
+        for (int i = tid; i < 256 * FOLD_ROWS / 8; i += 256) {
             const int row = i / 8, c = i % 8;
 
             *(u32x4 *)(Ys + swz_off(row, c, 2 * FOLD_ROWS)) = *(const u32x4 *)(yt + 8 * i);
@@ -332,6 +349,9 @@ __global__ __launch_bounds__(64 * I2T_WAVES, 8 / I2T_WAVES) void k_i2t_fused(
         s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, bx, s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, bx, s1, 0, 0, 0);
     }
+    /* Every wave's reads of Wt are done past this point: the epilogue
+     * reuses its LDS for staging. */
+    __syncthreads();
 
     /* Grouped softmax: register r of tile T_ is row 32 T_ + 8 (r / 4) +
      * 4 hh + r % 4, i.e. head 4 T_ + r / 4 and prompt token 4 hh + r % 4:
@@ -375,18 +395,17 @@ __global__ __launch_bounds__(64 * I2T_WAVES, 8 / I2T_WAVES) void k_i2t_fused(
     }
 
     /* Epilogue through a per-wave [32 tokens][32 channels] fp32 staging
-     * tile in the Y^T area (free once every wave's U^T product is done:
-     * the barrier), so that the residual is read and the output written
-     * as whole 128-byte row segments: in the coalesced phase lane L takes
-     * token 8 k + L / 8, 16-byte chunk L % 8 of the tile; chunk c of
-     * staging row r sits at c ^ (r & 7). Register r of U^T tile c is
-     * channel 32 c + 8 (r / 4) + 4 hh + r % 4, i.e. chunk 2 (r / 4) + hh
-     * of the tile's row l32. */
-    __syncthreads();
+     * tile in the (now free) Wt area, so that the residual is read and the
+     * output written as whole 128-byte row segments: in the coalesced
+     * phase lane L takes token 8 k + L / 8, 16-byte chunk L % 8 of the
+     * tile; chunk c of staging row r sits at c ^ (r & 7). Register r of
+     * U^T tile c is channel 32 c + 8 (r / 4) + 4 hh + r % 4, i.e. chunk
+     * 2 (r / 4) + hh of the tile's row l32. The barrier after the S^T
+     * product guarantees every wave is done reading Wt. */
     /* Nothing of the epilogue is scheduled into the products above (its
      * loads would stay live across them and spill). */
     __builtin_amdgcn_sched_barrier(0);
-    char *stg = Ys + 4096 * w;
+    char *stg = Ws + 4096 * w;
     const int j0 = ch0 + 32 * w;
     const float *rbase = R + (long)p * rs;
 
@@ -467,15 +486,15 @@ extern "C" int launch_i2t_fused(const float *X, long xs, int K, const void *pq16
                                 const float *b, float *out, int T, int P,
                                 float eps, void *stream)
 {
-    const long C = T > 0 ? (T + I2T_TOK - 1) / I2T_TOK : 0;
-    /* 8 x the largest region (ceil(P / 8) C or P ceil(C / 8) items of 256
-     * tokens; 64-bit, so that sizes past the grid limit are refused rather
-     * than wrapped). */
-    const long grid = P < 1 ? 0 : 8L * (P >= 8 ? (P + 7L) / 8 * C : P * ((C + 7) / 8));
     /* K = 256 is layer 1 (residual = input, position term); K = 128 is
      * layer 0 (shared image queries, separate residual, no position
-     * term). */
+     * term). The grids of i2t_item, in 64-bit arithmetic so that sizes
+     * past the grid limit are refused rather than wrapped. */
     const bool l1 = K == 256;
+    const long C = T > 0 ? (T + 127) / 128 : 0;
+    const long grid = P < 1 ? 0
+                      : !l1 ? ((long)P * C + 7) / 8 * 8
+                      : 8L * (P >= 8 ? (P + 7L) / 8 * C : P * ((C + 7) / 8));
 
     if (P < 1 || T < 1 || grid > 0x7fffffffL || (K != 128 && K != 256) ||
         ((xs | rs) & 3) || (l1 && (R != X || rs != xs || !pq16 || !Kc16)) ||
@@ -485,12 +504,12 @@ extern "C" int launch_i2t_fused(const float *X, long xs, int K, const void *pq16
           (uintptr_t)(l1 ? Kc16 : X) | (uintptr_t)Wt16 | (uintptr_t)YT16) & 15))
         return hipErrorInvalidValue;
     if (l1)
-        hipLaunchKernelGGL((k_i2t_fused<256, true>), dim3((unsigned)grid), dim3(64 * I2T_WAVES), 0,
+        hipLaunchKernelGGL((k_i2t_fused<256, true>), dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, X, xs, (const uint16_t *)pq16,
                            (const uint16_t *)Kc16, (const uint16_t *)Wt16, bt,
                            (const uint16_t *)YT16, bo, R, rs, g, b, out, T, P, eps);
     else
-        hipLaunchKernelGGL((k_i2t_fused<128, false>), dim3((unsigned)grid), dim3(64 * I2T_WAVES), 0,
+        hipLaunchKernelGGL((k_i2t_fused<128, false>), dim3((unsigned)grid), dim3(256), 0,
                            (hipStream_t)stream, X, xs, nullptr, nullptr,
                            (const uint16_t *)Wt16, bt, (const uint16_t *)YT16, bo, R,
                            rs, g, b, out, T, P, eps);

@@ -84,9 +84,11 @@ def test_prepare_caches(hip, be, orc, weights):
         d.free()
 
 
-@pytest.mark.parametrize("G,P", [(72, 2), (16, 6)])
+@pytest.mark.parametrize("G,P", [(72, 2), (16, 6), (16, 12)])
 def test_decode(hip, be, orc, weights, G, P):
-    """The whole sam_decode: IoU predictions and low-resolution logits."""
+    """The whole sam_decode: IoU predictions and low-resolution logits.
+    P = 12 puts one or two prompts on each XCD in the fused blocks' work
+    split (P >= 8 with an uneven share), P = 2 and 6 split the chunks."""
     d = Dec(hip, be, orc, weights, G, P, 41 + G)
     try:
         pts = np.random.default_rng(G).uniform(0, 14 * G, (P, 2)).astype(np.float32)

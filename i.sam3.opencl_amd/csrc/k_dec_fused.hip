@@ -585,26 +585,6 @@ extern "C" int launch_upscale_prep(const void *up0w, int dt0, const void *up3w,
     return hipGetLastError();
 }
 
-/* GELU with erf from Abramowitz & Stegun, Handbook of Mathematical
- * Functions, formula 7.1.26 (|error| <= 1.5e-7 on erf): erf(z) = 1 -
- * (a1 t + ... + a5 t^5) exp(-z^2), t = 1 / (1 + p z), z >= 0, odd
- * extension; far below the bf16 rounding of its result's consumers. */
-__device__ __forceinline__ float gelu_as(float v)
-{
-    const float z = fabsf(v) * 0.70710678118654752f;
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-    float poly = fmaf(1.061405429f, t, -1.453152027f);
-
-    poly = fmaf(poly, t, 1.421413741f);
-    poly = fmaf(poly, t, -0.284496736f);
-    poly = fmaf(poly, t, 0.254829592f);
-    poly *= t;
-    const float e = __builtin_amdgcn_exp2f(-z * z * LOG2E_F);
-    const float erf_abs = fmaf(-poly, e, 1.0f);
-
-    return 0.5f * v * (1.0f + copysignf(erf_abs, v));
-}
-
 /* Persistent: one 8-wave workgroup per CU keeps W1T (128 KB) and W2T
  * (16 KB) in LDS, XOR-swizzled by 16-byte chunk, and each wave walks the
  * (prompt, 32-token group) items with stride 8 x gridDim.x. */
@@ -754,7 +734,7 @@ __global__ __launch_bounds__(512, 1) void k_upscale_fused(
                         #pragma unroll
                         for (int i = 0; i < 4; i++)
                             ub[2 * half + (q >> 1)][4 * (q & 1) + i] =
-                                (__bf16)gelu_as(fmaf((v[4 * q + i] - mean) * rs, gw[i], gb[i]));
+                                (__bf16)gelu_bf16path(fmaf((v[4 * q + i] - mean) * rs, gw[i], gb[i]));
                     }
                 }
                 /* Per sub-pixel tile c2: G2^T (4 k steps), + up3b + feat_s0,
@@ -783,7 +763,7 @@ __global__ __launch_bounds__(512, 1) void k_upscale_fused(
 
                             #pragma unroll
                             for (int i = 0; i < 4; i++)
-                                ub2[4 * h2 + i] = (__bf16)gelu_as(g2[8 * s + 4 * h2 + i] + bb[i] + ff[i]);
+                                ub2[4 * h2 + i] = (__bf16)gelu_bf16path(g2[8 * s + 4 * h2 + i] + bb[i] + ff[i]);
                         }
                         d3 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hyb[s], ub2, d3, 0, 0, 0);
                     }

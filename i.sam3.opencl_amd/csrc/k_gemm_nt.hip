@@ -162,26 +162,14 @@ __device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0
     }
 }
 
-/* Epilogue activation of the bf16 products: GELU with erf from
- * Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7, far below the bf16
- * rounding of fc1's stored output), whose short straight-line code leaves
- * the K loop more registers than the library erff. */
+/* Epilogue activation of the bf16 products: GELU through gelu_bf16path
+ * (erf within 2.5e-5, below the bf16 rounding of fc1's stored output; its
+ * short straight-line code leaves the K loop more registers than the
+ * library erff). */
 __device__ __forceinline__ float nt_act(float v, int act)
 {
-    if (act == ACT_GELU_K) {
-        const float z = fabsf(v) * 0.70710678118654752f;
-        const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-        float poly = fmaf(1.061405429f, t, -1.453152027f);
-
-        poly = fmaf(poly, t, 1.421413741f);
-        poly = fmaf(poly, t, -0.284496736f);
-        poly = fmaf(poly, t, 0.254829592f);
-        poly *= t;
-        const float e = __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-        const float erf_abs = fmaf(-poly, e, 1.0f);
-
-        return 0.5f * v * (1.0f + copysignf(erf_abs, v));
-    }
+    if (act == ACT_GELU_K)
+        return gelu_bf16path(v);
     return act == ACT_RELU_K ? fmaxf(v, 0.0f) : v;
 }
 

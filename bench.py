@@ -12,10 +12,11 @@ baseline (the oracle's restatement of the reference's profile=cpu
 sequence on the host cores).
 
 Order: the host-side sections run first, then the GPU sections (fp32
-path, decoder, mask decoder, text path, backbone), then the headline's W
-warm-up and K timed launches, so that those K launches (a few ms at
+path, decoder, mask decoder, text path, backbone), then ~27 ms of the
+global attention region back to back (COND_REGIONS), then the headline's
+W warm-up and K timed launches, so that those K launches (a few ms at
 most) see the engine clock at its loaded steady state instead of its
-ramp from idle.
+ramp from idle (from idle the clock needs 10-20 ms of sustained work).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -38,6 +39,11 @@ PEAK_BF16 = 2516.6   # TFLOP/s, dense bf16 MFMA, MI355X
 PEAK_F32 = 157.3     # TFLOP/s, f32 MFMA
 PEAK_HBM = 8000.0    # GB/s
 COPY_BYTES = 256 << 20
+# Replays of the global attention region (~0.18 ms each) that bring the
+# engine clock to its loaded state before the headline's warm-up steps.
+COND_REGIONS = 150
+# Warm-up launches of the windowed batch before its timed launches (~21 ms).
+WIN_WARM = 1200
 
 # HBM bytes per k_attn_bf16 launch (global, 5184 tokens x 16 heads), from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --kernel-only`
@@ -732,16 +738,30 @@ def main():
         mdec["cpu_oracle"] = mdec_cpu
     text = text_attention(hip, sub_steps, sub_warm)
     bb = backbone(hip, 5, 2)
+    # Clock conditioning: the sections above end in profiled passes (a
+    # synchronisation per kernel) and buffer frees, after which the engine
+    # clock has dropped; from there it takes 10-20 ms of sustained work to
+    # come back (the global kernel runs 122 us after 5 warm-up launches
+    # from idle, 110.6 us after 200). The global block's attention region,
+    # replayed back to back for ~27 ms, brings it to its loaded state
+    # before the W warm-up steps of the headline.
+    for _ in range(COND_REGIONS):
+        glob.region()
+    be.finish()
 
     # The headline: W warm-up launches, then exactly K timed launches of the
     # global attention, right after the GPU sections above, so the engine
     # clock is at its loaded steady state rather than ramping from idle
     # within the short timed region; then the windowed batch over the same
-    # GPU time: its launches are a sixth as long, so 6 W warm-up and 6 K
-    # timed ones (20 launches of a 19 us kernel are too short a window).
+    # GPU time: its launches are a sixth as long, so 6 K timed ones (20
+    # launches of a 19 us kernel are too short a window), after at least
+    # WIN_WARM back-to-back warm-up launches: run alone, the windowed kernel
+    # takes 19.5 us per launch after 30 or 300 of them and 17.3 us after
+    # 1200, its steady state inside the trunk.
     ms = timed(be, glob.attn, args.steps, args.warmup)
     tflops = glob.flops() / ms / 1e9
-    wms = timed(be, win.attn, 6 * args.steps, 6 * args.warmup)
+    win_warm = max(6 * args.warmup, WIN_WARM)
+    wms = timed(be, win.attn, 6 * args.steps, win_warm)
     # Config 1: one 576-token window (16 heads), the shape the reference's
     # own CPU run takes; and its exact path.
     one = Block(hip, be, 24, seed=1, grid=24)
@@ -777,8 +797,12 @@ def main():
                    "tokens": 5184, "heads": 16, "head_dim": 64,
                    "parallelism": "none (1 GPU)"},
         "pct_bf16_peak": round(100 * tflops / PEAK_BF16, 2),
+        "clock_conditioning": "%d back-to-back replays of the global block's attention "
+                              "region (LayerNorm, QKV projection, attention; ~27 ms) "
+                              "before the W warm-up steps" % COND_REGIONS,
         "windowed": {"workload": "9 windows x 576 tokens, 16 heads x 64, bf16",
                      "ms": round(wms, 5), "launches_timed": 6 * args.steps,
+                     "warmup_launches": win_warm,
                      "TFLOP/s": round(win.flops() / wms / 1e9, 2),
                      "pct_bf16_peak": round(100 * win.flops() / wms / 1e9 /
                                             PEAK_BF16, 2),

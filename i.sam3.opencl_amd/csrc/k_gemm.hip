@@ -298,6 +298,41 @@ __global__ __launch_bounds__(256) void k_gemm_bf16(gemm_desc d, int avec,
  * Unbatched, B stored N x K, K % 64 == 0, 16-byte aligned operand rows
  * (checked by the launcher). Rows / columns past M / N read row 0 and are
  * not stored. */
+/* Eight consecutive elements of an operand of element type DT (a
+ * compile-time constant, so that the loads of a batch of k steps are
+ * issued together) as an MFMA fragment. */
+template <int DT> __device__ __forceinline__ bf16x8 frag8(const void *base, long idx)
+{
+    bf16x8 r;
+
+    if constexpr (DT == DT_F32) {
+        const f32x4 *p = (const f32x4 *)((const float *)base + idx);
+        const f32x4 x = p[0], y = p[1];
+
+        for (int e = 0; e < 4; e++) {
+            r[e] = (__bf16)x[e];
+            r[4 + e] = (__bf16)y[e];
+        }
+    }
+    else if constexpr (DT == DT_BF16) {
+        r = *(const bf16x8 *)((const uint16_t *)base + idx);
+    }
+    else {
+        const u32x4 v = *(const u32x4 *)((const uint16_t *)base + idx);
+
+        for (int e = 0; e < 4; e++) {
+            r[2 * e] = (__bf16)h2f((uint16_t)(v[e] & 0xffffu));
+            r[2 * e + 1] = (__bf16)h2f((uint16_t)(v[e] >> 16));
+        }
+    }
+    return r;
+}
+
+/* Batches of SMALL_BATCH k steps: all their loads, then their MFMAs, so a
+ * wave waits for memory once per batch (once in all for K <= 512). */
+#define SMALL_BATCH 8
+
+template <int ADT, int BDT>
 __global__ __launch_bounds__(256) void k_gemm_small(gemm_desc d)
 {
     __shared__ float red[3][16][64];
@@ -305,21 +340,42 @@ __global__ __launch_bounds__(256) void k_gemm_small(gemm_desc d)
     const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
     const int m = m0 + l32 < d.M ? m0 + l32 : 0, n = n0 + l32 < d.N ? n0 + l32 : 0;
     const int kq = d.K / 4; /* a multiple of 16 */
-    f32x16 acc = {};
+    const int nst = kq / 16;
+    const long arow = d.aoff + (long)m * d.lda + w * kq + 8 * h;
+    const long brow = d.boff + (long)n * d.ldb + w * kq + 8 * h;
+    const bool f32c = d.cdt == DT_F32;
+    const void *R = d.R ? (const void *)((f32c ? 4 : 2) * d.roff + (const char *)d.R) : nullptr;
+    f32x16 acc = {}, res = {};
+    float bn = 0.0f;
 
-#pragma unroll 4
-    for (int k = w * kq + 8 * h; k < (w + 1) * kq; k += 16) {
-        float fa[8], fb[8];
-        bf16x8 a, b;
+    /* Wave 0 stores the tile: its bias and residual loads go out with the
+     * operand loads instead of after the reduction. */
+    if (w == 0 && n0 + l32 < d.N) {
+        if (d.bias)
+            bn = d.bias[n0 + l32];
+        if (R)
+            for (int r = 0; r < 16; r++) {
+                const int mr = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const long idx = (long)(mr < d.M ? mr : 0) * d.ldc + n0 + l32;
 
-        load8(d.A, d.adt, d.aoff + (long)m * d.lda + k, 8, true, fa);
-        load8(d.B, d.bdt, d.boff + (long)n * d.ldb + k, 8, true, fb);
-        for (int e = 0; e < 8; e++) {
-            a[e] = (__bf16)fa[e];
-            b[e] = (__bf16)fb[e];
-        }
-        /* D = A B^T tile: rows m (A operand), columns n (B operand). */
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+                res[r] = f32c ? ((const float *)R)[idx] : bf2f(((const uint16_t *)R)[idx]);
+            }
+    }
+
+    for (int s0 = 0; s0 < nst; s0 += SMALL_BATCH) {
+        bf16x8 a[SMALL_BATCH], b[SMALL_BATCH];
+
+#pragma unroll
+        for (int u = 0; u < SMALL_BATCH; u++)
+            if (s0 + u < nst) {
+                a[u] = frag8<ADT>(d.A, arow + 16 * (s0 + u));
+                b[u] = frag8<BDT>(d.B, brow + 16 * (s0 + u));
+            }
+#pragma unroll
+        for (int u = 0; u < SMALL_BATCH; u++)
+            if (s0 + u < nst)
+                /* D = A B^T tile: rows m (A operand), columns n (B operand). */
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[u], b[u], acc, 0, 0, 0);
     }
     if (w > 0)
         for (int r = 0; r < 16; r++)
@@ -329,12 +385,36 @@ __global__ __launch_bounds__(256) void k_gemm_small(gemm_desc d)
         return;
     for (int r = 0; r < 16; r++)
         acc[r] += (red[0][r][l] + red[1][r][l]) + red[2][r][l];
-    const void *R = d.R ? (const void *)((d.cdt == DT_F32 ? 4 : 2) * d.roff +
-                                         (const char *)d.R) : nullptr;
-    void *C = (char *)d.C + (d.cdt == DT_F32 ? 4 : 2) * d.coff;
+    void *C = (char *)d.C + (f32c ? 4 : 2) * d.coff;
 
-    if (n0 + l32 < d.N)
-        store_block(d, C, R, acc, m0, n0 + l32);
+    if (n0 + l32 >= d.N)
+        return;
+    /* store_block's epilogue with the preloaded bias and residual. */
+    for (int r = 0; r < 16; r++) {
+        const int mr = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const long idx = (long)mr * d.ldc + n0 + l32;
+        float v = act_k(d.alpha * acc[r] + bn, d.act);
+
+        if (mr >= d.M)
+            continue;
+        if (R)
+            v += res[r];
+        if (f32c)
+            ((float *)C)[idx] = v;
+        else
+            ((uint16_t *)C)[idx] = f2bf(v);
+    }
+}
+
+template <int ADT>
+static void launch_small_b(const gemm_desc *d, dim3 grid, hipStream_t s)
+{
+    if (d->bdt == DT_F32)
+        hipLaunchKernelGGL((k_gemm_small<ADT, DT_F32>), grid, dim3(256), 0, s, *d);
+    else if (d->bdt == DT_BF16)
+        hipLaunchKernelGGL((k_gemm_small<ADT, DT_BF16>), grid, dim3(256), 0, s, *d);
+    else
+        hipLaunchKernelGGL((k_gemm_small<ADT, DT_F16>), grid, dim3(256), 0, s, *d);
 }
 
 static int vec_ok(int dt, long off, long s0, long s1, int ld)
@@ -364,8 +444,13 @@ extern "C" int launch_gemm(const gemm_desc *d, void *stream)
     if (d->mode == MODE_BF16 && d->transb && d->nb == 1 && d->K % 64 == 0 &&
         avec && bvec && (long)grid.x * grid.y <= 64 &&
         ((uintptr_t)d->A & 15) == 0 && ((uintptr_t)d->B & 15) == 0) {
-        hipLaunchKernelGGL(k_gemm_small, dim3((d->N + 31) / 32, (d->M + 31) / 32),
-                           dim3(256), 0, s, *d);
+        const dim3 sg((d->N + 31) / 32, (d->M + 31) / 32);
+
+        /* A is never half (the gemm wrapper rejects it). */
+        if (d->adt == DT_F32)
+            launch_small_b<DT_F32>(d, sg, s);
+        else
+            launch_small_b<DT_BF16>(d, sg, s);
         return hipGetLastError();
     }
     if (d->mode == MODE_BF16) {

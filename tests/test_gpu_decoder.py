@@ -68,7 +68,10 @@ class Dec:
 
 def test_prepare_caches(hip, be, orc, weights):
     """sam_dec_prepare: dense PE, src, src + PE and the layer-0
-    projections of the shared image keys, values and queries."""
+    projections of the shared image keys, values and queries; on the bf16
+    path also PE through the layer-1 image-query, layer-1 key and final
+    key projections without their biases (the fused blocks' position
+    term), against float64 products of the oracle's PE."""
     d = Dec(hip, be, orc, weights, 72, 1, 40)
     try:
         tol = TOL[be.precision]
@@ -80,6 +83,14 @@ def test_prepare_caches(hip, be, orc, weights):
             got = be.read_f32(d.dec.buf(name), T * cols).reshape(T, cols)
             assert report("prepare %s %s" % (name, be.precision), got,
                           d.prep[name]) <= tol
+        if be.precision == "bf16":
+            pe64 = d.prep["pe"].astype(np.float64)
+            for name, wname in (("pe_q1", "layers.1.i2t.qw"),
+                                ("pe_k1", "layers.1.t2i.kw"),
+                                ("pe_kf", "final_t2i.kw")):
+                got = be.read_f32(d.dec.buf(name), T * 128).reshape(T, 128)
+                want = pe64 @ np.asarray(weights[wname], np.float64).T
+                assert report("prepare %s bf16" % name, got, want) <= tol
     finally:
         d.free()
 

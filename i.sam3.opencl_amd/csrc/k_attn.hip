@@ -851,26 +851,38 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         const int fs = (kb1 - kb0) & 1;
         char *stg = w < 2 ? (char *)&Ks[fs][32 * w][0] : (char *)&Vt[fs][32 * (w - 2)][0];
         const int q0 = qi - l32, c = l & 7;
+        /* All 32 rows of the wave inside N (every wave but those of a
+         * ragged tail tile): the stores need no per-row test. */
+        const bool full = q0 + 32 <= N;
 
         if (f32out) {
-            /* Two passes of 32 columns (128 B per row); one for hd 32. */
+            /* Two passes of 32 columns (128 B per row); one for hd 32. The
+             * four staged chunks are read before any is stored, so their
+             * LDS latencies overlap instead of one per store. */
             for (int half = 0; half < ocols / 32; half++) {
                 const f32x16 &o = half ? st.o1 : st.o0;
+                f32x4 v[4];
 
                 for (int g = 0; g < 4; g++) {
-                    const f32x4 v = {o[4 * g] * inv, o[4 * g + 1] * inv,
+                    const f32x4 x = {o[4 * g] * inv, o[4 * g + 1] * inv,
                                      o[4 * g + 2] * inv, o[4 * g + 3] * inv};
 
-                    *(f32x4 *)(stg + 128 * l32 + 16 * ((2 * g + h) ^ (l32 & 7))) = v;
+                    *(f32x4 *)(stg + 128 * l32 + 16 * ((2 * g + h) ^ (l32 & 7))) = x;
                 }
                 for (int j = 0; j < 4; j++) {
                     const int row = 8 * j + (l >> 3);
-                    const f32x4 v = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
-                    if (q0 + row < N)
-                        __builtin_nontemporal_store(
-                            v, (f32x4 *)((float *)Obuf + obase + (long)(q0 + row) * ldo + 32 * half + 4 * c));
+                    v[j] = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
                 }
+                float *ob = (float *)Obuf + obase + (long)(q0 + (l >> 3)) * ldo + 32 * half + 4 * c;
+
+                if (full)
+                    for (int j = 0; j < 4; j++)
+                        __builtin_nontemporal_store(v[j], (f32x4 *)(ob + (long)8 * j * ldo));
+                else
+                    for (int j = 0; j < 4; j++)
+                        if (q0 + 8 * j + (l >> 3) < N)
+                            __builtin_nontemporal_store(v[j], (f32x4 *)(ob + (long)8 * j * ldo));
             }
         }
         else {
@@ -884,12 +896,23 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
 
                 *(uint2 *)(stg + 128 * l32 + 16 * (g ^ (l32 & 7)) + 8 * h) = pk;
             }
+            u32x4 v[4];
+
             for (int j = 0; j < 4; j++) {
                 const int row = 8 * j + (l >> 3);
-                const u32x4 v = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
 
-                if (q0 + row < N && 8 * c < ocols)
-                    *(u32x4 *)((uint16_t *)Obuf + obase + (long)(q0 + row) * ldo + 8 * c) = v;
+                v[j] = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
+            }
+            uint16_t *ob = (uint16_t *)Obuf + obase + (long)(q0 + (l >> 3)) * ldo + 8 * c;
+
+            if (8 * c < ocols) {
+                if (full)
+                    for (int j = 0; j < 4; j++)
+                        *(u32x4 *)(ob + (long)8 * j * ldo) = v[j];
+                else
+                    for (int j = 0; j < 4; j++)
+                        if (q0 + 8 * j + (l >> 3) < N)
+                            *(u32x4 *)(ob + (long)8 * j * ldo) = v[j];
             }
         }
     }

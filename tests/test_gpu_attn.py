@@ -245,13 +245,15 @@ def test_vit_attention_full_size(hip, be, orc, ws):
     assert worst <= TOL[be.precision], worst
 
 
-@pytest.mark.parametrize("grid,ws", [(16, 8), (24, 8), (16, 0)])
-def test_packed_projection_matches_packing_kernel(hip, orc, grid, ws):
+@pytest.mark.parametrize("grid,ws,E,H", [(16, 8, 128, 2), (24, 8, 128, 2), (16, 0, 128, 2),
+                                         (72, 24, 1024, 16), (72, 0, 1024, 16)])
+def test_packed_projection_matches_packing_kernel(hip, orc, grid, ws, E, H):
     """bf16 path: the operands the QKV projection's store packs (RoPE,
     scale, bf16, V^T, key block norms) are the packing kernel's, bit for
-    bit (norm bounds to 1e-6), on the same device projection."""
+    bit (norm bounds to 1e-6), on the same device projection, at small
+    shapes and at the full-size windowed and global blocks (projection
+    tiles spanning windows, every unit and key block of a 72 x 72 grid)."""
     be = hip.Backend(precision="bf16")
-    E, H = 128, 2
     x, n1w, n1b, w, b = block_inputs(grid + 3 * ws, grid, E)
     s = ws if ws else grid
     N = s * s

@@ -150,10 +150,14 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
     fetch(kb0);
     stage(0);
     __syncthreads();
+    int lvl = -1;
+
     for (int kb = kb0; kb < kb1; kb++) {
         const int buf = (kb - kb0) & 1;
         f32x16 s;
         float mx, m_new, mref, corr, rs = 0.0f;
+
+        prio_by_progress(kb - kb0, kb1 - kb0, lvl);
 
         if (kb + 1 < kb1)
             fetch(kb + 1);
@@ -220,6 +224,7 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
             stage(buf ^ 1);
         __syncthreads();
     }
+    __builtin_amdgcn_s_setprio(0);
 
     l_run += __shfl_xor(l_run, 32, 64);
     if (qi >= N)
@@ -815,11 +820,15 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         }
         st.l += sum32(s0, s1);
     };
+    int lvl = -1;
+
     for (int kb = kb0; kb < kb1; kb += 2) {
+        prio_by_progress(kb - kb0, kb1 - kb0, lvl);
         block(kb, std::integral_constant<int, 0>());
         if (kb + 1 < kb1)
             block(kb + 1, std::integral_constant<int, 1>());
     }
+    __builtin_amdgcn_s_setprio(0);
 
     st.l += __shfl_xor(st.l, 32, 64);
     /* Final O / l, or with key splits the unnormalised O of this split

@@ -560,6 +560,22 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * x |v|). */
 #define SAFE_SPAN 64.0f
 
+/* Balanced launch of k_attn_bf16 when the tiles fill between two and
+ * three workgroups per CU (the global ViT block: 82 tiles per XCD on 32
+ * CUs): on each XCD, dp workgroups take one whole tile each and the
+ * remaining tiles' (tile, key block) pairs are shared evenly by G more
+ * workgroups (stream-K), so every CU gets about the same number of key
+ * blocks instead of some three tiles and others two. rec holds 2 records
+ * of 4 waves x 34 x 64 floats per stream-K workgroup (8 G of them) for
+ * the pieces of cut tiles, cnt one arrival counter per tile (zero before
+ * the first launch; the last piece of each tile zeroes it again). G = 0
+ * turns it off. */
+struct sk_desc {
+    float *rec;
+    unsigned *cnt;
+    int G, dp;
+};
+
 /* Packed bf16 operands (k_qkv_pack layout), v_mfma_f32_32x32x16_bf16 with
  * f32 accumulation, 64-key blocks.
  *
@@ -583,41 +599,53 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
  * no weight exceeds 2^SAFE_SPAN and the largest is >= 2^-SAFE_SPAN, at
  * any score magnitude. While every m of the wave is 0 the scores feed
  * exp2 directly. */
-template <bool EXT, bool H32>
-__global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
-                                                      const uint16_t *__restrict__ q16,
-                                                      const uint16_t *__restrict__ k16,
-                                                      const uint16_t *__restrict__ vt16,
-                                                      const float *__restrict__ knorm,
-                                                      float *__restrict__ part,
-                                                      int nsplit)
+/* Key blocks [kb0, kb1) of query tile `tile` of unit `unit`: the body
+ * of k_attn_bf16 (a function rather than a lambda: wrapping it in a
+ * lambda costs the bias variant its register budget). `d` is the
+ * descriptor or, in stream-K mode, an opaque alias of it. */
+template <bool EXT, bool H32, bool SK, class Desc>
+__device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restrict__ q16,
+                                          const uint16_t *__restrict__ k16,
+                                          const uint16_t *__restrict__ vt16,
+                                          const float *__restrict__ knorm,
+                                          float *__restrict__ part, int nsplit, int sp,
+                                          const sk_desc &sk, unsigned rank, long unit,
+                                          int tile, int kb0, int kb1, int pdone, int ptotal,
+                                          int rbase, int R)
 {
     __shared__ __attribute__((aligned(16))) uint16_t Ks[2][64][64];
     __shared__ __attribute__((aligned(16))) uint16_t Vt[2][64][64];
+    __shared__ unsigned arrived;
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
     /* N queries and Nk keys per unit, each padded to a multiple of 64. */
     const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64,
               Npk = (Nk + 63) / 64 * 64, nblk = Npk / 64;
     const int ntiles = (N + 127) / 128;
-    /* 32-bit item arithmetic (the launcher keeps the grid below 2^31). */
-    const unsigned total = (unsigned)d.nb * ntiles * nsplit,
-                   per_xcd = (total + NXCD - 1) / NXCD;
-    /* XCD-aware order: workgroups are dispatched to the XCDs round-robin,
-     * so workgroup g runs on XCD g % NXCD; give each XCD a contiguous run
-     * of (unit, tile) items, i.e. whole units, whose K / V then stay in
-     * that XCD's L2 instead of every XCD streaming every unit. */
-    const unsigned item = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
-    if (item >= total)
-        return;
-    /* Item = (unit, query tile, key split); split sp takes key blocks
-     * [kb0, kb1) and, with nsplit > 1, leaves partial (O, m, l) records
-     * in `part` for k_attn_merge. */
-    const unsigned us = nsplit > 1 ? item / (unsigned)nsplit : item;
-    const int sp = (int)(item - us * (unsigned)nsplit);
-    const long unit = us / (unsigned)ntiles;
-    const int tile = (int)(us - (unsigned)unit * (unsigned)ntiles);
-    const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
+    const int krow = kperm(l32);
+    const f32x16 zero16 = {};
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    unsigned koff[2], voff[2];
+    for (int j = 0; j < 2; j++) {
+        const int row = 8 * (2 * w + j) + (l >> 3);
+        const int chunk = (l & 7) ^ ((row >> 1) & 7);
+
+        koff[j] = 2u * (row * 64 + 8 * chunk);
+        voff[j] = 2u * (row * Npk + 8 * chunk);
+    }
+    const unsigned lds_k = (unsigned)(uintptr_t)&Ks[0][0][0] + 2048u * wu,
+                   lds_v = (unsigned)(uintptr_t)&Vt[0][0][0] + 2048u * wu;
+    /* Byte offsets of this lane's MFMA operand fragments within one slot:
+     * K rows 32 c + kperm(l32) (c adds 4096 B), V^T rows l32 and 32 + l32
+     * (+4096 B); the swizzle depends only on row bits 1..3, which c and
+     * the +32 leave alone. */
+    unsigned kro[4], vro[4];
+    for (int i = 0; i < 4; i++) {
+        kro[i] = 2u * (krow * 64 + swz(krow, 2 * i + h));
+        vro[i] = 2u * (l32 * 64 + swz(l32, 2 * i + h));
+    }
+    const char *Kb = (const char *)&Ks[0][0][0], *Vb = (const char *)&Vt[0][0][0];
+
     const uint16_t *Qu = q16 + unit * Np * 64;
     const uint16_t *Ku = k16 + unit * Npk * 64;
     const uint16_t *Vu = vt16 + unit * 64 * Npk;
@@ -633,8 +661,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     const float *brow = EXT && d.bias
                             ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * Npk
                             : nullptr;
-    const int krow = kperm(l32);
-    const f32x16 zero16 = {};
     bf16x8 qb[4];
     SoftState st;
     float qn; /* |q| of this lane's query, rounded up */
@@ -646,17 +672,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
      * per-lane byte offsets do not depend on the block; the bases (block
      * start in global memory, destination rows in LDS) are wave-uniform
      * and live in SGPRs. */
-    const int wu = __builtin_amdgcn_readfirstlane(w);
-    unsigned koff[2], voff[2];
-    for (int j = 0; j < 2; j++) {
-        const int row = 8 * (2 * w + j) + (l >> 3);
-        const int chunk = (l & 7) ^ ((row >> 1) & 7);
-
-        koff[j] = 2u * (row * 64 + 8 * chunk);
-        voff[j] = 2u * (row * Npk + 8 * chunk);
-    }
-    const unsigned lds_k = (unsigned)(uintptr_t)&Ks[0][0][0] + 2048u * wu,
-                   lds_v = (unsigned)(uintptr_t)&Vt[0][0][0] + 2048u * wu;
     auto load_block = [&](int kb, int slot) {
         const uint16_t *kb_ = Ku + (long)kb * 64 * 64, *vb_ = Vu + kb * 64;
 
@@ -665,16 +680,6 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
             g2lds16_s(vb_, voff[j], lds_v + 8192u * slot + 1024u * j);
         }
     };
-    /* Byte offsets of this lane's MFMA operand fragments within one slot:
-     * K rows 32 c + kperm(l32) (c adds 4096 B), V^T rows l32 and 32 + l32
-     * (+4096 B); the swizzle depends only on row bits 1..3, which c and
-     * the +32 leave alone. */
-    unsigned kro[4], vro[4];
-    for (int i = 0; i < 4; i++) {
-        kro[i] = 2u * (krow * 64 + swz(krow, 2 * i + h));
-        vro[i] = 2u * (l32 * 64 + swz(l32, 2 * i + h));
-    }
-    const char *Kb = (const char *)&Ks[0][0][0], *Vb = (const char *)&Vt[0][0][0];
     float kn_next = kn[kb0];
 
     load_block(kb0, 0);
@@ -823,13 +828,79 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     int lvl = -1;
 
     for (int kb = kb0; kb < kb1; kb += 2) {
-        prio_by_progress(kb - kb0, kb1 - kb0, lvl);
+        prio_by_progress(pdone + kb - kb0, ptotal, lvl);
         block(kb, std::integral_constant<int, 0>());
         if (kb + 1 < kb1)
             block(kb + 1, std::integral_constant<int, 1>());
     }
     __builtin_amdgcn_s_setprio(0);
 
+    if (SK && (kb0 > 0 || kb1 < nblk)) {
+        /* A piece of a tile cut between workgroups: leave this piece's
+         * per-lane state (O, m, l; 34 floats, lane-minor) in the record
+         * of (workgroup, first or last piece), count it in, and let the
+         * last piece to arrive merge the others into its registers and
+         * store the tile. The pieces of a tile come from the stream-K
+         * workgroups of its XCD whose ranges meet its key blocks in that
+         * XCD's list of R shared (tile, key block) pairs, whose first tile
+         * is rbase; `rank` is the workgroup's record owner index, XCD
+         * G + its index among the XCD's G stream-K workgroups.
+         *
+         * Records and counters are only touched by agent-scope relaxed
+         * atomics, which go to the device's coherent memory rather than
+         * an XCD's L2; waiting for the record stores to complete
+         * (vmcnt(0)) before the count orders them without the L2
+         * write-back and invalidate of a device-scope fence, which cost
+         * far more than the kernel itself when every workgroup issues
+         * them. */
+        const int tid = (int)unit * ntiles + tile, t0 = (tid - rbase) * nblk;
+        /* An XCD whose remainder has fewer pairs than sk.G workgroups
+         * uses one per pair. */
+        const int G = R < sk.G ? R : sk.G, xg = (int)rank / sk.G * sk.G, me = (int)rank - xg;
+        auto owner = [&](int idx) { return (int)((((unsigned)idx + 1) * (unsigned)G - 1) / (unsigned)R); };
+        auto start = [&](int r) { return (int)((unsigned)r * (unsigned)R / (unsigned)G); };
+        auto slot_of = [&](int r) { return 2 * (xg + r) + (start(r) < t0 ? 1 : 0); };
+        const int r0 = owner(t0), r1 = owner(t0 + nblk - 1);
+        float *rec = sk.rec + ((long)slot_of(me) * 4 + w) * 34 * 64 + l;
+
+        auto put = [&](int k, float v) {
+            __hip_atomic_store(rec + 64 * k, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        };
+        for (int r = 0; r < 16; r++) {
+            put(r, st.o0[r]);
+            put(16 + r, st.o1[r]);
+        }
+        put(32, st.m);
+        put(33, st.l);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t == 0)
+            arrived = __hip_atomic_fetch_add(&sk.cnt[tid], 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived != (unsigned)(r1 - r0))
+            return;
+        if (t == 0)
+            __hip_atomic_store(&sk.cnt[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r = r0; r <= r1; r++) {
+            if (r == me)
+                continue;
+            float *pr = sk.rec + ((long)slot_of(r) * 4 + w) * 34 * 64 + l;
+            auto get = [&](int k) {
+                return __hip_atomic_load(pr + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            };
+            const float mp = get(32), lp = get(33);
+            const float M = __builtin_fmaxf(st.m, mp);
+            const float ca = __builtin_amdgcn_exp2f(st.m - M), cb = __builtin_amdgcn_exp2f(mp - M);
+
+            for (int r2 = 0; r2 < 16; r2++) {
+                st.o0[r2] = fmaf(st.o0[r2], ca, get(r2) * cb);
+                st.o1[r2] = fmaf(st.o1[r2], ca, get(16 + r2) * cb);
+            }
+            st.l = fmaf(st.l, ca, lp * cb);
+            st.m = M;
+        }
+    }
     st.l += __shfl_xor(st.l, 32, 64);
     /* Final O / l, or with key splits the unnormalised O of this split
      * (fp32 rows of 64 at part [unit][split][Np][64]) and its (m, l) pair
@@ -950,6 +1021,94 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     }
 }
 
+template <bool EXT, bool H32, bool SK>
+__global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
+                                                      const uint16_t *__restrict__ q16,
+                                                      const uint16_t *__restrict__ k16,
+                                                      const uint16_t *__restrict__ vt16,
+                                                      const float *__restrict__ knorm,
+                                                      float *__restrict__ part,
+                                                      int nsplit, sk_desc sk)
+{
+    const int nblk = (d.Nk + 63) / 64, ntiles = (d.N + 127) / 128;
+    /* XCD-aware order: workgroups are dispatched to the XCDs round-robin,
+     * so workgroup g runs on XCD g % NXCD; give each XCD a contiguous run
+     * of work, i.e. whole units, whose K / V then stay in that XCD's L2
+     * instead of every XCD streaming every unit. */
+    const unsigned per_xcd = gridDim.x / NXCD;
+    const unsigned rank = (blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
+
+    if (!SK) {
+        /* One (unit, query tile, key split) item per workgroup: split sp
+         * takes key blocks [sp nblk / nsplit, (sp + 1) nblk / nsplit) and,
+         * with nsplit > 1, leaves partial (O, m, l) records in `part` for
+         * k_attn_merge. 32-bit item arithmetic (the launcher keeps the
+         * grid below 2^31). */
+        const unsigned total = (unsigned)d.nb * ntiles * nsplit, item = rank;
+
+        if (item >= total)
+            return;
+        const unsigned us = nsplit > 1 ? item / (unsigned)nsplit : item;
+        const int sp = (int)(item - us * (unsigned)nsplit);
+        const long unit = us / (unsigned)ntiles;
+        const int tile = (int)(us - (unsigned)unit * (unsigned)ntiles);
+
+        const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
+
+        attn_tile<EXT, H32, false>(d, q16, k16, vt16, knorm, part, nsplit, sp, sk, rank,
+                                   unit, tile, kb0, kb1, 0, kb1 - kb0, 0, 0);
+        return;
+    }
+    /* Balanced launch (sk_desc): XCD x (workgroup g runs on XCD g % NXCD)
+     * owns tiles [x per, x per + nx), per = total / NXCD rounded up; its
+     * workgroups j < dp take whole tiles, its G further ones (j = dp + s)
+     * share the R key blocks of its remaining tiles, [s R / G, (s + 1) R /
+     * G) each, tile after tile; a tile cut between them is finished by the
+     * piece that arrives last. 32-bit arithmetic: the launcher keeps R G
+     * below 2^31. A barrier between segments keeps the next segment's
+     * first copies out of LDS the last one still reads. */
+    const unsigned total = (unsigned)d.nb * ntiles, per = (total + NXCD - 1) / NXCD;
+    const unsigned x = blockIdx.x % NXCD, j = blockIdx.x / NXCD;
+    const int tx0 = (int)(x * per);
+    const int nx = total > x * per ? (int)(total - x * per < per ? total - x * per : per) : 0;
+
+    const bool whole = (int)j < sk.dp;
+    const int sidx = (int)j - sk.dp, rbase = tx0 + sk.dp, R = (nx - sk.dp) * nblk;
+    /* Stream-K workgroups of this XCD: one per pair if it has fewer
+     * pairs left than sk.G (the last XCD's share may be short). */
+    const int G = R < sk.G ? R : sk.G;
+
+    if (whole ? (int)j >= nx : sidx >= G || R <= 0)
+        return;
+    /* A whole-tile workgroup is a stream-K range of one uncut tile (no
+     * record), so that both kinds share one instance of the tile body. */
+    const int a0 = whole ? ((int)j - sk.dp) * nblk
+                         : (int)((unsigned)sidx * (unsigned)R / (unsigned)G);
+    const int b = whole ? a0 + nblk : (int)(((unsigned)sidx + 1) * (unsigned)R / (unsigned)G);
+    int a = a0;
+
+    while (a < b) {
+        const int tl = a / nblk, tid = rbase + tl;
+        const int k0 = a - tl * nblk;
+        const int k1 = k0 + (b - a) < nblk ? k0 + (b - a) : nblk;
+        /* The descriptor read afresh in each segment, through an opaque
+         * copy of its kernel-argument address (d is the first argument,
+         * at offset 0): otherwise the compiler hoists every field the
+         * epilogue reads out of the segment loop and holds them in SGPRs
+         * across the key loop, which then spills. */
+        typedef const __attribute__((address_space(4))) attn_desc kdesc;
+        kdesc *dp = (kdesc *)__builtin_amdgcn_kernarg_segment_ptr();
+
+        asm volatile("" : "+s"(dp));
+        attn_tile<EXT, H32, true>(*dp, q16, k16, vt16, knorm, part, 1, 0, sk,
+                                  x * (unsigned)sk.G + (unsigned)sidx, tid / ntiles, tid % ntiles,
+                                  k0, k1, a - a0, b - a0, rbase, R);
+        a += k1 - k0;
+        if (a < b)
+            __syncthreads();
+    }
+}
+
 /* Merge of a few key-split partials (nsplit <= 8): 16 threads per
  * (unit, query), four channels each, looping over the splits: M = the
  * largest m_s over splits that saw a key, O = sum w_s o_s / sum w_s l_s
@@ -1057,28 +1216,59 @@ __global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__
     }
 }
 
+/* Zero fill of the balanced attention's arrival counters (a kernel, not
+ * a memset, so that it may sit in a captured graph). */
+__global__ __launch_bounds__(256) void k_attn_sk_zero(unsigned *cnt, long n)
+{
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (i < n)
+        cnt[i] = 0u;
+}
+
+extern "C" int launch_attn_sk_zero(unsigned *cnt, long n, void *stream)
+{
+    if (n < 1 || (n + 255) / 256 > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn_sk_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, cnt, n);
+    return hipGetLastError();
+}
+
 extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 const void *k16, const void *vt16,
                                 const float *knorm, float *part, int nsplit,
+                                float *skrec, unsigned *skcnt, int skG, int skdp,
                                 void *stream)
 {
     const int Np = (d->N + 63) / 64 * 64, nblk = (d->Nk + 63) / 64;
-    const long total = (long)d->nb * ((d->N + 127) / 128) * nsplit;
-    const long grid = (total + NXCD - 1) / NXCD * NXCD;
+    const long tiles = (long)d->nb * ((d->N + 127) / 128);
+    const long total = tiles * nsplit, per = (tiles + NXCD - 1) / NXCD;
+    const long grid = skG ? (long)NXCD * (skdp + skG) : (total + NXCD - 1) / NXCD * NXCD;
+    const sk_desc sk = {skrec, skcnt, skG, skdp};
     int err;
 
     if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk || nsplit > 64 ||
         (nsplit > 1 && !part))
         return hipErrorInvalidConfiguration;
+    /* Balanced launch: whole-key tiles, head width 64 without bias or
+     * causal mask, some tiles left over on an XCD after dp whole ones and
+     * at least one shared key block per stream-K workgroup, both buffers
+     * given, 32-bit pair arithmetic. */
+    if (skG && (nsplit != 1 || skG < 0 || skdp < 0 || per <= skdp ||
+                (per - skdp) * nblk < skG || (per - skdp) * nblk * skG > 0x7fffffffL ||
+                !skrec || !skcnt || d->bias || d->causal || d->hd != 64))
+        return hipErrorInvalidConfiguration;
     {
-        auto kern = d->bias || d->causal ? (d->hd == 32 ? k_attn_bf16<true, true>
-                                                        : k_attn_bf16<true, false>)
-                                         : (d->hd == 32 ? k_attn_bf16<false, true>
-                                                        : k_attn_bf16<false, false>);
+        auto kern = skG ? k_attn_bf16<false, false, true>
+                    : d->bias || d->causal ? (d->hd == 32 ? k_attn_bf16<true, true, false>
+                                                          : k_attn_bf16<true, false, false>)
+                                           : (d->hd == 32 ? k_attn_bf16<false, true, false>
+                                                          : k_attn_bf16<false, false, false>);
 
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
-                           (const uint16_t *)vt16, knorm, part, nsplit);
+                           (const uint16_t *)vt16, knorm, part, nsplit, sk);
     }
     err = hipGetLastError();
     if (err != hipSuccess || nsplit == 1)

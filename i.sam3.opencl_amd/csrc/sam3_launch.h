@@ -152,10 +152,20 @@ int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
 /* bf16 MFMA attention on the packed operands; O addressed as in d. With
  * 1 < nsplit <= 64 the key blocks are split nsplit ways and `part` (nb nsplit
  * Np 66 floats, Np = N rounded up to 64) holds the partials that a merge
- * kernel combines into O. */
+ * kernel combines into O. With skG > 0 (nsplit 1, head width 64 without
+ * bias or causal mask) the tiles of each XCD's share (the tile list in
+ * eight contiguous parts) go to skdp whole-tile workgroups and skG
+ * workgroups that share the rest's (tile, key block) pairs evenly:
+ * skrec holds ATTN_SK_REC_FLOATS floats per stream-K workgroup (8 skG of
+ * them), skcnt one counter per 128-query tile (nb ceil(N / 128)), zero
+ * before the first launch and left zero by every launch. */
+#define ATTN_SK_REC_FLOATS (2 * 4 * 34 * 64)
 int launch_attn_bf16(const struct attn_desc *d, const void *q16,
                      const void *k16, const void *vt16, const float *knorm,
-                     float *part, int nsplit, void *stream);
+                     float *part, int nsplit, float *skrec, unsigned *skcnt,
+                     int skG, int skdp, void *stream);
+/* Zero the n counters of launch_attn_bf16's balanced launch. */
+int launch_attn_sk_zero(unsigned *cnt, long n, void *stream);
 
 /* Additive bias table of the fused attention from the box relative
  * position bias of softmax_ext: out [heads][Nq][Nk padded to 64] =

@@ -517,6 +517,59 @@ static float *attn_part(struct sam_model *m, int N, int nb, int nsplit)
     return (float *)m->apart->ptr;
 }
 
+/* Balanced launch of the bf16 attention (launch_attn_bf16's skG, skdp):
+ * when an XCD's share of the 128-query tiles lies strictly between two
+ * and three per CU (the global ViT block: 82 tiles per XCD on 32 CUs),
+ * two whole tiles per CU run as before and one more workgroup per CU
+ * takes an even share of the remaining tiles' key blocks (stream-K), so
+ * that no CU runs three whole tiles while others run two. Only for head
+ * width 64 without bias or causal mask, with tiles of at least 16 key
+ * blocks. Returns skG (0: the plain grid) and sets *dp. */
+static int attn_sk(const struct hipb_backend *b, const struct attn_desc *d, int N,
+                   int Nk, int nb, int nsplit, int *dp)
+{
+    const long tiles = (long)nb * ((N + 127) / 128), per = (tiles + 7) / 8;
+    const int nblk = (Nk + 63) / 64, cus = b->cu_count > 0 ? b->cu_count : 256;
+    const int c = cus / 8; /* CUs per XCD */
+
+    *dp = 0;
+    if (nsplit != 1 || d->hd != 64 || d->bias || d->causal || nblk < 16 || c < 1 ||
+        per <= 2L * c || per >= 3L * c || (per - 2L * c) * nblk < c ||
+        (per - 2L * c) * nblk * c > 0x7fffffffL)
+        return 0;
+    *dp = 2 * c;
+    return c;
+}
+
+/* Records and per-tile arrival counters of the balanced attention (G
+ * stream-K workgroups per XCD); the counters are cleared by a fill kernel
+ * when (re)allocated, which happens outside graph capture (the eager pass
+ * before a capture allocates every work buffer), and every launch leaves
+ * them zero. */
+static int attn_skbuf(struct sam_model *m, int G, long tiles, float **rec,
+                      unsigned **cnt)
+{
+    struct hipb_backend *b = m->hip;
+    const int fresh = !m->askcnt || hipb_count(m->askcnt) < (size_t)tiles;
+    int err;
+
+    if (!ensure_typed(b, &m->askrec, (size_t)8 * G * ATTN_SK_REC_FLOATS, HIPB_F32,
+                      "balanced attention records") ||
+        !ensure_typed(b, &m->askcnt, (size_t)tiles, HIPB_F32,
+                      "balanced attention counters"))
+        return 0;
+    if (fresh) {
+        hipb_run_begin(b);
+        err = launch_attn_sk_zero((unsigned *)m->askcnt->ptr, tiles, b->stream);
+        hipb_run_end(b, err, "attn_sk_zero", 0.0);
+        if (hipb_failed())
+            return 0;
+    }
+    *rec = (float *)m->askrec->ptr;
+    *cnt = (unsigned *)m->askcnt->ptr;
+    return 1;
+}
+
 /* The fused attention of attn_fused at head width hd: 64 on both paths,
  * 32 on the bf16 path (operands packed with zero channels 32..63). */
 static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
@@ -603,14 +656,18 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
             return;
         {
             const int ns = attn_splits(b, N, Nk, nb);
-            float *part = attn_part(m, N, nb, ns);
+            int dp;
+            const int G = attn_sk(b, &d, N, Nk, nb, ns, &dp);
+            float *part = attn_part(m, N, nb, ns), *skrec = NULL;
+            unsigned *skcnt = NULL;
 
-            if (ns > 1 && !part)
+            if ((ns > 1 && !part) ||
+                (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
                 return;
             hipb_run_begin(b);
             err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                                   (const float *)m->knorm->ptr, part, ns,
-                                   b->stream);
+                                   (const float *)m->knorm->ptr, part, ns, skrec,
+                                   skcnt, G, dp, b->stream);
             hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)Nk * hd * nb);
         }
         return;
@@ -644,8 +701,9 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     struct hipb_backend *b = m->hip;
     const size_t np = ((size_t)N + 63) / 64 * 64;
     struct attn_desc d;
-    float *part;
-    int err, ns;
+    float *part, *skrec = NULL;
+    unsigned *skcnt = NULL;
+    int err, ns, G, dp;
 
     if (N < 1 || nb < 1 || nb1 < 1) {
         hipb_fatal("attn_packed: invalid shape N=%d nb=%d nb1=%d", N, nb, nb1);
@@ -676,12 +734,15 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.so1 = O.s1;
     d.odt = O.buf->dtype;
     ns = attn_splits(b, N, N, nb);
+    G = attn_sk(b, &d, N, N, nb, ns, &dp);
     part = attn_part(m, N, nb, ns);
-    if (ns > 1 && !part)
+    if ((ns > 1 && !part) ||
+        (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
         return;
     hipb_run_begin(b);
     err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                           (const float *)m->knorm->ptr, part, ns, b->stream);
+                           (const float *)m->knorm->ptr, part, ns, skrec, skcnt,
+                           G, dp, b->stream);
     hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
 }
 
@@ -1314,4 +1375,6 @@ void sam_path_free(struct sam_model *m)
     hipb_release(&m->mlp16);
     hipb_release(&m->abias);
     hipb_release(&m->apart);
+    hipb_release(&m->askrec);
+    hipb_release(&m->askcnt);
 }

@@ -101,7 +101,8 @@ class SamModel(ctypes.Structure):
                             "mlpbuf", "mlp16")] + \
         [("trunk_graph", ctypes.c_void_p), ("trunk_exec", ctypes.c_void_p),
          ("trunk_gen", ctypes.c_ulong), ("abias", Mem),
-         ("apart", Mem), ("dec", ctypes.c_void_p),
+         ("apart", Mem), ("askrec", Mem), ("askcnt", Mem),
+         ("dec", ctypes.c_void_p),
          ("owns_weights", ctypes.c_int)]
 
 

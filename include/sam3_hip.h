@@ -214,6 +214,9 @@ struct sam_model {
     /* Key-split partial records of the bf16 attention ([unit][split][Np]
      * rows of 64 O values, then their (m, l) pairs). */
     hipb_mem apart;
+    /* Stream-K balance of the bf16 attention: piece records and per-tile
+     * arrival counters (launch_attn_bf16's skrec, skcnt). */
+    hipb_mem askrec, askcnt;
     /* The point-prompt mask decoder (sam_dec_init), or NULL. */
     struct sam_decoder *dec;
     /* Set by sam_load: the blocks array, the weights, the rope tables and

@@ -89,13 +89,19 @@ def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
     assert report("ragged N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
 
 
-def test_many_units(hip, be, orc):
-    """80 units of 1024 tokens (5 images x 16 heads, RoPE): 640 query
-    tiles, more workgroups than one per CU on a 256-CU device, every row
-    against the oracle."""
-    N, H, E, imgs = 1024, 16, 1024, 5
+@pytest.mark.parametrize("side,H", [(32, 16), (31, 13)])
+def test_many_units(hip, be, orc, side, H):
+    """5 images x H heads of side^2 tokens (RoPE), every row against the
+    oracle. 32 x 32, 16 heads: 640 query tiles, 80 per XCD of a 256-CU
+    device, between two and three per CU, so the bf16 path takes its
+    balanced launch (two whole tiles per CU, the rest's key blocks shared
+    by one more workgroup per CU). 31 x 31, 13 heads: 520 ragged tiles (65
+    queries in the last, one key in the last block), one tile over the
+    whole ones on every XCD, whose 16 key blocks are fewer than its 32
+    sharing workgroups."""
+    N, E, imgs = side * side, 64 * H, 5
     m = hip.Model(be, embed=E, heads=H)
-    table = orc.rope_table(32)
+    table = orc.rope_table(side)
     qkv = np.random.default_rng(77).standard_normal((imgs * N, 3 * E), np.float32)
     dq, dt = be.upload(qkv), be.upload(table)
     do = be.alloc(imgs * N * E * 4)

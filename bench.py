@@ -50,9 +50,12 @@ WIN_WARM = 1200
 # (KiB per dispatch), each scaled by what the counter reads for the same
 # run's LayerNorm, whose bytes are known exactly (5184 x 1024 fp32 read with
 # gamma and beta, 20744 KiB, against FETCH_SIZE 10470 KiB; 5184 x 1024 bf16
-# written, 10368 KiB, against WRITE_SIZE 10370 KiB). Summary and commands:
+# written, 10368 KiB, against WRITE_SIZE 10370 KiB). Above the operands and
+# O (15650 / 20740 KiB on the plain grid), the balanced launch's piece records
+# of cut tiles, stored and read back with agent-scope atomics, add ~8 MB
+# fetched and ~13 MB written. Summary and commands:
 # profiles/attn_bf16_global_5184.md.
-ATTN_FETCH_KIB, ATTN_WRITE_KIB = 15650.0, 20740.0
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 19801.0, 33808.0
 FETCH_SCALE, WRITE_SCALE = 20744.0 / 10470.0, 10368.0 / 10370.0
 
 

@@ -150,9 +150,14 @@ __device__ void nt_pack_store(const gemm_desc &d, const float *E, int m0, int n0
         }
     }
     else {
+        /* E's V tile is staged with columns XOR 4 ((row / 8) % 8) (see
+         * the staging in k_gemm_nt): the eight rows 8 c8 .. +7 a lane reads
+         * for one channel then sit on banks apart from the other lanes'
+         * rows instead of all on one bank (row stride 132 floats, 8 x 132
+         * = 0 mod 32 banks). */
         for (int pass = 0; pass < 8; pass++) {
             const int ch = 8 * pass + r8;
-            const float *src = E + (rbase + 8 * c8) * LD + hh * 64 + ch;
+            const float *src = E + (rbase + 8 * c8) * LD + ((hh * 64 + ch) ^ (c8 << 2));
             u32x4 pk;
 
             for (int e = 0; e < 4; e++)
@@ -308,6 +313,11 @@ k_gemm_nt(gemm_desc d)
             nt_pack_rope(d, m0, n0, t, rot);
     }
 
+    /* The V third of a packed QKV tile stages its columns XOR 4 ((row / 8)
+     * % 8) for the V^T store's column reads (nt_pack_store); vmask is 0
+     * otherwise. */
+    const int vmask = BM == 128 && BN == 128 && d.pack_N > 0 && n0 >= 2 * d.pack_E ? 0x1c : 0;
+
     /* The activation is chosen once, outside the element loops: a
      * per-element switch on d.act costs more than the K loop's tail. */
     auto stage_out = [&](int c, auto act_c) {
@@ -325,9 +335,14 @@ k_gemm_nt(gemm_desc d)
                 const f32x16 cv = acc[i][j];
 
 #pragma clang loop unroll(full)
-                for (int r = 0; r < 16; r++)
-                    E[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * LD + col] =
+                for (int r = 0; r < 16; r++) {
+                    /* Row rb + 8 (r / 4) + 4 h + r % 4, rb a multiple of 32:
+                     * its (row / 8) % 8 is (rb / 8 + r / 4) % 8. */
+                    const int sw = ((((rb >> 3) + (r >> 2)) & 7) << 2) & vmask;
+
+                    E[(rb + 8 * (r >> 2) + 4 * h + (r & 3)) * LD + (col ^ sw)] =
                         nt_act(d.alpha * cv[r] + bn, ACT);
+                }
             }
         }
     };

@@ -682,13 +682,44 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
     };
     float kn_next = kn[kb0];
 
-    load_block(kb0, 0);
-    for (int s = 0; s < 4; s++) {
-        if (qi < Np)
-            qb[s] = *(const bf16x8 *)(Qu + (long)qi * 64 + 16 * s + 8 * h);
-        else
-            for (int e = 0; e < 8; e++)
-                qb[s][e] = (__bf16)0.0f;
+    /* Q through LDS (not in the bias / causal instance, whose registers
+     * it would spill): the wave's 32 query rows (128 B each) go to slot 1
+     * (free until the first barrier; rows 32 w .. +31 of a 128-row area,
+     * Ks[1] then Vt[1]) by four whole-row copies with K's swizzle, then
+     * into the MFMA B fragments: row l32, logical chunk 2 s + h. A direct
+     * load per fragment touches 32 rows at 32 bytes each per instruction,
+     * four instructions per line, in the start-up burst of every
+     * workgroup (windowed 15.82 -> 15.62 us). Rows past Np read row
+     * Np - 1 (never stored). */
+    if constexpr (!EXT) {
+        const unsigned qlds = (unsigned)(uintptr_t)(wu < 2 ? &Ks[1][32 * wu][0]
+                                                           : &Vt[1][32 * (wu - 2)][0]);
+
+        for (int j = 0; j < 4; j++) {
+            const int row = 32 * w + 8 * j + (l >> 3), chunk = (l & 7) ^ ((row >> 1) & 7);
+            const int qrow = tile * 128 + row < Np ? tile * 128 + row : Np - 1;
+
+            g2lds16_s(Qu, 2u * ((unsigned)qrow * 64u + 8u * chunk), qlds + 1024u * j);
+        }
+        load_block(kb0, 0);
+        /* The Q copies landed (the block's four may still be in flight). */
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+
+        const char *qa = wu < 2 ? (const char *)&Ks[1][32 * wu][0]
+                                : (const char *)&Vt[1][32 * (wu - 2)][0];
+
+        for (int s = 0; s < 4; s++)
+            qb[s] = *(const bf16x8 *)(qa + 128 * l32 + 2 * swz(l32, 2 * s + h));
+    }
+    else {
+        load_block(kb0, 0);
+        for (int s = 0; s < 4; s++) {
+            if (qi < Np)
+                qb[s] = *(const bf16x8 *)(Qu + (long)qi * 64 + 16 * s + 8 * h);
+            else
+                for (int e = 0; e < 8; e++)
+                    qb[s][e] = (__bf16)0.0f;
+        }
     }
     qn = 0.0f;
     for (int s = 0; s < 4; s++)

@@ -210,6 +210,43 @@ def test_gemm_nt_bf16(hip, be16, orc, M, N, K, act, res, cbf):
                   (M, N, K, act, res, cbf), got[rows], want) <= tol
 
 
+@pytest.mark.parametrize("M,N,K,act,res,cbf", [
+    (5184, 4096, 1024, 1, False, True),    # fc1, GELU, bf16 hidden
+    (5184, 1024, 4096, 0, True, False),    # fc2 + residual
+])
+def test_gemm_nt_every_row(hip, be16, orc, M, N, K, act, res, cbf):
+    """The MLP's NT GEMMs at full size: every row against the oracle, and
+    a second launch gives the same bits."""
+    m = model(hip, be16)
+    g = rng(M + 2 * N + K)
+    A = to_bf16(g.standard_normal((M, K), dtype=np.float32))
+    W = to_bf16(g.uniform(-0.06, 0.06, (N, K)).astype(np.float32))
+    bias = g.standard_normal(N, dtype=np.float32)
+    C0 = g.standard_normal((M, N), dtype=np.float32)
+    if cbf:
+        C0 = from_bf16(to_bf16(C0))
+    dA, dW = be16.upload_typed(A, hip.BF16), be16.upload_typed(W, hip.BF16)
+    db = be16.upload(bias)
+
+    def run():
+        dC = be16.upload_typed(to_bf16(C0), hip.BF16) if cbf else be16.upload(C0)
+        hip.linear(m, M, K, N, dA, 0, dW, db, dC, 0, act, int(res))
+        got = be16.read(dC)
+        be16.release(dC)
+        return (from_bf16(got) if cbf else got).reshape(M, N)
+
+    print("gemm_nt every row %dx%dx%d" % (M, N, K), flush=True)
+    first, second = run(), run()
+    assert np.array_equal(first, second)
+    want = orc.linear(from_bf16(A), from_bf16(W), bias, act=act, cpu=False)
+    if res:
+        want = want + C0
+    if cbf:
+        want = from_bf16(to_bf16(want))
+    tol = 1e-2 if cbf else 1e-5
+    assert report("gemm_nt every row %dx%dx%d" % (M, N, K), first, want) <= tol
+
+
 def test_linear_fp16_weights(hip, orc):
     be = hip.Backend(precision="fp16")
     try:

@@ -287,13 +287,26 @@ k_gemm_nt(gemm_desc d)
         }
     };
 
+    /* 128 x 64 tiles are taken where 128 x 128 would give fewer than two
+     * per CU: the launch is one round of three workgroups per CU, whose
+     * waves then issue by progress (prio_by_progress: those behind first)
+     * rather than oldest first, so that a CU's workgroups finish together
+     * (projection 450 -> 466, fc2 690 -> 708 TFLOP/s; the multi-round
+     * 128 x 128 launches gain nothing from it). */
+    constexpr bool PRIO = BM == 128 && BN == 64;
+    int lvl = -1;
+
     load_stage(0, 0);
     for (int ks = 0; ks + 1 < nk; ks += 2) {
+        if (PRIO)
+            prio_by_progress(ks, nk, lvl);
         stage(ks, std::integral_constant<int, 0>());
         stage(ks + 1, std::integral_constant<int, 1>());
     }
     if (nk & 1)
         stage(nk - 1, std::integral_constant<int, 0>());
+    if (PRIO)
+        __builtin_amdgcn_s_setprio(0);
 
     /* Epilogue (store_one, sam3_kernels.cl:306-319), through LDS: in
      * chunks of 64 rows, the waves owning the rows write alpha acc + bias

@@ -913,37 +913,24 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
             return;
         if (t == 0)
             __hip_atomic_store(&sk.cnt[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        /* The pieces are summed in workgroup order, whichever arrived
-         * last, so that the tile's result does not depend on the
-         * arrival order: M = the largest m, then O and l accumulate
-         * 2^(m_r - M) (O_r, l_r) for r = r0 .. r1 (this piece's own from
-         * its registers, the same values as its record). */
-        auto rec_of = [&](int r) { return sk.rec + ((long)slot_of(r) * 4 + w) * 34 * 64 + l; };
-        auto get = [&](const float *pr, int k) {
-            return __hip_atomic_load(pr + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        };
-        float M = -INFINITY;
-
-        for (int r = r0; r <= r1; r++)
-            M = __builtin_fmaxf(M, r == me ? st.m : get(rec_of(r), 32));
-        f32x16 o0 = {}, o1 = {};
-        float lsum = 0.0f;
-
         for (int r = r0; r <= r1; r++) {
-            const float *pr = rec_of(r);
-            const float mr = r == me ? st.m : get(pr, 32);
-            const float c = __builtin_amdgcn_exp2f(mr - M);
+            if (r == me)
+                continue;
+            float *pr = sk.rec + ((long)slot_of(r) * 4 + w) * 34 * 64 + l;
+            auto get = [&](int k) {
+                return __hip_atomic_load(pr + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            };
+            const float mp = get(32), lp = get(33);
+            const float M = __builtin_fmaxf(st.m, mp);
+            const float ca = __builtin_amdgcn_exp2f(st.m - M), cb = __builtin_amdgcn_exp2f(mp - M);
 
             for (int r2 = 0; r2 < 16; r2++) {
-                o0[r2] = fmaf(r == me ? st.o0[r2] : get(pr, r2), c, o0[r2]);
-                o1[r2] = fmaf(r == me ? st.o1[r2] : get(pr, 16 + r2), c, o1[r2]);
+                st.o0[r2] = fmaf(st.o0[r2], ca, get(r2) * cb);
+                st.o1[r2] = fmaf(st.o1[r2], ca, get(16 + r2) * cb);
             }
-            lsum = fmaf(r == me ? st.l : get(pr, 33), c, lsum);
+            st.l = fmaf(st.l, ca, lp * cb);
+            st.m = M;
         }
-        st.o0 = o0;
-        st.o1 = o1;
-        st.l = lsum;
-        st.m = M;
     }
     st.l += __shfl_xor(st.l, 32, 64);
     /* Final O / l, or with key splits the unnormalised O of this split

@@ -114,13 +114,17 @@ def test_many_units(hip, be, orc, side, H):
     got = be.read(do).reshape(imgs * N, E)
     want = _oracle_units(orc, qkv, N, imgs, H, E, table)
     assert report("many units %s" % be.precision, got, want) <= TOL[be.precision]
-    # The balanced launch merges cut tiles in a fixed order, whichever
-    # piece arrives last: a second launch gives the same bits.
+    # A second launch reuses the cut tiles' counters and records (the last
+    # piece to arrive resets its tile's counter). The pieces merge in
+    # arrival order, so the bits of a cut tile may differ in the last
+    # places of fp32 between launches, and no further.
     hip.attn_fused(m, N, imgs * H, H, hip.bmat(dq, 0, 3 * E, st, 64),
                    hip.bmat(dq, E, 3 * E, st, 64),
                    hip.bmat(dq, 2 * E, 3 * E, st, 64),
                    hip.bmat(do, 0, E, N * E, 64), dt, N, 0.125)
-    assert np.array_equal(be.read(do).reshape(imgs * N, E), got)
+    again = be.read(do).reshape(imgs * N, E)
+    assert report("many units again %s" % be.precision, again, want) <= TOL[be.precision]
+    assert np.allclose(again, got, rtol=1e-5, atol=1e-6)
     be.release(dq)
     be.release(dt)
     be.release(do)

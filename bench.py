@@ -55,7 +55,7 @@ WIN_WARM = 1200
 # of cut tiles, stored and read back with agent-scope atomics, add ~8 MB
 # fetched and ~13 MB written. Summary and commands:
 # profiles/attn_bf16_global_5184.md.
-ATTN_FETCH_KIB, ATTN_WRITE_KIB = 19801.0, 33808.0
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 20457.0, 35344.0
 FETCH_SCALE, WRITE_SCALE = 20744.0 / 10470.0, 10368.0 / 10370.0
 
 

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <ctype.h>
+#include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -174,19 +175,25 @@ void hipb_prof_print(void)
 
 /* ------------------------------------------------------------ init */
 
-static int contains_nocase(const char *hay, const char *needle)
+/* Lower-case copy of at most cap - 1 characters of s. */
+static void fold_lower(char *dst, const char *s, size_t cap)
 {
-    size_t n = strlen(needle), i, j;
+    size_t i = 0;
 
-    for (i = 0; hay[i]; i++) {
-        for (j = 0; j < n && hay[i + j]; j++)
-            if (tolower((unsigned char)hay[i + j]) !=
-                tolower((unsigned char)needle[j]))
-                break;
-        if (j == n)
-            return 1;
-    }
-    return n == 0;
+    for (; s[i] && i + 1 < cap; i++)
+        dst[i] = (char)tolower((unsigned char)s[i]);
+    dst[i] = 0;
+}
+
+/* Does the platform name hold `want`, ignoring case? Both folded to
+ * lower case, then a plain substring search; an empty `want` matches. */
+static int name_has(const char *name, const char *want)
+{
+    char a[512], b[512];
+
+    fold_lower(a, name, sizeof a);
+    fold_lower(b, want, sizeof b);
+    return strstr(a, b) != NULL;
 }
 
 const char *hipb_arch_name(int arch)
@@ -234,7 +241,7 @@ void hipb_init(struct hipb_backend *b, const char *device_opt,
 
     if (hipGetDeviceCount(&n) != hipSuccess)
         n = 0;
-    if (platform_opt && !contains_nocase(platform_name, platform_opt))
+    if (platform_opt && !name_has(platform_name, platform_opt))
         n = 0;
     if (n == 0 || dev >= n) {
         hipb_fatal("HIP: no usable %s device found%s%s",
@@ -421,43 +428,40 @@ hipb_mem hipb_upload(struct hipb_backend *b, const void *src, size_t n,
     return m;
 }
 
-/* IEEE binary16, round to nearest even (the storage of precision=fp16). */
+/* IEEE 754 binary16 from binary32, round to nearest, ties to even (the
+ * weight storage of precision=fp16). Worked on the magnitude's bit
+ * pattern: results in binary16's normal range re-bias the exponent
+ * (127 -> 15) and round the 13 dropped mantissa bits by adding
+ * 0xfff plus the kept low bit before the shift (a carry out of the
+ * mantissa moves the exponent up, up to infinity); results below
+ * 2^-14 are whole multiples of binary16's subnormal step 2^-24, so the
+ * magnitude scaled by 2^24 (exact) and rounded to an integer by rintf
+ * (the default mode rounds halves to even) is the subnormal pattern,
+ * 0x400 being the smallest normal one. NaN keeps its upper payload bits
+ * and is made quiet. */
 static uint16_t f32_to_f16(float f)
 {
-    uint32_t x, sign, mant;
-    int exp;
+    uint32_t bits, mag, r;
+    uint16_t sign;
 
-    memcpy(&x, &f, 4);
-    sign = (x >> 16) & 0x8000u;
-    exp = (int)((x >> 23) & 0xff) - 127 + 15;
-    mant = x & 0x7fffffu;
-    if (((x >> 23) & 0xff) == 0xff) /* inf / nan */
-        return (uint16_t)(sign | 0x7c00u | (mant ? 0x200u : 0));
-    if (exp >= 31)
+    memcpy(&bits, &f, 4);
+    sign = (uint16_t)((bits >> 16) & 0x8000u);
+    mag = bits & 0x7fffffffu;
+    if (mag > 0x7f800000u)
+        return (uint16_t)(sign | 0x7e00u | (mag >> 13 & 0x3ffu));
+    /* 65520 = halfway between binary16's largest finite 65504 and 2^16,
+     * which ties to the even 2^16: infinity. */
+    if (mag >= 0x477ff000u)
         return (uint16_t)(sign | 0x7c00u);
-    if (exp <= 0) {
-        uint32_t m, r, half;
-        int shift;
+    if (mag < 0x38800000u) {
+        float a;
 
-        if (exp < -10)
-            return (uint16_t)sign;
-        m = mant | 0x800000u;
-        shift = 14 - exp;
-        r = m >> shift;
-        half = 1u << (shift - 1);
-        if ((m & ((half << 1) - 1)) > half ||
-            ((m & ((half << 1) - 1)) == half && (r & 1)))
-            r++;
-        return (uint16_t)(sign | r);
+        memcpy(&a, &mag, 4);
+        return (uint16_t)(sign | (uint16_t)rintf(a * 0x1p24f));
     }
-    {
-        uint32_t r = ((uint32_t)exp << 10) | (mant >> 13);
-        uint32_t low = mant & 0x1fffu;
-
-        if (low > 0x1000u || (low == 0x1000u && (r & 1)))
-            r++;
-        return (uint16_t)(sign | r);
-    }
+    r = mag - (112u << 23);
+    r += 0x0fffu + ((r >> 13) & 1u);
+    return (uint16_t)(sign | (r >> 13));
 }
 
 /* bfloat16, round to nearest even. */
@@ -472,13 +476,24 @@ static uint16_t f32_to_bf16(float f)
     return (uint16_t)(x >> 16);
 }
 
+void hipb_round_half(const float *src, uint16_t *dst, size_t count, int dtype)
+{
+    size_t i;
+
+    if (dtype == HIPB_F16)
+        for (i = 0; i < count; i++)
+            dst[i] = f32_to_f16(src[i]);
+    else
+        for (i = 0; i < count; i++)
+            dst[i] = f32_to_bf16(src[i]);
+}
+
 hipb_mem hipb_upload_weight(struct hipb_backend *b, const float *src,
                             size_t count, const char *what)
 {
     int dtype = b->fp16w ? HIPB_F16 : b->bf16 ? HIPB_BF16 : HIPB_F32;
     hipb_mem m;
     uint16_t *h;
-    size_t i;
 
     if (dtype == HIPB_F32)
         return hipb_upload(b, src, count * sizeof(float), what);
@@ -486,8 +501,7 @@ hipb_mem hipb_upload_weight(struct hipb_backend *b, const float *src,
     if (!m)
         return NULL;
     h = malloc(count * 2 + 2);
-    for (i = 0; i < count; i++)
-        h[i] = dtype == HIPB_F16 ? f32_to_f16(src[i]) : f32_to_bf16(src[i]);
+    hipb_round_half(src, h, count, dtype);
     hipb_write(b, m, 0, h, count * 2);
     free(h);
     return m;

@@ -692,44 +692,64 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou)
     }
 }
 
+/* Root of pixel i's set, halving the path on the way up. */
+static int hole_root(int *par, int i)
+{
+    while (par[i] != i) {
+        par[i] = par[par[i]];
+        i = par[i];
+    }
+    return i;
+}
+
 /* Background components (v <= 0, 8-connected) of at most max_area pixels
- * of an L x L map become 10 (fill_holes, sam3_model.c:1406-1443). lab and
- * queue hold L^2 ints each. Returns 1 if the map changed. */
-static int fill_holes(float *v, int L, int max_area, int *lab, int *queue)
+ * of an L x L map become 10 (the hole filling of sam3_model.c:1406-1443).
+ * Union-find over one raster pass: each background pixel starts its own
+ * set and joins the sets of its background neighbours already passed
+ * (left, upper left, up, upper right), every set rooted at its smallest
+ * pixel index; a second pass counts each root's pixels and a third fills
+ * the pixels of the small sets. par and cnt hold L^2 ints each (par -1:
+ * foreground). A NaN logit counts as foreground here. Returns 1 if the
+ * map changed. */
+static int fill_holes(float *v, int L, int max_area, int *par, int *cnt)
 {
     const int n = L * L;
     int i, changed = 0;
 
-    memset(lab, 0, n * sizeof(int));
     for (i = 0; i < n; i++) {
-        int sp = 0, j;
+        const int x = i % L;
+        int nb[4], k;
 
-        if (lab[i] || v[i] > 0.0f)
+        par[i] = -1;
+        if (!(v[i] <= 0.0f))
             continue;
-        lab[i] = 1;
-        queue[sp++] = i;
-        /* Breadth first; the queue ends up holding the component. */
-        for (j = 0; j < sp; j++) {
-            const int c = queue[j], cx = c % L, cy = c / L;
-            int dy, dx;
+        par[i] = i;
+        nb[0] = x > 0 ? i - 1 : -1;
+        nb[1] = x > 0 && i >= L ? i - L - 1 : -1;
+        nb[2] = i >= L ? i - L : -1;
+        nb[3] = x + 1 < L && i >= L ? i - L + 1 : -1;
+        for (k = 0; k < 4; k++) {
+            int ra, rb;
 
-            for (dy = -1; dy <= 1; dy++)
-                for (dx = -1; dx <= 1; dx++) {
-                    const int nx = cx + dx, ny = cy + dy;
-
-                    if (nx < 0 || ny < 0 || nx >= L || ny >= L ||
-                        lab[ny * L + nx] || v[ny * L + nx] > 0.0f)
-                        continue;
-                    lab[ny * L + nx] = 1;
-                    queue[sp++] = ny * L + nx;
-                }
-        }
-        if (sp <= max_area) {
-            for (j = 0; j < sp; j++)
-                v[queue[j]] = 10.0f;
-            changed = 1;
+            if (nb[k] < 0 || par[nb[k]] < 0)
+                continue;
+            ra = hole_root(par, i);
+            rb = hole_root(par, nb[k]);
+            if (ra < rb)
+                par[rb] = ra;
+            else if (rb < ra)
+                par[ra] = rb;
         }
     }
+    memset(cnt, 0, (size_t)n * sizeof(int));
+    for (i = 0; i < n; i++)
+        if (par[i] >= 0)
+            cnt[hole_root(par, i)]++;
+    for (i = 0; i < n; i++)
+        if (par[i] >= 0 && cnt[hole_root(par, i)] <= max_area) {
+            v[i] = 10.0f;
+            changed = 1;
+        }
     return changed;
 }
 
@@ -754,18 +774,18 @@ void sam_postprocess(struct sam_model *m, int n, const int *sel, int out_h,
             return;
         }
     if (fill) {
-        int *lab = malloc((size_t)L * L * sizeof(int));
-        int *queue = malloc((size_t)L * L * sizeof(int));
+        int *par = malloc((size_t)L * L * sizeof(int));
+        int *cnt = malloc((size_t)L * L * sizeof(int));
 
         for (i = 0; i < n; i++) {
             float *v = d->h_lowres + (size_t)i * L * L;
 
             hipb_read(m->hip, d->lowres, sel[i] * plane, v, plane);
-            if (fill_holes(v, L, SAM_HOLE, lab, queue))
+            if (fill_holes(v, L, SAM_HOLE, par, cnt))
                 hipb_write(m->hip, d->lowres, sel[i] * plane, v, plane);
         }
-        free(lab);
-        free(queue);
+        free(par);
+        free(cnt);
     }
     if (need > d->mask_cap) {
         hipb_release(&d->mask);

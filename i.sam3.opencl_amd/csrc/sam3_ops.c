@@ -383,7 +383,7 @@ static void mha_run(struct sam_model *m, const char *who, int noalloc, int P,
     /* The reference takes c == 16 for many keys and its float16 vector
      * kernels need c of 16 or 32 (sam3_kernels.cl:527-569). */
     if ((many && c != 16) || dint % DEC_HEADS || (c != 16 && c != 32)) {
-        hipb_fatal("mha: unsupported shape");
+        hipb_fatal("%s: unsupported shape", who);
         return;
     }
     /* The many-keys kernel reads rows as 16-byte vectors. */

@@ -26,7 +26,7 @@ ERR_FATAL, ERR_RECORD = 0, 1
 EXPORTS = [
     "hipb_init", "hipb_arch_name", "hipb_free", "hipb_errstr", "hipb_check",
     "hipb_alloc", "hipb_alloc_typed", "hipb_upload", "hipb_upload_weight",
-    "hipb_is_half", "hipb_write", "hipb_read", "hipb_release", "hipb_finish",
+    "hipb_is_half", "hipb_round_half", "hipb_write", "hipb_read", "hipb_release", "hipb_finish",
     "hipb_copy", "hipb_set_error_mode", "hipb_last_error", "hipb_clear_error",
     "hipb_prof_count", "hipb_prof_entry", "hipb_prof_reset",
     "hipb_prof_print", "hipb_timer_start", "hipb_timer_stop",
@@ -203,6 +203,8 @@ def lib():
     L.hipb_upload_weight.argtypes = [BP, vp, c_size, cp]
     L.hipb_upload_weight.restype = Mem
     L.hipb_is_half.argtypes = [Mem]
+    L.hipb_round_half.argtypes = [vp, vp, c_size, c_int]
+    L.hipb_round_half.restype = None
     L.hipb_write.argtypes = [BP, Mem, c_size, vp, c_size]
     L.hipb_read.argtypes = [BP, Mem, c_size, vp, c_size]
     L.hipb_release.argtypes = [ctypes.POINTER(Mem)]

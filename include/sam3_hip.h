@@ -31,6 +31,7 @@
 #define SAM3_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -121,6 +122,10 @@ hipb_mem hipb_upload(struct hipb_backend *b, const void *src, size_t n,
  * bf16 with precision=bf16, else float (ocl_upload_weight). */
 hipb_mem hipb_upload_weight(struct hipb_backend *b, const float *src,
                             size_t count, const char *what);
+/* The host rounding hipb_upload_weight applies: float to IEEE binary16
+ * (dtype HIPB_F16) or to bfloat16 (HIPB_BF16), round to nearest even;
+ * the reference's is static inside ocl_backend.c:521-557 (f32_to_f16). */
+void hipb_round_half(const float *src, uint16_t *dst, size_t count, int dtype);
 int hipb_is_half(hipb_mem m);                           /* ocl_is_half */
 /* Blocking transfers at byte offsets (ocl_write / ocl_read). */
 void hipb_write(struct hipb_backend *b, hipb_mem dst, size_t off,

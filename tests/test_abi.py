@@ -6,6 +6,8 @@ import ctypes
 import os
 import re
 
+import numpy as np
+
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -100,3 +102,67 @@ def test_error_is_cleared_after_raise(hip):
     with pytest.raises(hip.Sam3HipError):
         hip.Backend(precision="bogus")
     assert hip.lib().hipb_last_error() is None
+
+
+def _round_half(hip, x, dtype):
+    out = np.empty(x.size, np.uint16)
+    hip.lib().hipb_round_half(x.ctypes.data, out.ctypes.data, x.size, dtype)
+    return out
+
+
+def _check_f16(hip, bits):
+    x = bits.view(np.float32)
+    got = _round_half(hip, x, hip.F16)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    bad = (got != want) & ~nan
+    assert not bad.any(), hex(int(bits[np.argmax(bad)]))
+    g = got[nan]
+    assert np.all((g & 0x7c00) == 0x7c00) and np.all(g & 0x3ff)
+    assert np.array_equal(g >> 15, (bits[nan] >> 31).astype(np.uint16))
+
+
+def test_round_half_f16(hip):
+    """hipb_round_half to IEEE binary16 (the host rounding of
+    hipb_upload_weight with precision=fp16) against numpy's float32 ->
+    float16 cast: identical bits for every non-NaN input, a NaN of the
+    same sign for every NaN. Every one of the 2^23 mantissas for each
+    float32 exponent where a case of the conversion lives (zero and
+    subnormal inputs, inputs that round to zero or to binary16 subnormals
+    and up to the smallest normal, the overflow boundary at 65520,
+    infinities and NaNs: biased exponents 0, 101-113, 142-143 and 255),
+    and 2^16 random mantissas of each sign for every exponent."""
+    mant = np.arange(1 << 23, dtype=np.uint32)
+    g = np.random.default_rng(11)
+    full = [0] + list(range(101, 114)) + [142, 143, 255]
+    _check_f16(hip, (np.array(full, np.uint32)[:, None] << 23 | mant[None, :]).ravel())
+    e = np.arange(256, dtype=np.uint32)[:, None]
+    m = g.integers(0, 1 << 23, (256, 1 << 16), dtype=np.uint32)
+    for sign in (0, 1):
+        _check_f16(hip, (np.uint32(sign << 31) | (e << 23) | m).ravel())
+
+
+def test_round_half_bf16(hip):
+    """hipb_round_half to bfloat16: round to nearest even on the upper 16
+    bits (restated in integer numpy arithmetic; NaN stays a NaN of the same
+    sign), for all 2^16 low halves under 1024 upper halves: every upper
+    half next to a class boundary (zero, the largest finite, infinity,
+    NaN, both signs) and random others."""
+    g = np.random.default_rng(12)
+    ups = np.concatenate([
+        np.array([0x0000, 0x0001, 0x007f, 0x0080, 0x3f7f, 0x3f80, 0x7f7e,
+                  0x7f7f, 0x7f80, 0x7f81, 0x7fbf, 0x7fc0, 0x7fff], np.uint32),
+        g.integers(0, 1 << 15, 499, dtype=np.uint32)])
+    ups = np.concatenate([ups, ups | 0x8000])
+    low = np.arange(1 << 16, dtype=np.uint32)
+    bits = ((ups[:, None] << 16) | low[None, :]).ravel()
+    got = _round_half(hip, bits.view(np.float32), hip.BF16)
+    up = bits >> 16
+    rem = bits & 0xffff
+    want = (up + ((rem > 0x8000) | ((rem == 0x8000) & (up & 1 == 1)))).astype(np.uint16)
+    nan = (bits & 0x7fffffff) > 0x7f800000
+    assert np.array_equal(got[~nan], want[~nan])
+    g = got[nan]
+    assert np.all((g & 0x7f80) == 0x7f80) and np.all(g & 0x7f)
+    assert np.array_equal(g >> 15, (bits[nan] >> 31).astype(np.uint16))

@@ -78,12 +78,13 @@ def test_mha_noalloc_matches_mha(hip, orc, precision):
 
 
 def test_mha_noalloc_errors_match_mha(hip):
-    """Shape errors are those of mha (fatal with a message)."""
+    """Shape errors are those of mha (fatal with a message naming the
+    call)."""
     be = hip.Backend(precision="fp32")
     m = hip.Model(be, embed=1024, heads=16)
     d = be.alloc(100 * 256 * 4)
     try:
-        with pytest.raises(hip.Sam3HipError, match="mha: unsupported shape"):
+        with pytest.raises(hip.Sam3HipError, match="mha_noalloc: unsupported shape"):
             hip.mha_noalloc(m, 1, 4, 100, 256, d, 0, d, 0, d, 0, d)
         with pytest.raises(hip.Sam3HipError, match="mha_noalloc: per-prompt strides"):
             hip.mha_noalloc(m, 2, 4, 100, 128, d, 0, d, 100 * 128 + 2, d, 0, d)

@@ -469,6 +469,469 @@ k_gemm_nt(gemm_desc d)
     }
 }
 
+/* ------------------------------------------------------------ big tiles */
+
+/* Wait until at most N_ vector memory operations of this wave are in
+ * flight (the global -> LDS copies of the stages issued after the one
+ * about to be read). */
+template <int N_> __device__ __forceinline__ void nt_vmwait()
+{
+    static_assert(N_ >= 0 && N_ < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+/* Big-tile variant of k_gemm_nt: one workgroup per CU, BM x BN tiles of
+ * NW = (BM / WM) (BN / WN) waves with WN = 64 (a wave's columns are one
+ * 64-wide head of a packed QKV product), K stages of 64 in NSLOT LDS
+ * slots, and fragments read one 16-wide K step ahead: the barrier of
+ * stage ks + 1 sits before the last K step of stage ks, so the next
+ * stage's first fragments load under the current stage's last products
+ * and the copy of stage ks + NSLOT (into the slot stage ks leaves) goes
+ * out right after it. Operand bytes per MFMA from LDS: (WM + WN) / (WM
+ * WN / 1024) x 1 KiB / 16... 0.75 KiB for 128 x 64 waves, 0.83 for 96 x
+ * 64. The epilogue stages each wave's tile in its own share of the freed
+ * slots (fp32, 16-byte chunk c of a row at chunk c ^ (row & 15)) in
+ * passes of PR rows and writes whole rows: 16-byte stores of fp32 (4
+ * columns per lane) or bf16 (8 per lane), the residual read likewise; or
+ * (packed QKV, 256 x 256 tiles) the attention operands of one 64-key
+ * block and head per pass. SCH interleaves one fragment read between
+ * consecutive products (the 4-wave configuration, one wave per SIMD). */
+template <int BM, int BN, int WM, int WN, int NSLOT, bool SCH>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
+k_gemm_nt2(gemm_desc d)
+{
+    constexpr int NW = (BM / WM) * (BN / WN);
+    constexpr int NA = WM / 32, NB = WN / 32, NS = NT_KS / 16;
+    constexpr int ROWS = BM + BN;
+    constexpr int SLOT = ROWS * NT_KS * 2;
+    constexpr int LPW = ROWS / (8 * NW);
+    constexpr int SHARE = NSLOT * SLOT / NW;
+    constexpr int PR = SHARE >= WM * WN * 4 ? WM : SHARE >= 64 * WN * 4 ? 64 : 32;
+    static_assert(ROWS % (8 * NW) == 0 && WN == 64 && WM % PR == 0 && WM % 32 == 0, "shape");
+    static_assert(PR * WN * 4 <= SHARE, "staging");
+    __shared__ __attribute__((aligned(16))) uint16_t S[NSLOT * SLOT / 2];
+    const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5, l32 = l & 31;
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int wm = wu / (BN / WN), wn = wu % (BN / WN);
+    const int tm = (d.M + BM - 1) / BM, tn = (d.N + BN - 1) / BN;
+    const int total = tm * tn, per_xcd = (total + NT_NXCD - 1) / NT_NXCD;
+    /* XCD-aware: XCD x takes tiles [x per_xcd, (x + 1) per_xcd) of an
+     * order that walks groups of four tile rows column by column, so the
+     * tiles an XCD runs at once share a few A and B panels in its L2. */
+    const int tile = (int)(blockIdx.x % NT_NXCD) * per_xcd + (int)(blockIdx.x / NT_NXCD);
+    if (tile >= total)
+        return;
+    constexpr int GR = 4;
+    const int grp = tile / (GR * tn), in = tile - grp * GR * tn;
+    const int rows_g = min(GR, tm - grp * GR);
+    const int m0 = (grp * GR + in % rows_g) * BM, n0 = (in / rows_g) * BN;
+    const char *Ab = (const char *)((const uint16_t *)d.A + d.aoff + (long)m0 * d.lda);
+    const char *Bb = (const char *)((const uint16_t *)d.B + d.boff + (long)n0 * d.ldb);
+    const int nk = d.K / NT_KS;
+    unsigned goff[LPW];
+
+    /* Copy j of wave w fills stage rows 8 (w LPW + j) .. +7 (all of A or
+     * all of B: BM is a multiple of 8); lane i lands on row + i / 8,
+     * physical chunk i % 8, fetching logical chunk (i % 8) ^ ((row >> 1)
+     * & 7). Rows past M or N read the last row (never stored). */
+    for (int j = 0; j < LPW; j++) {
+        const int row = 8 * (wu * LPW + j) + (l >> 3);
+        const int chunk = (l & 7) ^ ((row >> 1) & 7);
+
+        if (row < BM)
+            goff[j] = 2u * ((unsigned)(min(m0 + row, d.M - 1) - m0) * d.lda + 8 * chunk);
+        else
+            goff[j] = 2u * ((unsigned)(min(n0 + row - BM, d.N - 1) - n0) * d.ldb + 8 * chunk);
+    }
+    const unsigned lds0 = (unsigned)(uintptr_t)S + 1024u * LPW * wu;
+    auto load_stage = [&](int ks, int slot) {
+#pragma unroll
+        for (int j = 0; j < LPW; j++)
+            nt_g2lds16_s((8 * (wu * LPW + j) < BM ? Ab : Bb) + 128L * ks, goff[j],
+                         lds0 + (unsigned)SLOT * slot + 1024u * j);
+    };
+    /* Fragment byte offsets per K step s: A rows wm WM + 32 i + l32, B
+     * rows BM + wn WN + 32 j + l32 (i, j add 4096 B; the swizzle depends on
+     * row bits 1..3 only). */
+    unsigned aro[NS], bro[NS];
+    for (int s = 0; s < NS; s++) {
+        const int ra = wm * WM + l32, rb = BM + wn * WN + l32;
+
+        aro[s] = 2u * (ra * NT_KS + nt_swz(ra, 2 * s + h));
+        bro[s] = 2u * (rb * NT_KS + nt_swz(rb, 2 * s + h));
+    }
+    f32x16 acc[NA][NB];
+#pragma unroll
+    for (int i = 0; i < NA; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            acc[i][j] = (f32x16){};
+    const char *Sb = (const char *)S;
+    bf16x8 fa[2][NA], fb[2][NB];
+    auto rd = [&](int ks, int s, int buf) {
+        const char *sl = Sb + SLOT * (ks % NSLOT);
+#pragma unroll
+        for (int i = 0; i < NA; i++)
+            fa[buf][i] = *(const bf16x8 *)(sl + 4096 * i + aro[s]);
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+            fb[buf][j] = *(const bf16x8 *)(sl + 4096 * j + bro[s]);
+    };
+    /* Stage ks landed for this wave: the stages issued after it (at most
+     * NSLOT - 2, fewer near the end) may still be in flight. */
+    auto wait_stage = [&](int ks) {
+        const int young = min(NSLOT - 2, nk - 1 - ks);
+
+        if (young >= NSLOT - 2)
+            nt_vmwait<LPW * (NSLOT - 2)>();
+        else if (young == 1)
+            nt_vmwait<LPW>();
+        else
+            nt_vmwait<0>();
+    };
+
+#pragma unroll
+    for (int s = 0; s < NSLOT - 1; s++)
+        if (s < nk)
+            load_stage(s, s);
+    wait_stage(0);
+    __syncthreads();
+    if (NSLOT - 1 < nk)
+        load_stage(NSLOT - 1, NSLOT - 1);
+    rd(0, 0, 0);
+    for (int ks = 0; ks < nk; ks++) {
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            const int buf = s & 1;
+
+            if (s + 1 < NS)
+                rd(ks, s + 1, buf ^ 1);
+            else if (ks + 1 < nk) {
+                wait_stage(ks + 1);
+                __syncthreads();
+                if (ks + NSLOT < nk)
+                    load_stage(ks + NSLOT, (ks + NSLOT) % NSLOT);
+                rd(ks + 1, 0, buf ^ 1);
+            }
+#pragma unroll
+            for (int i = 0; i < NA; i++)
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[buf][i], fb[buf][j],
+                                                                        acc[i][j], 0, 0, 0);
+            if constexpr (SCH) {
+#pragma unroll
+                for (int q = 0; q < NA + NB; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, NA * NB - NA - NB, 0);
+            }
+        }
+    }
+
+    /* Epilogue. Every wave is past its last fragment read of every slot. */
+    __syncthreads();
+    float *st = (float *)((char *)S + wu * SHARE);
+    const int mw = m0 + wm * WM, nw = n0 + wn * WN;
+    /* Staged element (row, col) of the wave's pass: 16-byte chunk col / 4
+     * of the 256-byte row at chunk (col / 4) ^ (row & 15). */
+    auto sidx = [](int row, int col) { return row * 64 + ((((col >> 2) ^ (row & 15))) << 2) + (col & 3); };
+    /* The raw accumulators of rows [p0, p0 + PR): alpha, the bias and the
+     * activation are applied as the rows are read back (applying them
+     * here would let the compiler hoist every product of alpha out of the
+     * pass loop and spill). */
+    auto stage_pass = [&](int p0) {
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            if (32 * i < p0 || 32 * i >= p0 + PR)
+                continue;
+#pragma unroll
+            for (int j = 0; j < NB; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    st[sidx(32 * i - p0 + 8 * (r >> 2) + 4 * h + (r & 3), 32 * j + l32)] =
+                        acc[i][j][r];
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): the wave's own rows */
+    };
+    /* act(alpha v + bias) for 4 staged columns, the bias values loaded
+     * once per lane before any store (reloading them per row would wait
+     * on memory each time: the stores may alias the bias). */
+    auto finish4 = [&](f32x4 v, f32x4 bv, auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
+        f32x4 o;
+
+        for (int e = 0; e < 4; e++)
+            o[e] = nt_act(d.alpha * v[e] + bv[e], ACT);
+        return o;
+    };
+    auto bias4 = [&](int n) {
+        f32x4 b;
+
+        for (int e = 0; e < 4; e++)
+            b[e] = d.bias && n + e < d.N ? d.bias[n + e] : 0.0f;
+        return b;
+    };
+
+    if constexpr (BM == 256 && BN == 256 && WM == 128) {
+        if (d.pack_N > 0) {
+            /* Packed QKV: the wave's columns are head `head` of one third,
+             * each 64-row pass one 64-key block of one unit (pack_N is a
+             * multiple of 64 and M of pack_N, so a block is whole or past
+             * M). The arithmetic is k_qkv_pack's (same bits). */
+            static_assert(PR == 64, "one key block per pass");
+            const int third = n0 / d.pack_E, heads = d.pack_E / 64, Np = d.pack_N;
+            const int head = (nw - third * d.pack_E) / 64;
+            const int c8 = l & 7, r8 = l >> 3;
+            const f32x4 bq0 = bias4(nw + 8 * c8), bq1 = bias4(nw + 8 * c8 + 4);
+            float bvt[8];
+
+            for (int it = 0; it < 8; it++)
+                bvt[it] = d.bias ? d.bias[nw + 8 * it + r8] : 0.0f;
+
+#pragma unroll
+            for (int p0 = 0; p0 < WM; p0 += 64) {
+                const int mb = mw + p0;
+
+                if (mb >= d.M)
+                    break;
+                stage_pass(p0);
+                const int win = mb / Np, pb = mb - win * Np;
+                const long unit = (long)win * heads + head;
+
+                if (third < 2) {
+                    uint16_t *dst = (uint16_t *)(third == 0 ? d.pack_q16 : d.pack_k16) +
+                                    (unit * Np + pb) * 64 + 8 * c8;
+                    float mx = 0.0f; /* largest row |k|^2 of the bf16 values */
+
+                    for (int it = 0; it < 8; it++) {
+                        const int row = 8 * it + r8;
+                        const f32x4 x0 = finish4(*(const f32x4 *)&st[sidx(row, 8 * c8)], bq0,
+                                                 std::integral_constant<int, ACT_NONE_K>());
+                        const f32x4 x1 = finish4(*(const f32x4 *)&st[sidx(row, 8 * c8 + 4)], bq1,
+                                                 std::integral_constant<int, ACT_NONE_K>());
+                        float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                        float ps = 0.0f;
+                        u32x4 pk;
+
+                        if (d.pack_rope) {
+                            const int p = pb + row;
+                            const float4 *src = (const float4 *)((const float2 *)d.pack_rope +
+                                                                 (long)(p % d.pack_npos) * 32 + 4 * c8);
+                            const float4 r0 = src[0], r1 = src[1];
+                            const float2 rot[4] = {make_float2(r0.x, r0.y), make_float2(r0.z, r0.w),
+                                                   make_float2(r1.x, r1.y), make_float2(r1.z, r1.w)};
+
+                            for (int jj = 0; jj < 4; jj++) {
+                                const float a = v[2 * jj], b = v[2 * jj + 1];
+
+                                v[2 * jj] = fmaf(a, rot[jj].x, -(b * rot[jj].y));
+                                v[2 * jj + 1] = fmaf(a, rot[jj].y, b * rot[jj].x);
+                            }
+                        }
+                        if (third == 0)
+                            for (int e = 0; e < 8; e++)
+                                v[e] *= d.pack_scale * LOG2E_F;
+                        for (int e = 0; e < 4; e++) {
+                            pk[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+                            if (third == 1) {
+                                const uint32_t u = pk[e];
+                                const float lo = __builtin_bit_cast(float, u << 16),
+                                            hi = __builtin_bit_cast(float, u & 0xffff0000u);
+
+                                ps = fmaf(hi, hi, fmaf(lo, lo, ps));
+                            }
+                        }
+                        *(u32x4 *)(dst + (long)row * 64) = pk;
+                        if (third == 1) {
+                            ps += __shfl_xor(ps, 1, 64);
+                            ps += __shfl_xor(ps, 2, 64);
+                            ps += __shfl_xor(ps, 4, 64);
+                            mx = fmaxf(mx, ps);
+                        }
+                    }
+                    if (third == 1) {
+                        mx = wave_max(mx);
+                        if (l == 0)
+                            d.pack_knorm[unit * (Np / 64) + pb / 64] = sqrtf(mx) * (1.0f + 0x1p-10f);
+                    }
+                }
+                else {
+                    /* V^T: lane l takes channel 8 it + l / 8 and keys 8 (l % 8)
+                     * .. +7, read down the staged column (the row swizzle puts
+                     * eight consecutive rows of a column on distinct banks). */
+                    for (int it = 0; it < 8; it++) {
+                        const int ch = 8 * it + r8;
+                        const float bc = bvt[it];
+                        u32x4 pk;
+
+                        for (int e = 0; e < 4; e++)
+                            pk[e] = pack_bf16x2(d.alpha * st[sidx(8 * c8 + 2 * e, ch)] + bc,
+                                                d.alpha * st[sidx(8 * c8 + 2 * e + 1, ch)] + bc);
+                        *(u32x4 *)((uint16_t *)d.pack_vt16 + (unit * 64 + ch) * Np + pb + 8 * c8) = pk;
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+            }
+            return;
+        }
+    }
+
+    /* Generic store: alpha acc + bias -> act, then the residual (R, same
+     * type and layout as C) and the window-unpartition row remap. fp32 C:
+     * lane l writes columns 4 (l % 16) .. +3 of row l / 16 of each 4-row
+     * group; bf16 C: columns 8 (l % 8) .. +7 of row l / 8 of each 8-row
+     * group. 16-byte accesses when aligned, per element otherwise. */
+    const bool f32 = d.cdt == DT_F32;
+    const bool vec = f32 ? ((d.ldc | d.coff | d.roff) & 3) == 0 : ((d.ldc | d.coff | d.roff) & 7) == 0;
+    auto out_row = [&](int m, bool &keep) -> long {
+        long crow = m;
+
+        keep = m < d.M;
+        if (d.unpart_ws > 0) {
+            const int ws = d.unpart_ws, wsz = ws * ws;
+            const int wi = m / wsz, p = m - wi * wsz;
+            const int py = p / ws, wy = wi / d.unpart_nwx;
+            const int y = wy * ws + py, x = (wi - wy * d.unpart_nwx) * ws + (p - py * ws);
+
+            keep = keep && y < d.unpart_H && x < d.unpart_H;
+            crow = (long)y * d.unpart_H + x;
+        }
+        return crow;
+    };
+
+    const f32x4 bg0 = bias4(nw + (f32 ? 4 * (l & 15) : 8 * (l & 7)));
+    const f32x4 bg1 = bias4(nw + 8 * (l & 7) + 4);
+    /* Rows of a pass are stored in batches of row groups whose residual
+     * values are all read before any of the batch's stores: C may alias R
+     * (x += ...), so a load after a store would wait for it. Each element
+     * is read and written by one lane, and a batch's rows are not
+     * another batch's (the window remap is one to one), so reading ahead
+     * is exact. */
+    /* Batch size: 4 row groups when the wave holds 128 accumulators of
+     * later passes (more spill), else 8. */
+    constexpr int BTM = NA * NB >= 8 ? 4 : 8;
+    auto store_pass = [&](int p0, auto act_c) {
+        if (f32) {
+            constexpr int NIT = PR / 4, BT = NIT < BTM ? NIT : BTM;
+#pragma unroll
+            for (int b0 = 0; b0 < NIT; b0 += BT) {
+                f32x4 rv[BT];
+                long ci[BT];
+                bool ok[BT];
+                const int c4 = 4 * (l & 15), n = nw + c4;
+                const bool full = vec && n + 3 < d.N;
+
+#pragma unroll
+                for (int k = 0; k < BT; k++) {
+                    const int row = 4 * (b0 + k) + (l >> 4);
+                    bool keep;
+
+                    ok[k] = false;
+                    if (b0 + k >= NIT) /* a short last batch */
+                        continue;
+                    const long crow = out_row(mw + p0 + row, keep);
+
+                    ok[k] = keep && n < d.N;
+                    ci[k] = crow * d.ldc + n;
+                    rv[k] = (f32x4){};
+                    if (ok[k] && full && d.R)
+                        rv[k] = *(const f32x4 *)((const float *)d.R + d.roff + ci[k]);
+                }
+#pragma unroll
+                for (int k = 0; k < BT; k++) {
+                    if (!ok[k])
+                        continue;
+                    const int row = 4 * (b0 + k) + (l >> 4);
+                    const f32x4 v = finish4(*(const f32x4 *)&st[sidx(row, c4)], bg0, act_c);
+                    float *cp = (float *)d.C + d.coff + ci[k];
+
+                    if (full)
+                        *(f32x4 *)cp = v + rv[k];
+                    else {
+                        const float *rp = d.R ? (const float *)d.R + d.roff + ci[k] : nullptr;
+
+                        for (int e = 0; e < 4 && n + e < d.N; e++)
+                            cp[e] = v[e] + (rp ? rp[e] : 0.0f);
+                    }
+                }
+            }
+        }
+        else {
+            constexpr int NIT = PR / 8, BT = NIT < BTM ? NIT : BTM;
+#pragma unroll
+            for (int b0 = 0; b0 < NIT; b0 += BT) {
+                u32x4 rv[BT];
+                long ci[BT];
+                bool ok[BT];
+                const int c8 = 8 * (l & 7), n = nw + c8;
+                const bool full = vec && n + 7 < d.N;
+
+#pragma unroll
+                for (int k = 0; k < BT; k++) {
+                    const int row = 8 * (b0 + k) + (l >> 3);
+                    bool keep;
+
+                    ok[k] = false;
+                    if (b0 + k >= NIT) /* a short last batch */
+                        continue;
+                    const long crow = out_row(mw + p0 + row, keep);
+
+                    ok[k] = keep && n < d.N;
+                    ci[k] = crow * d.ldc + n;
+                    rv[k] = (u32x4){};
+                    if (ok[k] && full && d.R)
+                        rv[k] = *(const u32x4 *)((const uint16_t *)d.R + d.roff + ci[k]);
+                }
+#pragma unroll
+                for (int k = 0; k < BT; k++) {
+                    if (!ok[k])
+                        continue;
+                    const int row = 8 * (b0 + k) + (l >> 3);
+                    const f32x4 v0 = finish4(*(const f32x4 *)&st[sidx(row, c8)], bg0, act_c);
+                    const f32x4 v1 = finish4(*(const f32x4 *)&st[sidx(row, c8 + 4)], bg1, act_c);
+                    float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                    uint16_t *cp = (uint16_t *)d.C + d.coff + ci[k];
+
+                    if (full) {
+                        u32x4 pk;
+
+                        for (int e = 0; e < 4; e++) {
+                            const float lo = v[2 * e] + __builtin_bit_cast(float, rv[k][e] << 16);
+                            const float hi = v[2 * e + 1] +
+                                             __builtin_bit_cast(float, rv[k][e] & 0xffff0000u);
+
+                            pk[e] = pack_bf16x2(lo, hi);
+                        }
+                        *(u32x4 *)cp = pk;
+                    }
+                    else {
+                        const uint16_t *rp = d.R ? (const uint16_t *)d.R + d.roff + ci[k] : nullptr;
+
+                        for (int e = 0; e < 8 && n + e < d.N; e++)
+                            cp[e] = f2bf(v[e] + (rp ? bf2f(rp[e]) : 0.0f));
+                    }
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int p0 = 0; p0 < WM; p0 += PR) {
+        if (mw + p0 >= d.M)
+            break;
+        stage_pass(p0);
+        if (d.act == ACT_GELU_K)
+            store_pass(p0, std::integral_constant<int, ACT_GELU_K>());
+        else if (d.act == ACT_RELU_K)
+            store_pass(p0, std::integral_constant<int, ACT_RELU_K>());
+        else
+            store_pass(p0, std::integral_constant<int, ACT_NONE_K>());
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+    }
+}
+
 /* The NT kernel applies to unbatched bf16 x bf16 (weights as [N][K])
  * products with K a multiple of 64 and 16-byte aligned rows. */
 extern "C" int gemm_nt_ok(const gemm_desc *d)
@@ -483,15 +946,76 @@ extern "C" int gemm_nt_ok(const gemm_desc *d)
              d->unpart_ws == 0 && d->pack_npos >= 1));
 }
 
+/* Big-tile configuration for d (k_gemm_nt2), or 0 for the k_gemm_nt
+ * tiles: 1 = 256 x 256 (8 waves of 128 x 64), 2 = 192 x 256 (8 waves of
+ * 96 x 64), 3 = 192 x 128 (4 waves of 96 x 64). The packed QKV store
+ * takes 1 when a tile's 256 columns are four heads of one third. Other
+ * products take the configuration of least rounds x tile area / rate
+ * (K-loop rates measured on random operands at M = 5184: 1150, 1070 and
+ * 870 TFLOP/s), if they are large enough to fill the device: either K >=
+ * 2048 or the chosen tiles cover >= 90 % of the CUs. (The attention
+ * projection, N = K = 1024 with an fp32 residual, stays on 128 x 64
+ * tiles, three workgroups per CU: 462 against 396 TFLOP/s.) */
+static int nt2_config(const gemm_desc *d)
+{
+    const long cus = dev_cu_count();
+    static const int bm[4] = {0, 256, 192, 192}, bn[4] = {0, 256, 256, 128};
+    static const double rate[4] = {0.0, 1.0, 0.93, 0.76};
+    int best = 0;
+    double cost = 0.0;
+
+    if (d->pack_N > 0)
+        return d->pack_E % 256 == 0 ? 1 : 0;
+    if ((long)d->M * d->N < (1L << 21) || d->K < 512)
+        return 0;
+    for (int c = 1; c <= 3; c++) {
+        const long tiles = (long)((d->M + bm[c] - 1) / bm[c]) * ((d->N + bn[c] - 1) / bn[c]);
+        const double k = (double)((tiles + cus - 1) / cus) * bm[c] * bn[c] / rate[c];
+
+        if (best == 0 || k < cost) {
+            best = c;
+            cost = k;
+        }
+    }
+    {
+        const long tiles = (long)((d->M + bm[best] - 1) / bm[best]) *
+                           ((d->N + bn[best] - 1) / bn[best]);
+
+        if (d->K < 2048 && tiles * 10 < cus * 9)
+            return 0;
+    }
+    return best;
+}
+
 /* Returns -1 when the NT kernel does not apply, else a hipError_t. */
 extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
 {
     hipStream_t s = (hipStream_t)stream;
     long t256;
-    int bm, bn;
+    int bm, bn, big;
 
     if (!gemm_nt_ok(d))
         return -1;
+    big = nt2_config(d);
+    if (big) {
+        static const int bm2[4] = {0, 256, 192, 192}, bn2[4] = {0, 256, 256, 128};
+        const long tiles = (long)((d->M + bm2[big] - 1) / bm2[big]) *
+                           ((d->N + bn2[big] - 1) / bn2[big]);
+        const long grid = (tiles + NT_NXCD - 1) / NT_NXCD * NT_NXCD;
+
+        if (grid > 0x7fffffffL)
+            return hipErrorInvalidConfiguration;
+        if (big == 1)
+            hipLaunchKernelGGL((k_gemm_nt2<256, 256, 128, 64, 2, false>), dim3((unsigned)grid),
+                               dim3(512), 0, s, *d);
+        else if (big == 2)
+            hipLaunchKernelGGL((k_gemm_nt2<192, 256, 96, 64, 2, false>), dim3((unsigned)grid),
+                               dim3(512), 0, s, *d);
+        else
+            hipLaunchKernelGGL((k_gemm_nt2<192, 128, 96, 64, 3, true>), dim3((unsigned)grid),
+                               dim3(256), 0, s, *d);
+        return hipGetLastError();
+    }
     /* 128 x 128 tiles (4 waves of 64 x 64, two workgroups per CU, so one
      * workgroup's pipeline fill and output drain overlap the other's
      * products); 256 x 256 tiles (8 waves of 128 x 64, half the operand

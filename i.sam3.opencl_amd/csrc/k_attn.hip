@@ -1226,6 +1226,346 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
     }
 }
 
+/* Launch-starved shapes (one 576-token window: 16 units of 9 key blocks)
+ * in one launch: a workgroup of NG WPG waves takes 32 WPG queries of one
+ * unit, and its NG groups of WPG waves take NG contiguous ranges of the
+ * key blocks (double-buffered K / V^T slots per group), in lockstep: each
+ * iteration's barrier serves every group, a group past its last block
+ * only meets the barriers. The groups then meet in LDS: groups 1 .. NG -
+ * 1 leave their per-lane (O^T, m, l), and group 0 scales every group's
+ * (O, l) to the largest m and sums them in group order (the same bits
+ * every launch) before storing O / l. Block body and softmax reference
+ * point as k_attn_bf16's (plain instance: head width 64, no bias, no
+ * causal mask). With RES (at most RESB key blocks) every key block of
+ * the unit stays resident in LDS: each group's copies are all issued at
+ * the start, and iteration i waits only for the copies of its group's
+ * block i (the younger ones may still fly), so no block waits for a
+ * copy issued one block earlier. */
+#define RESB 9
+template <int NG, int WPG, bool RES>
+__global__ __launch_bounds__(64 * NG * WPG) void k_attn_bf16_grp(attn_desc d,
+                                                               const uint16_t *__restrict__ q16,
+                                                               const uint16_t *__restrict__ k16,
+                                                               const uint16_t *__restrict__ vt16,
+                                                               const float *__restrict__ knorm)
+{
+    constexpr int QT = 32 * WPG, CPW = 16 / WPG; /* queries per tile, copies per wave */
+    /* Double-buffered: [group][slot][K, V^T][row][64 bf16], 32 KiB per
+     * group. Resident: [key block][K, V^T][row][64] plus 4 KiB of output
+     * staging per group-0 wave. */
+    constexpr int LDSB = RES ? RESB * 16384 + 4096 * WPG : NG * 32768;
+    __shared__ __attribute__((aligned(16))) char KV[LDSB];
+    const int t = threadIdx.x, l = t & 63, h = l >> 5, l32 = l & 31;
+    const int wu = __builtin_amdgcn_readfirstlane(t >> 6), g = wu / WPG, wl = wu - g * WPG;
+    const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64, Npk = (Nk + 63) / 64 * 64,
+              nblk = Npk / 64;
+    const int ntiles = (N + QT - 1) / QT;
+    const long unit = blockIdx.x / ntiles;
+    const int tile = (int)(blockIdx.x - unit * ntiles);
+    const int kb0 = g * nblk / NG, kb1 = (g + 1) * nblk / NG, iters = (nblk + NG - 1) / NG;
+    const int qi = tile * QT + wl * 32 + l32;
+    const bool idle = tile * QT + wl * 32 >= N;
+    const uint16_t *Ku = k16 + unit * Npk * 64, *Vu = vt16 + unit * 64 * Npk;
+    const float *kn = knorm + unit * nblk;
+    const int krow = kperm(l32);
+    const f32x16 zero16 = {};
+    const char *base = KV + (RES ? 0 : 32768 * g);
+    const unsigned lds_g = (unsigned)(uintptr_t)base;
+    unsigned goffk[CPW], goffv[CPW], ldso[CPW];
+    bool isk[CPW];
+
+    /* Copy c = wl CPW + j of the group's 16 per block: K rows (c < 8) or
+     * V^T rows (c >= 8) 8 (c % 8) .. +7; lane i lands on row + i / 8,
+     * physical chunk i % 8, logical chunk (i % 8) ^ ((row >> 1) & 7). */
+    for (int j = 0; j < CPW; j++) {
+        const int c = wl * CPW + j, row = 8 * (c & 7) + (l >> 3);
+        const int chunk = (l & 7) ^ ((row >> 1) & 7);
+
+        isk[j] = c < 8;
+        goffk[j] = 2u * ((unsigned)row * 64u + 8u * chunk);
+        goffv[j] = 2u * ((unsigned)row * (unsigned)Npk + 8u * chunk);
+        ldso[j] = (c < 8 ? 0u : 8192u) + 1024u * (c & 7);
+    }
+    /* Copies of block kb into 16 KiB area `area` of the group's LDS. */
+    auto load_block = [&](int kb, int area) {
+        for (int j = 0; j < CPW; j++) {
+            if (isk[j])
+                g2lds16_s(Ku + (long)kb * 64 * 64, goffk[j], lds_g + 16384u * area + ldso[j]);
+            else
+                g2lds16_s(Vu + kb * 64, goffv[j], lds_g + 16384u * area + ldso[j]);
+        }
+    };
+    unsigned kro[4], vro[4];
+    for (int i = 0; i < 4; i++) {
+        kro[i] = 2u * (krow * 64 + swz(krow, 2 * i + h));
+        vro[i] = 2u * (l32 * 64 + swz(l32, 2 * i + h));
+    }
+    bf16x8 qb[4];
+    SoftState st;
+    float qn;
+    bool shifted = false;
+    {
+        const int qr = qi < Np ? qi : Np - 1;
+        const uint16_t *Qr = q16 + (unit * Np + qr) * 64;
+
+        for (int s = 0; s < 4; s++)
+            qb[s] = *(const bf16x8 *)(Qr + 16 * s + 8 * h);
+    }
+    if constexpr (RES) {
+        for (int kb = kb0; kb < kb1; kb++)
+            load_block(kb, kb);
+    }
+    else if (kb0 < kb1)
+        load_block(kb0, 0);
+    qn = 0.0f;
+    for (int s = 0; s < 4; s++)
+        for (int e = 0; e < 8; e++)
+            qn = fmaf((float)qb[s][e], (float)qb[s][e], qn);
+    qn = sqrtf(qn + __shfl_xor(qn, 32, 64)) * (1.0f + 0x1p-10f);
+    for (int r = 0; r < 16; r++) {
+        st.o0[r] = 0.0f;
+        st.o1[r] = 0.0f;
+    }
+    st.m = 0.0f;
+    st.l = 0.0f;
+
+    for (int it = 0; it < iters; it++) {
+        const int kb = kb0 + it, slot = it & 1;
+        const bool active = kb < kb1;
+        const float kbound = active ? kn[kb] : 0.0f;
+
+        if constexpr (RES) {
+            /* This wave's copies of the group's later blocks may fly. */
+            const int later = kb1 - 1 - kb;
+
+            if (later >= 2)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * CPW) : "memory");
+            else if (later == 1)
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPW) : "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (!RES && kb + 1 < kb1)
+            load_block(kb + 1, slot ^ 1);
+        if (!active || idle)
+            continue;
+        const char *Kb = base + 16384 * (RES ? kb : slot), *Vb = Kb + 8192;
+        bf16x8 kf[8], vf[8], pb[4];
+        f32x16 s0, s1;
+        const bool check = __ballot(qn * kbound - st.m > SAFE_SPAN) != 0;
+
+        for (int c = 0; c < 2; c++)
+            for (int ds = 0; ds < 4; ds++)
+                kf[4 * c + ds] = *(const bf16x8 *)(Kb + 4096 * c + kro[ds]);
+        for (int t4 = 0; t4 < 4; t4++) {
+            vf[2 * t4] = *(const bf16x8 *)(Vb + vro[t4]);
+            vf[2 * t4 + 1] = *(const bf16x8 *)(Vb + 4096 + vro[t4]);
+        }
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qb[0], zero16, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4], qb[0], zero16, 0, 0, 0);
+        for (int ds = 1; ds < 4; ds++) {
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ds], qb[ds], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[4 + ds], qb[ds], s1, 0, 0, 0);
+        }
+        if (shifted)
+            for (int r = 0; r < 16; r++) {
+                s0[r] -= st.m;
+                s1[r] -= st.m;
+            }
+        if (kb * 64 + 64 > Nk)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 64 + 16 * (r >> 3) + 8 * h + (r & 7);
+
+                s0[r] += key < Nk ? 0.0f : -INFINITY;
+                s1[r] += key + 32 < Nk ? 0.0f : -INFINITY;
+            }
+        if (check) {
+            float mx = max16(s1, max16(s0, -INFINITY));
+
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const bool empty = st.l + __shfl_xor(st.l, 32, 64) == 0.0f;
+            const float mv = mx > SAFE_SPAN || (empty && mx < -SAFE_SPAN && mx != -INFINITY)
+                                 ? mx
+                                 : 0.0f;
+
+            if (__ballot(mv != 0.0f) != 0) {
+                const float corr = __builtin_amdgcn_exp2f(-__builtin_fmaxf(mv, 0.0f));
+
+                st.l *= corr;
+                for (int r = 0; r < 16; r++) {
+                    st.o0[r] *= corr;
+                    st.o1[r] *= corr;
+                    s0[r] -= mv;
+                    s1[r] -= mv;
+                }
+                st.m += mv;
+                shifted = true;
+            }
+        }
+        for (int r = 0; r < 16; r++) {
+            s0[r] = __builtin_amdgcn_exp2f(s0[r]);
+            s1[r] = __builtin_amdgcn_exp2f(s1[r]);
+        }
+        for (int a = 0; a < 2; a++)
+            for (int e = 0; e < 8; e++) {
+                pb[a][e] = (__bf16)s0[8 * a + e];
+                pb[2 + a][e] = (__bf16)s1[8 * a + e];
+            }
+        for (int t4 = 0; t4 < 4; t4++) {
+            st.o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4], pb[t4], st.o0, 0, 0, 0);
+            st.o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[2 * t4 + 1], pb[t4], st.o1, 0, 0, 0);
+        }
+        st.l += sum32(s0, s1);
+    }
+
+    /* Groups 1 .. NG - 1 leave (O^T, m, l) per lane (34 floats, lane-minor)
+     * in the freed slots; group 0 merges them in group order. */
+    __syncthreads();
+    float *ex = (float *)KV;
+    if (g > 0) {
+        float *rec = ex + ((g - 1) * WPG + wl) * 34 * 64 + l;
+
+        for (int r = 0; r < 16; r++) {
+            rec[64 * r] = st.o0[r];
+            rec[64 * (16 + r)] = st.o1[r];
+        }
+        rec[64 * 32] = st.m;
+        rec[64 * 33] = st.l;
+    }
+    __syncthreads();
+    if (g > 0 || idle)
+        return;
+    float M = st.m;
+
+    for (int gg = 1; gg < NG; gg++)
+        M = __builtin_fmaxf(M, ex[((gg - 1) * WPG + wl) * 34 * 64 + 64 * 32 + l]);
+    {
+        const float c0 = __builtin_amdgcn_exp2f(st.m - M);
+
+        for (int r = 0; r < 16; r++) {
+            st.o0[r] *= c0;
+            st.o1[r] *= c0;
+        }
+        st.l *= c0;
+    }
+    for (int gg = 1; gg < NG; gg++) {
+        const float *rec = ex + ((gg - 1) * WPG + wl) * 34 * 64 + l;
+        const float c = __builtin_amdgcn_exp2f(rec[64 * 32] - M);
+
+        for (int r = 0; r < 16; r++) {
+            st.o0[r] = fmaf(rec[64 * r], c, st.o0[r]);
+            st.o1[r] = fmaf(rec[64 * (16 + r)], c, st.o1[r]);
+        }
+        st.l = fmaf(rec[64 * 33], c, st.l);
+    }
+    st.l += __shfl_xor(st.l, 32, 64);
+    const float inv = 1.0f / st.l;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+    const long obase = d.ooff + b0 * d.so0 + b1 * d.so1;
+    const bool f32out = d.odt == DT_F32;
+
+    if ((((obase | (long)d.ldo) & (f32out ? 3 : 7)) | ((uintptr_t)d.O & 15)) == 0) {
+        /* Rows 16-byte aligned: O^T transposed through a 4 KiB staging area
+         * per wave at the end of LDS (past the groups' records), 16-byte
+         * chunk c of staging row r at chunk c ^ (r & 7); 8 lanes write one
+         * 128-byte line of a query row. */
+        char *stg = KV + LDSB - 4096 * (WPG - wl);
+        const int q0 = qi - l32, c = l & 7;
+
+        if (f32out) {
+            for (int half = 0; half < 2; half++) {
+                const f32x16 &o = half ? st.o1 : st.o0;
+                f32x4 v[4];
+
+                for (int gq = 0; gq < 4; gq++) {
+                    const f32x4 x = {o[4 * gq] * inv, o[4 * gq + 1] * inv, o[4 * gq + 2] * inv,
+                                     o[4 * gq + 3] * inv};
+
+                    *(f32x4 *)(stg + 128 * l32 + 16 * ((2 * gq + h) ^ (l32 & 7))) = x;
+                }
+                for (int j = 0; j < 4; j++) {
+                    const int row = 8 * j + (l >> 3);
+
+                    v[j] = *(const f32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
+                }
+                float *ob = (float *)d.O + obase + (long)(q0 + (l >> 3)) * d.ldo + 32 * half + 4 * c;
+
+                for (int j = 0; j < 4; j++)
+                    if (q0 + 8 * j + (l >> 3) < N)
+                        *(f32x4 *)(ob + (long)8 * j * d.ldo) = v[j];
+            }
+        }
+        else {
+            for (int gq = 0; gq < 8; gq++) {
+                const f32x16 &o = gq < 4 ? st.o0 : st.o1;
+                const int r = 4 * (gq & 3);
+                const uint2 pk = {pack_bf16x2(o[r] * inv, o[r + 1] * inv),
+                                  pack_bf16x2(o[r + 2] * inv, o[r + 3] * inv)};
+
+                *(uint2 *)(stg + 128 * l32 + 16 * (gq ^ (l32 & 7)) + 8 * h) = pk;
+            }
+            u32x4 v[4];
+
+            for (int j = 0; j < 4; j++) {
+                const int row = 8 * j + (l >> 3);
+
+                v[j] = *(const u32x4 *)(stg + 128 * row + 16 * (c ^ (row & 7)));
+            }
+            uint16_t *ob = (uint16_t *)d.O + obase + (long)(q0 + (l >> 3)) * d.ldo + 8 * c;
+
+            for (int j = 0; j < 4; j++)
+                if (q0 + 8 * j + (l >> 3) < N)
+                    *(u32x4 *)(ob + (long)8 * j * d.ldo) = v[j];
+        }
+        return;
+    }
+    if (qi >= N)
+        return;
+    const long orow = obase + (long)qi * d.ldo;
+
+    for (int r = 0; r < 16; r++) {
+        const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
+
+        if (d.odt == DT_F32) {
+            ((float *)d.O)[orow + dd] = st.o0[r] * inv;
+            ((float *)d.O)[orow + 32 + dd] = st.o1[r] * inv;
+        }
+        else {
+            ((uint16_t *)d.O)[orow + dd] = f2bf(st.o0[r] * inv);
+            ((uint16_t *)d.O)[orow + 32 + dd] = f2bf(st.o1[r] * inv);
+        }
+    }
+}
+
+/* ng key groups (4: 64-query tiles of 2 waves per group; 2: 128-query
+ * tiles of 4 waves per group); plain attention of head width 64. */
+extern "C" int launch_attn_bf16_grp(const attn_desc *d, const void *q16, const void *k16,
+                                    const void *vt16, const float *knorm, int ng, void *stream)
+{
+    const int nblk = (d->Nk + 63) / 64, qt = ng == 4 ? 64 : 128;
+    const long grid = (long)d->nb * ((d->N + qt - 1) / qt);
+
+    if ((ng != 2 && ng != 4) || nblk < ng || d->Nk < 1 || d->N < 1 || d->hd != 64 ||
+        d->bias || d->causal || grid > 0x7fffffffL)
+        return hipErrorInvalidConfiguration;
+    if (ng == 4 && nblk <= RESB)
+        hipLaunchKernelGGL((k_attn_bf16_grp<4, 2, true>), dim3((unsigned)grid), dim3(512), 0,
+                           (hipStream_t)stream, *d, (const uint16_t *)q16, (const uint16_t *)k16,
+                           (const uint16_t *)vt16, knorm);
+    else if (ng == 4)
+        hipLaunchKernelGGL((k_attn_bf16_grp<4, 2, false>), dim3((unsigned)grid), dim3(512), 0,
+                           (hipStream_t)stream, *d, (const uint16_t *)q16, (const uint16_t *)k16,
+                           (const uint16_t *)vt16, knorm);
+    else
+        hipLaunchKernelGGL((k_attn_bf16_grp<2, 4, false>), dim3((unsigned)grid), dim3(512), 0,
+                           (hipStream_t)stream, *d, (const uint16_t *)q16, (const uint16_t *)k16,
+                           (const uint16_t *)vt16, knorm);
+    return hipGetLastError();
+}
+
 /* Merge of a few key-split partials (nsplit <= 8): 16 threads per
  * (unit, query), four channels each, looping over the splits: M = the
  * largest m_s over splits that saw a key, O = sum w_s o_s / sum w_s l_s

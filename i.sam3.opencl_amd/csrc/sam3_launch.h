@@ -164,6 +164,12 @@ int launch_attn_bf16(const struct attn_desc *d, const void *q16,
                      const void *k16, const void *vt16, const float *knorm,
                      float *part, int nsplit, float *skrec, unsigned *skcnt,
                      int skG, int skdp, void *stream);
+/* The same attention in one launch for shapes with too few query tiles
+ * to fill the device: ng (2 or 4) groups of waves in each workgroup take
+ * contiguous key ranges and merge in LDS (head width 64, no bias or causal
+ * mask, at least ng key blocks). */
+int launch_attn_bf16_grp(const struct attn_desc *d, const void *q16, const void *k16,
+                         const void *vt16, const float *knorm, int ng, void *stream);
 /* Zero the n counters of launch_attn_bf16's balanced launch. */
 int launch_attn_sk_zero(unsigned *cnt, long n, void *stream);
 

@@ -504,6 +504,28 @@ static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
     return ns > 1 ? (int)ns : 1;
 }
 
+/* Key groups inside the workgroup (launch_attn_bf16_grp) for plain
+ * attention that the query tiles alone leave launch-starved (attn_splits
+ * would split the keys): 4 groups of 64-query tiles when those tiles fit
+ * on the CUs at once with two key blocks per group, else 2 groups of
+ * 128-query tiles with two blocks each, else 0 (the split launch and its
+ * merge kernel). One 576-token window of 16 heads: 144 workgroups of four
+ * groups of 2-3 key blocks. */
+static int attn_groups(const struct hipb_backend *b, const struct attn_desc *d, int N,
+                       int Nk, int nb)
+{
+    const int nblk = (Nk + 63) / 64, cus = b->cu_count > 0 ? b->cu_count : 256;
+    const long t64 = (long)nb * ((N + 63) / 64), t128 = (long)nb * ((N + 127) / 128);
+
+    if (d->hd != 64 || d->bias || d->causal || attn_splits(b, N, Nk, nb) <= 1)
+        return 0;
+    if (t64 <= cus && nblk >= 8)
+        return 4;
+    if (t128 <= cus && nblk >= 4)
+        return 2;
+    return 0;
+}
+
 /* Partial records for nsplit key splits: nb nsplit Np (64 + 2) floats. */
 static float *attn_part(struct sam_model *m, int N, int nb, int nsplit)
 {
@@ -655,7 +677,8 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         if (hipb_failed())
             return;
         {
-            const int ns = attn_splits(b, N, Nk, nb);
+            const int ng = attn_groups(b, &d, N, Nk, nb);
+            const int ns = ng ? 1 : attn_splits(b, N, Nk, nb);
             int dp;
             const int G = attn_sk(b, &d, N, Nk, nb, ns, &dp);
             float *part = attn_part(m, N, nb, ns), *skrec = NULL;
@@ -665,15 +688,34 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
                 (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
                 return;
             hipb_run_begin(b);
-            err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                                   (const float *)m->knorm->ptr, part, ns, skrec,
-                                   skcnt, G, dp, b->stream);
+            err = ng ? launch_attn_bf16_grp(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                                            (const float *)m->knorm->ptr, ng, b->stream)
+                     : launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                                        (const float *)m->knorm->ptr, part, ns, skrec,
+                                        skcnt, G, dp, b->stream);
             hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)Nk * hd * nb);
         }
         return;
     }
     {
-        const int ns = attn_splits(b, N, Nk, nb);
+        /* The exact kernel's key blocks are 32 keys: split by those (one
+         * 576-token window of 16 heads: 9 splits of 2 blocks, 720
+         * workgroups, against 4 splits of 64-key blocks: 35.5 against 39.5
+         * us with the merge). */
+        int ns = attn_splits(b, N, Nk, nb);
+
+        if (ns > 1) {
+            const int cus = b->cu_count > 0 ? b->cu_count : 256;
+            const long items = (long)nb * ((N + 127) / 128);
+            long n32 = 3L * cus / items;
+
+            if (n32 > (Nk + 31) / 32 / 2)
+                n32 = (Nk + 31) / 32 / 2;
+            if (n32 > 64)
+                n32 = 64;
+            if (n32 > ns)
+                ns = (int)n32;
+        }
         float *part = attn_part(m, N, nb, ns);
 
         if (ns > 1 && !part)
@@ -703,7 +745,7 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     struct attn_desc d;
     float *part, *skrec = NULL;
     unsigned *skcnt = NULL;
-    int err, ns, G, dp;
+    int err, ns, G, dp, ng;
 
     if (N < 1 || nb < 1 || nb1 < 1) {
         hipb_fatal("attn_packed: invalid shape N=%d nb=%d nb1=%d", N, nb, nb1);
@@ -733,16 +775,19 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     d.so0 = O.s0;
     d.so1 = O.s1;
     d.odt = O.buf->dtype;
-    ns = attn_splits(b, N, N, nb);
+    ng = attn_groups(b, &d, N, N, nb);
+    ns = ng ? 1 : attn_splits(b, N, N, nb);
     G = attn_sk(b, &d, N, N, nb, ns, &dp);
     part = attn_part(m, N, nb, ns);
     if ((ns > 1 && !part) ||
         (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
         return;
     hipb_run_begin(b);
-    err = launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
-                           (const float *)m->knorm->ptr, part, ns, skrec, skcnt,
-                           G, dp, b->stream);
+    err = ng ? launch_attn_bf16_grp(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                                    (const float *)m->knorm->ptr, ng, b->stream)
+             : launch_attn_bf16(&d, m->q16->ptr, m->k16->ptr, m->vt16->ptr,
+                                (const float *)m->knorm->ptr, part, ns, skrec, skcnt,
+                                G, dp, b->stream);
     hipb_run_end(b, err, "attn_bf16", 4.0 * N * (double)N * 64 * nb);
 }
 

@@ -89,6 +89,47 @@ def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
     assert report("ragged N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
 
 
+@pytest.mark.parametrize("N,nunits,H", [(576, 1, 16), (700, 1, 2), (300, 3, 1)])
+def test_grouped_launch(hip, be, orc, N, nunits, H):
+    """Shapes whose query tiles leave the device launch-starved take, on
+    the bf16 path, one launch whose workgroups split the key blocks
+    between groups of waves and merge them in LDS in group order (no
+    partials, no merge kernel): one 576-token window of 16 heads (four
+    groups of 64-query tiles, every key block resident in LDS), 700 tokens
+    (four double-buffered groups; 60 keys in the last block, 60 queries in
+    the last tile) and 300 tokens (two groups of 128-query tiles; 44 keys
+    in the last block). The exact path splits the 32-key blocks across
+    workgroups and merges the partials. Every row against the oracle, and
+    a relaunch gives the same bits."""
+    E = 64 * H
+    m = hip.Model(be, embed=E, heads=H)
+    side = math.isqrt(N)
+    table = orc.rope_table(side) if side * side == N else orc.rope_table(side + 1)[:N]
+    qkv = np.random.default_rng(N + H).standard_normal((nunits * N, 3 * E), np.float32)
+    dq, dt = be.upload(qkv), be.upload(table)
+    do = be.alloc(nunits * N * E * 4)
+    st = N * 3 * E
+    print("grouped N=%d units=%d %s" % (N, nunits * H, be.precision), flush=True)
+
+    def launch():
+        hip.attn_fused(m, N, nunits * H, H, hip.bmat(dq, 0, 3 * E, st, 64),
+                       hip.bmat(dq, E, 3 * E, st, 64),
+                       hip.bmat(dq, 2 * E, 3 * E, st, 64),
+                       hip.bmat(do, 0, E, N * E, 64), dt, N, 0.125)
+        return be.read(do).reshape(nunits * N, E)
+
+    got = launch()
+    if be.precision == "bf16":
+        # No key-split partials were allocated: the grouped launch ran.
+        assert not m.m.apart
+    want = _oracle_units(orc, qkv, N, nunits, H, E, table)
+    assert report("grouped N=%d %s" % (N, be.precision), got, want) <= TOL[be.precision]
+    assert np.array_equal(launch(), got)
+    be.release(dq)
+    be.release(dt)
+    be.release(do)
+
+
 @pytest.mark.parametrize("N,imgs,H,balanced", [
     (1024, 5, 16, True), (961, 5, 13, False), (1795, 1, 37, True),
     (1027, 2, 29, True)])

@@ -487,14 +487,16 @@ template <int N_> __device__ __forceinline__ void nt_vmwait()
  * stage ks + 1 sits before the last K step of stage ks, so the next
  * stage's first fragments load under the current stage's last products
  * and the copy of stage ks + NSLOT (into the slot stage ks leaves) goes
- * out right after it. Operand bytes per MFMA from LDS: (WM + WN) / (WM
- * WN / 1024) x 1 KiB / 16... 0.75 KiB for 128 x 64 waves, 0.83 for 96 x
- * 64. The epilogue stages each wave's tile in its own share of the freed
- * slots (fp32, 16-byte chunk c of a row at chunk c ^ (row & 15)) in
- * passes of PR rows and writes whole rows: 16-byte stores of fp32 (4
- * columns per lane) or bf16 (8 per lane), the residual read likewise; or
- * (packed QKV, 256 x 256 tiles) the attention operands of one 64-key
- * block and head per pass. SCH interleaves one fragment read between
+ * out right after it. A wave's WM / 32 + WN / 32 operand fragments of
+ * 1 KiB per 16-wide K step feed (WM / 32) (WN / 32) MFMAs: 0.75 KiB of LDS
+ * reads per MFMA for 128 x 64 waves, 0.83 KiB for 96 x 64 (1 KiB for the
+ * 64 x 64 waves of k_gemm_nt's 128 x 128 tiles). The epilogue stages each
+ * wave's tile in its own share of the freed slots and writes whole rows
+ * with 16-byte stores: bf16 C in one pass of bf16 rows, fp32 C in passes
+ * of PR rows of fp32 (16-byte chunk c of a row at chunk c ^ (row & 15)),
+ * or (packed QKV, 256 x 256 tiles) the attention operands of one 64-key
+ * block and head per pass. Products with a residual or a window remap
+ * stay on k_gemm_nt. SCH interleaves one fragment read between
  * consecutive products (the 4-wave configuration, one wave per SIMD). */
 template <int BM, int BN, int WM, int WN, int NSLOT, bool SCH>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
@@ -778,145 +780,86 @@ k_gemm_nt2(gemm_desc d)
         }
     }
 
-    /* Generic store: alpha acc + bias -> act, then the residual (R, same
-     * type and layout as C) and the window-unpartition row remap. fp32 C:
-     * lane l writes columns 4 (l % 16) .. +3 of row l / 16 of each 4-row
-     * group; bf16 C: columns 8 (l % 8) .. +7 of row l / 8 of each 8-row
-     * group. 16-byte accesses when aligned, per element otherwise. */
-    const bool f32 = d.cdt == DT_F32;
-    const bool vec = f32 ? ((d.ldc | d.coff | d.roff) & 3) == 0 : ((d.ldc | d.coff | d.roff) & 7) == 0;
-    auto out_row = [&](int m, bool &keep) -> long {
-        long crow = m;
+    /* Generic store (no residual and no window remap: launch_gemm_nt keeps
+     * those products on k_gemm_nt): act(alpha acc + bias) into C. */
+    static_assert(WM * WN * 2 <= SHARE, "one bf16 staging pass");
+    const bool vec = ((d.ldc | d.coff) & (d.cdt == DT_F32 ? 3 : 7)) == 0;
 
-        keep = m < d.M;
-        if (d.unpart_ws > 0) {
-            const int ws = d.unpart_ws, wsz = ws * ws;
-            const int wi = m / wsz, p = m - wi * wsz;
-            const int py = p / ws, wy = wi / d.unpart_nwx;
-            const int y = wy * ws + py, x = (wi - wy * d.unpart_nwx) * ws + (p - py * ws);
+    if (d.cdt != DT_F32) {
+        /* bf16 C: rounded once, staged in one pass as 128-byte rows
+         * (16-byte chunk c of row r at chunk c ^ (r & 7); lanes l and l ^ 1
+         * trade values so each writes two adjacent columns), then 16-byte
+         * stores of whole rows. */
+        uint16_t *sb = (uint16_t *)st;
+        const bool odd = l & 1;
+        auto stage16 = [&](auto act_c) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                const int cl = 32 * j + (l32 & ~1), n = nw + cl;
+                const float b0 = d.bias && n < d.N ? d.bias[n] : 0.0f;
+                const float b1 = d.bias && n + 1 < d.N ? d.bias[n + 1] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < NA; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r += 2) {
+                        /* even lane: rows r, r + 1 of column cl; odd: of cl + 1 */
+                        const float x0 = acc[i][j][r], x1 = acc[i][j][r + 1];
+                        const float got = __shfl_xor(odd ? x0 : x1, 1, 64);
+                        const float lo = odd ? got : x0, hi = odd ? x1 : got;
+                        const int rr = odd ? r + 1 : r;
+                        const int row = 32 * i + 8 * (rr >> 2) + 4 * h + (rr & 3);
 
-            keep = keep && y < d.unpart_H && x < d.unpart_H;
-            crow = (long)y * d.unpart_H + x;
+                        *(uint32_t *)(sb + row * 64 + (((cl >> 3) ^ (row & 7)) << 3) + (cl & 7)) =
+                            pack_bf16x2(nt_act(d.alpha * lo + b0, ACT), nt_act(d.alpha * hi + b1, ACT));
+                    }
+            }
+        };
+        if (d.act == ACT_GELU_K)
+            stage16(std::integral_constant<int, ACT_GELU_K>());
+        else if (d.act == ACT_RELU_K)
+            stage16(std::integral_constant<int, ACT_RELU_K>());
+        else
+            stage16(std::integral_constant<int, ACT_NONE_K>());
+        __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0): the wave's own rows */
+#pragma unroll
+        for (int it = 0; it < WM / 8; it++) {
+            const int row = 8 * it + (l >> 3), c8 = 8 * (l & 7), m = mw + row, n = nw + c8;
+
+            if (m >= d.M || n >= d.N)
+                continue;
+            const u32x4 v = *(const u32x4 *)(sb + row * 64 + (((c8 >> 3) ^ (row & 7)) << 3));
+            uint16_t *cp = (uint16_t *)d.C + d.coff + (long)m * d.ldc + n;
+
+            if (vec && n + 7 < d.N)
+                *(u32x4 *)cp = v;
+            else
+                for (int e = 0; e < 8 && n + e < d.N; e++)
+                    cp[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
         }
-        return crow;
-    };
-
-    const f32x4 bg0 = bias4(nw + (f32 ? 4 * (l & 15) : 8 * (l & 7)));
-    const f32x4 bg1 = bias4(nw + 8 * (l & 7) + 4);
-    /* Rows of a pass are stored in batches of row groups whose residual
-     * values are all read before any of the batch's stores: C may alias R
-     * (x += ...), so a load after a store would wait for it. Each element
-     * is read and written by one lane, and a batch's rows are not
-     * another batch's (the window remap is one to one), so reading ahead
-     * is exact. */
-    /* Batch size: 4 row groups when the wave holds 128 accumulators of
-     * later passes (more spill), else 8. */
-    constexpr int BTM = NA * NB >= 8 ? 4 : 8;
+        return;
+    }
+    /* fp32 C: passes of PR rows of raw accumulators, finished as they are
+     * read back; lane l writes columns 4 (l % 16) .. +3 of row l / 16 of
+     * each 4-row group. */
+    const f32x4 bg = bias4(nw + 4 * (l & 15));
     auto store_pass = [&](int p0, auto act_c) {
-        if (f32) {
-            constexpr int NIT = PR / 4, BT = NIT < BTM ? NIT : BTM;
 #pragma unroll
-            for (int b0 = 0; b0 < NIT; b0 += BT) {
-                f32x4 rv[BT];
-                long ci[BT];
-                bool ok[BT];
-                const int c4 = 4 * (l & 15), n = nw + c4;
-                const bool full = vec && n + 3 < d.N;
+        for (int it = 0; it < PR / 4; it++) {
+            const int row = 4 * it + (l >> 4), c4 = 4 * (l & 15), m = mw + p0 + row, n = nw + c4;
 
-#pragma unroll
-                for (int k = 0; k < BT; k++) {
-                    const int row = 4 * (b0 + k) + (l >> 4);
-                    bool keep;
+            if (m >= d.M || n >= d.N)
+                continue;
+            const f32x4 v = finish4(*(const f32x4 *)&st[sidx(row, c4)], bg, act_c);
+            float *cp = (float *)d.C + d.coff + (long)m * d.ldc + n;
 
-                    ok[k] = false;
-                    if (b0 + k >= NIT) /* a short last batch */
-                        continue;
-                    const long crow = out_row(mw + p0 + row, keep);
-
-                    ok[k] = keep && n < d.N;
-                    ci[k] = crow * d.ldc + n;
-                    rv[k] = (f32x4){};
-                    if (ok[k] && full && d.R)
-                        rv[k] = *(const f32x4 *)((const float *)d.R + d.roff + ci[k]);
-                }
-#pragma unroll
-                for (int k = 0; k < BT; k++) {
-                    if (!ok[k])
-                        continue;
-                    const int row = 4 * (b0 + k) + (l >> 4);
-                    const f32x4 v = finish4(*(const f32x4 *)&st[sidx(row, c4)], bg0, act_c);
-                    float *cp = (float *)d.C + d.coff + ci[k];
-
-                    if (full)
-                        *(f32x4 *)cp = v + rv[k];
-                    else {
-                        const float *rp = d.R ? (const float *)d.R + d.roff + ci[k] : nullptr;
-
-                        for (int e = 0; e < 4 && n + e < d.N; e++)
-                            cp[e] = v[e] + (rp ? rp[e] : 0.0f);
-                    }
-                }
-            }
-        }
-        else {
-            constexpr int NIT = PR / 8, BT = NIT < BTM ? NIT : BTM;
-#pragma unroll
-            for (int b0 = 0; b0 < NIT; b0 += BT) {
-                u32x4 rv[BT];
-                long ci[BT];
-                bool ok[BT];
-                const int c8 = 8 * (l & 7), n = nw + c8;
-                const bool full = vec && n + 7 < d.N;
-
-#pragma unroll
-                for (int k = 0; k < BT; k++) {
-                    const int row = 8 * (b0 + k) + (l >> 3);
-                    bool keep;
-
-                    ok[k] = false;
-                    if (b0 + k >= NIT) /* a short last batch */
-                        continue;
-                    const long crow = out_row(mw + p0 + row, keep);
-
-                    ok[k] = keep && n < d.N;
-                    ci[k] = crow * d.ldc + n;
-                    rv[k] = (u32x4){};
-                    if (ok[k] && full && d.R)
-                        rv[k] = *(const u32x4 *)((const uint16_t *)d.R + d.roff + ci[k]);
-                }
-#pragma unroll
-                for (int k = 0; k < BT; k++) {
-                    if (!ok[k])
-                        continue;
-                    const int row = 8 * (b0 + k) + (l >> 3);
-                    const f32x4 v0 = finish4(*(const f32x4 *)&st[sidx(row, c8)], bg0, act_c);
-                    const f32x4 v1 = finish4(*(const f32x4 *)&st[sidx(row, c8 + 4)], bg1, act_c);
-                    float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                    uint16_t *cp = (uint16_t *)d.C + d.coff + ci[k];
-
-                    if (full) {
-                        u32x4 pk;
-
-                        for (int e = 0; e < 4; e++) {
-                            const float lo = v[2 * e] + __builtin_bit_cast(float, rv[k][e] << 16);
-                            const float hi = v[2 * e + 1] +
-                                             __builtin_bit_cast(float, rv[k][e] & 0xffff0000u);
-
-                            pk[e] = pack_bf16x2(lo, hi);
-                        }
-                        *(u32x4 *)cp = pk;
-                    }
-                    else {
-                        const uint16_t *rp = d.R ? (const uint16_t *)d.R + d.roff + ci[k] : nullptr;
-
-                        for (int e = 0; e < 8 && n + e < d.N; e++)
-                            cp[e] = f2bf(v[e] + (rp ? bf2f(rp[e]) : 0.0f));
-                    }
-                }
-            }
+            if (vec && n + 3 < d.N)
+                *(f32x4 *)cp = v;
+            else
+                for (int e = 0; e < 4 && n + e < d.N; e++)
+                    cp[e] = v[e];
         }
     };
-
 #pragma unroll
     for (int p0 = 0; p0 < WM; p0 += PR) {
         if (mw + p0 >= d.M)
@@ -950,12 +893,13 @@ extern "C" int gemm_nt_ok(const gemm_desc *d)
  * tiles: 1 = 256 x 256 (8 waves of 128 x 64), 2 = 192 x 256 (8 waves of
  * 96 x 64), 3 = 192 x 128 (4 waves of 96 x 64). The packed QKV store
  * takes 1 when a tile's 256 columns are four heads of one third. Other
- * products take the configuration of least rounds x tile area / rate
- * (K-loop rates measured on random operands at M = 5184: 1150, 1070 and
- * 870 TFLOP/s), if they are large enough to fill the device: either K >=
- * 2048 or the chosen tiles cover >= 90 % of the CUs. (The attention
- * projection, N = K = 1024 with an fp32 residual, stays on 128 x 64
- * tiles, three workgroups per CU: 462 against 396 TFLOP/s.) */
+ * products without a residual take the configuration of least rounds x
+ * tile area / rate (K-loop rates measured on random operands at M = 5184:
+ * 1150, 1070 and 870 TFLOP/s), if they are large enough to fill the
+ * device: either K >= 2048 or the chosen tiles cover >= 90 % of the CUs.
+ * On N(0, 1) operands at M = 5184: fc1 (GELU, bf16) 708 against 616
+ * TFLOP/s on the 128 x 128 tiles, the QKV product with fp32 C 707 against
+ * 668. */
 static int nt2_config(const gemm_desc *d)
 {
     const long cus = dev_cu_count();
@@ -966,7 +910,11 @@ static int nt2_config(const gemm_desc *d)
 
     if (d->pack_N > 0)
         return d->pack_E % 256 == 0 ? 1 : 0;
-    if ((long)d->M * d->N < (1L << 21) || d->K < 512)
+    /* A residual (the attention projection and fc2, fp32 x += ...) keeps
+     * the 128 x 64 tiles: three workgroups per CU overlap one's residual
+     * traffic with the others' products (fc2 698 against 681-691 TFLOP/s
+     * with 192 x 128 tiles). */
+    if ((long)d->M * d->N < (1L << 21) || d->K < 512 || d->R)
         return 0;
     for (int c = 1; c <= 3; c++) {
         const long tiles = (long)((d->M + bm[c] - 1) / bm[c]) * ((d->N + bn[c] - 1) / bn[c]);

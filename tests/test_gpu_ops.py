@@ -173,10 +173,11 @@ def from_bf16(u):
     (5184, 1024, 1024, 0, True, False),    # attention projection + residual
     (5184, 4096, 1024, 1, False, True),    # MLP fc1, GELU, bf16 hidden
     (5184, 1024, 4096, 0, True, False),    # MLP fc2 + residual
-    (5000, 3000, 1024, 0, True, False),    # 256 x 256 tiles, ragged edges
+    (5000, 3000, 1024, 0, False, False),   # 256 x 256 tiles, ragged edges
     (5100, 3968, 1024, 1, False, True),    # 192 x 256 tiles, ragged edges
-    (2100, 1000, 2048, 2, True, False),    # 192 x 128 tiles, ragged edges
-    (2100, 1000, 2048, 0, True, True),     # the same, bf16 C and residual
+    (2100, 1000, 2048, 2, False, False),   # 192 x 128 tiles, ragged edges
+    (2100, 1000, 2048, 1, False, True),    # the same, bf16 C
+    (2100, 1000, 2048, 0, True, True),     # 128 x 64 tiles, bf16 C and residual
     (300, 200, 128, 1, True, False),       # ragged tiles on both sides
     (257, 129, 192, 2, True, True),
     (1, 1, 64, 0, False, False),

@@ -16,7 +16,9 @@ path, decoder, mask decoder, text path, backbone), then ~27 ms of the
 global attention region back to back (COND_REGIONS), then the headline's
 W warm-up and K timed launches, so that those K launches (a few ms at
 most) see the engine clock at its loaded steady state instead of its
-ramp from idle (from idle the clock needs 10-20 ms of sustained work).
+ramp from idle (from idle the clock needs 10-20 ms of sustained work);
+the windowed line follows the same protocol with its own block's
+region.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -39,11 +41,11 @@ PEAK_BF16 = 2516.6   # TFLOP/s, dense bf16 MFMA, MI355X
 PEAK_F32 = 157.3     # TFLOP/s, f32 MFMA
 PEAK_HBM = 8000.0    # GB/s
 COPY_BYTES = 256 << 20
-# Replays of the global attention region (~0.18 ms each) that bring the
-# engine clock to its loaded state before the headline's warm-up steps.
+# Replays of a block's attention region (LayerNorm, QKV projection,
+# attention; ~0.18 ms global, ~0.08 ms windowed) that bring the engine
+# clock to its loaded state before a line's warm-up steps: the headline
+# (global) and the windowed line are each conditioned by their own block.
 COND_REGIONS = 150
-# Warm-up launches of the windowed batch before its timed launches (~21 ms).
-WIN_WARM = 1200
 
 # HBM bytes per k_attn_bf16 launch (global, 5184 tokens x 16 heads), from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --kernel-only`
@@ -181,7 +183,7 @@ def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
     random-init weights (Xavier-uniform linears, U(+-1/sqrt(fan_in))
     biases, LayerNorm 1 / 0, position embedding tiled from a 24 x 24
     grid). ms per image for precision=bf16 and =fp32, and the attention
-    kernels' share of a profiled pass."""
+    kernels' share of a pass whose launches are timed in flow."""
     grid, E, H, mlp, ps, depth = 72, 1024, 16, 4096, 14, 32
     glob_at = (7, 15, 23, 31)
     g = np.random.default_rng(17)
@@ -236,10 +238,11 @@ def backbone(hip, steps, warmup, precisions=("bf16", "fp32")):
         # after the image upload).
         hip.sam_trunk_graph(m)
         ms = timed(be, lambda: hip.sam_encode_trunk(m, img), steps, warmup)
-        # One profiled pass (per-operator events, the reference's
-        # I_SAM3_OPENCL_PROFILE table) for the attention share.
+        # One pass with every launch bracketed by events in flow (profile
+        # 2: no wait between launches, as in the eager run) for the
+        # per-kernel times and the attention share.
         hip.prof_reset()
-        be._b.profile = 1
+        be._b.profile = 2
         hip.sam_encode_trunk(m, img)
         be.finish()
         be._b.profile = 0
@@ -463,7 +466,7 @@ def mask_decoder(hip, steps, warmup, precisions=("bf16", "fp32"), P=64,
         ms = timed(be, lambda: dec.decode(pts), steps, warmup)
         dec.graph(P, False)
         hip.prof_reset()
-        be._b.profile = 1
+        be._b.profile = 2
         dec.decode(pts)
         be.finish()
         be._b.profile = 0
@@ -755,16 +758,16 @@ def main():
     # The headline: W warm-up launches, then exactly K timed launches of the
     # global attention, right after the GPU sections above, so the engine
     # clock is at its loaded steady state rather than ramping from idle
-    # within the short timed region; then the windowed batch over the same
-    # GPU time: its launches are a sixth as long, so 6 K timed ones (20
-    # launches of a 19 us kernel are too short a window), after at least
-    # WIN_WARM back-to-back warm-up launches: run alone, the windowed kernel
-    # takes 19.5 us per launch after 30 or 300 of them and 17.3 us after
-    # 1200, its steady state inside the trunk.
+    # within the short timed region; then the windowed batch under the same
+    # protocol: COND_REGIONS replays of its own block's attention region,
+    # W warm-up launches and, its launches being a sixth as long, 6 K timed
+    # ones (20 launches of a 17 us kernel are too short a window).
     ms = timed(be, glob.attn, args.steps, args.warmup)
     tflops = glob.flops() / ms / 1e9
-    win_warm = max(6 * args.warmup, WIN_WARM)
-    wms = timed(be, win.attn, 6 * args.steps, win_warm)
+    for _ in range(COND_REGIONS):
+        win.region()
+    be.finish()
+    wms = timed(be, win.attn, 6 * args.steps, args.warmup)
     # Config 1: one 576-token window (16 heads), the shape the reference's
     # own CPU run takes; and its exact path.
     one = Block(hip, be, 24, seed=1, grid=24)
@@ -805,7 +808,9 @@ def main():
                               "before the W warm-up steps" % COND_REGIONS,
         "windowed": {"workload": "9 windows x 576 tokens, 16 heads x 64, bf16",
                      "ms": round(wms, 5), "launches_timed": 6 * args.steps,
-                     "warmup_launches": win_warm,
+                     "warmup_launches": args.warmup,
+                     "clock_conditioning": "%d replays of the windowed block's "
+                                           "attention region" % COND_REGIONS,
                      "TFLOP/s": round(win.flops() / wms / 1e9, 2),
                      "pct_bf16_peak": round(100 * win.flops() / wms / 1e9 /
                                             PEAK_BF16, 2),

@@ -94,10 +94,54 @@ static double now_ms(void)
     return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
 }
 
+/* profile = 2: every launch is bracketed by two events of a pool on the
+ * stream, without waiting (the kernels run back to back as they would
+ * unprofiled); hipb_finish reads the pairs and adds their durations to
+ * the table. A launch beyond the pool is not timed. */
+#define FLOW_EV 2048
+static void *flow_ev[2 * FLOW_EV];
+static struct {
+    const char *what;
+    double flops;
+} flow_op[FLOW_EV];
+static int nflow;
+
+static void flow_flush(void)
+{
+    int k;
+
+    for (k = 0; k < nflow; k++) {
+        float ms = 0.0f;
+        int i;
+
+        hipEventElapsedTime(&ms, (hipEvent_t)flow_ev[2 * k], (hipEvent_t)flow_ev[2 * k + 1]);
+        for (i = 0; i < nprof && strcmp(prof[i].what, flow_op[k].what) != 0; i++)
+            ;
+        if (i == nprof && nprof < 64)
+            prof[nprof++].what = flow_op[k].what;
+        if (i < 64) {
+            prof[i].ms += ms;
+            prof[i].flops += flow_op[k].flops;
+            prof[i].calls++;
+        }
+    }
+    nflow = 0;
+}
+
 void hipb_run_begin(struct hipb_backend *b)
 {
     if (!b->profile)
         return;
+    if (b->profile == 2) {
+        if (nflow < FLOW_EV) {
+            if (!flow_ev[2 * nflow]) {
+                hipEventCreate((hipEvent_t *)&flow_ev[2 * nflow]);
+                hipEventCreate((hipEvent_t *)&flow_ev[2 * nflow + 1]);
+            }
+            hipEventRecord((hipEvent_t)flow_ev[2 * nflow], (hipStream_t)b->stream);
+        }
+        return;
+    }
     hipStreamSynchronize((hipStream_t)b->stream);
     if (!prof_ev[0]) {
         hipEventCreate((hipEvent_t *)&prof_ev[0]);
@@ -120,6 +164,15 @@ void hipb_run_end(struct hipb_backend *b, int err, const char *what,
     }
     if (!b->profile)
         return;
+    if (b->profile == 2) {
+        if (nflow < FLOW_EV) {
+            hipEventRecord((hipEvent_t)flow_ev[2 * nflow + 1], (hipStream_t)b->stream);
+            flow_op[nflow].what = what;
+            flow_op[nflow].flops = flops;
+            nflow++;
+        }
+        return;
+    }
     hipEventRecord((hipEvent_t)prof_ev[1], (hipStream_t)b->stream);
     hipEventSynchronize((hipEvent_t)prof_ev[1]);
     w1 = now_ms();
@@ -157,6 +210,7 @@ int hipb_prof_entry(int i, const char **what, double *ms, double *wall_ms,
 void hipb_prof_reset(void)
 {
     nprof = 0;
+    nflow = 0;
     memset(prof, 0, sizeof(prof));
 }
 
@@ -525,6 +579,8 @@ void hipb_finish(struct hipb_backend *b)
 {
     hipb_check(hipStreamSynchronize((hipStream_t)b->stream),
                "hipStreamSynchronize");
+    if (b->profile == 2)
+        flow_flush();
 }
 
 void hipb_copy(struct hipb_backend *b, hipb_mem src, hipb_mem dst,

@@ -79,7 +79,10 @@ struct hipb_backend {
     int arch;              /* HIPB_ARCH_DGPU */
     int fp16w;    /* precision=fp16: weight matrices stored as half */
     int bf16;     /* precision=bf16: bf16 MFMA fast path */
-    int profile;  /* per-kernel timing (I_SAM3_OPENCL_PROFILE set) */
+    int profile;  /* per-kernel timing (I_SAM3_OPENCL_PROFILE set): 1 =
+                   * each launch waited for and timed alone (the
+                   * reference's run()), 2 = launches bracketed by event
+                   * pairs without waiting, read at hipb_finish */
     void *stream; /* hipStream_t, default priority, in order */
     void *ev[2];  /* hipEvent_t pair of the region timer */
     void *scratch;          /* backend-owned device scratch (split-K partials) */
@@ -147,7 +150,9 @@ void hipb_clear_error(void);
 
 /* Per-kernel profile, the reference's run() table (sam3_model.c:149-207):
  * with b->profile set every launch is timed with events on the stream
- * and accumulated per kernel name with its algorithmic FLOPs. */
+ * and accumulated per kernel name with its algorithmic FLOPs (profile 2:
+ * the launches run back to back and their times are added up at
+ * hipb_finish; wall_ms stays 0). */
 int hipb_prof_count(void);
 int hipb_prof_entry(int i, const char **what, double *ms, double *wall_ms,
                     double *flops, long *calls);
@@ -372,7 +377,7 @@ void sam_encode_trunk(struct sam_model *m, const float *img);
  * the graph. Weights, rope tables and work buffers are captured by
  * address: re-enable after changing weights; a work-buffer reallocation by
  * any later call drops the graph (later calls run the kernels one by
- * one). Profiling (profile=1) always runs the kernels one by one. No
+ * one). Profiling (profile 1 or 2) always runs the kernels one by one. No
  * counterpart in the reference (whose OpenCL queue has no graphs). */
 void sam_trunk_graph(struct sam_model *m, int enable);
 
@@ -478,7 +483,7 @@ void sam_decode(struct sam_model *m, int P, const float *points, float *iou);
  * sequence for P prompts; sam_decode then replays it (one launch after
  * the token upload) whenever it is called with that P and the backend's
  * scratch has not been reallocated, and runs the kernels one by one
- * otherwise. Profiling (profile=1) always runs them one by one. No
+ * otherwise. Profiling (profile 1 or 2) always runs them one by one. No
  * counterpart in the reference (whose OpenCL queue has no graphs). */
 void sam_dec_graph(struct sam_model *m, int P, int enable);
 

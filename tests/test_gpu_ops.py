@@ -215,6 +215,33 @@ def test_gemm_nt_bf16(hip, be16, orc, M, N, K, act, res, cbf):
                   (M, N, K, act, res, cbf), got[rows], want) <= tol
 
 
+def test_profile_in_flow(hip, be16):
+    """profile 2 brackets each launch with events without waiting: the
+    results are those of an unprofiled run, and hipb_finish adds each
+    launch's time to the per-kernel table (one entry per call)."""
+    m = model(hip, be16)
+    g = rng(5)
+    M, N, K = 512, 384, 256
+    A = be16.upload_typed(to_bf16(g.standard_normal((M, K), dtype=np.float32)), hip.BF16)
+    W = be16.upload_typed(to_bf16(g.uniform(-0.06, 0.06, (N, K)).astype(np.float32)), hip.BF16)
+    b = be16.upload(g.standard_normal(N, dtype=np.float32))
+    C = be16.alloc(M * N * 4)
+    hip.linear(m, M, K, N, A, 0, W, b, C, 0, 0, 0)
+    plain = be16.read(C)
+    hip.prof_reset()
+    be16._b.profile = 2
+    for _ in range(3):
+        hip.linear(m, M, K, N, A, 0, W, b, C, 0, 0, 0)
+    be16.finish()
+    be16._b.profile = 0
+    tab = {r[0]: r for r in hip.prof_table()}
+    assert np.array_equal(be16.read(C), plain)
+    row = tab["gemm_nt_bf16"]
+    assert row[4] == 3 and row[1] > 0.0 and row[3] == 3 * 2.0 * M * N * K
+    for d in (A, W, b, C):
+        be16.release(d)
+
+
 @pytest.mark.parametrize("M,N,K,act,res,cbf", [
     (5184, 4096, 1024, 1, False, True),    # fc1, GELU, bf16 hidden
     (5184, 1024, 4096, 0, True, False),    # fc2 + residual

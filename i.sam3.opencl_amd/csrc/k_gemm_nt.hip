@@ -498,7 +498,7 @@ template <int N_> __device__ __forceinline__ void nt_vmwait()
  * block and head per pass. Products with a residual or a window remap
  * stay on k_gemm_nt. SCH interleaves one fragment read between
  * consecutive products (the 4-wave configuration, one wave per SIMD). */
-template <int BM, int BN, int WM, int WN, int NSLOT, bool SCH>
+template <int BM, int BN, int WM, int WN, int NSLOT, bool SCH, bool PACK = false>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1) void
 k_gemm_nt2(gemm_desc d)
 {
@@ -676,8 +676,9 @@ k_gemm_nt2(gemm_desc d)
         return b;
     };
 
-    if constexpr (BM == 256 && BN == 256 && WM == 128) {
-        if (d.pack_N > 0) {
+    if constexpr (PACK) {
+        static_assert(BM == 256 && BN == 256 && WM == 128, "packed store tiles");
+        {
             /* Packed QKV: the wave's columns are head `head` of one third,
              * each 64-row pass one 64-key block of one unit (pack_N is a
              * multiple of 64 and M of pack_N, so a block is whole or past
@@ -698,15 +699,32 @@ k_gemm_nt2(gemm_desc d)
 
                 if (mb >= d.M)
                     break;
-                stage_pass(p0);
                 const int win = mb / Np, pb = mb - win * Np;
                 const long unit = (long)win * heads + head;
+                stage_pass(p0);
+                /* The pass's RoPE rows (position pb + 8 it + l / 8, pairs
+                 * 4 (l % 8) .. +3), all read before the first is used (once
+                 * the pass's accumulators are staged), so that the row groups
+                 * wait for the table once rather than once each. */
+                f32x4 rv[8][2];
+
+                if (third < 2 && d.pack_rope)
+#pragma unroll
+                    for (int it = 0; it < 8; it++) {
+                        const f32x4 *src = (const f32x4 *)((const float2 *)d.pack_rope +
+                                                           (long)((pb + 8 * it + r8) % d.pack_npos) * 32 +
+                                                           4 * c8);
+
+                        rv[it][0] = src[0];
+                        rv[it][1] = src[1];
+                    }
 
                 if (third < 2) {
                     uint16_t *dst = (uint16_t *)(third == 0 ? d.pack_q16 : d.pack_k16) +
                                     (unit * Np + pb) * 64 + 8 * c8;
                     float mx = 0.0f; /* largest row |k|^2 of the bf16 values */
 
+#pragma unroll
                     for (int it = 0; it < 8; it++) {
                         const int row = 8 * it + r8;
                         const f32x4 x0 = finish4(*(const f32x4 *)&st[sidx(row, 8 * c8)], bq0,
@@ -718,10 +736,7 @@ k_gemm_nt2(gemm_desc d)
                         u32x4 pk;
 
                         if (d.pack_rope) {
-                            const int p = pb + row;
-                            const float4 *src = (const float4 *)((const float2 *)d.pack_rope +
-                                                                 (long)(p % d.pack_npos) * 32 + 4 * c8);
-                            const float4 r0 = src[0], r1 = src[1];
+                            const f32x4 r0 = rv[it][0], r1 = rv[it][1];
                             const float2 rot[4] = {make_float2(r0.x, r0.y), make_float2(r0.z, r0.w),
                                                    make_float2(r1.x, r1.y), make_float2(r1.z, r1.w)};
 
@@ -953,7 +968,10 @@ extern "C" int launch_gemm_nt(const gemm_desc *d, void *stream)
 
         if (grid > 0x7fffffffL)
             return hipErrorInvalidConfiguration;
-        if (big == 1)
+        if (big == 1 && d->pack_N > 0)
+            hipLaunchKernelGGL((k_gemm_nt2<256, 256, 128, 64, 2, false, true>),
+                               dim3((unsigned)grid), dim3(512), 0, s, *d);
+        else if (big == 1)
             hipLaunchKernelGGL((k_gemm_nt2<256, 256, 128, 64, 2, false>), dim3((unsigned)grid),
                                dim3(512), 0, s, *d);
         else if (big == 2)

@@ -493,7 +493,7 @@ template <int N_> __device__ __forceinline__ void nt_vmwait()
  * 64 x 64 waves of k_gemm_nt's 128 x 128 tiles). The epilogue stages each
  * wave's tile in its own share of the freed slots and writes whole rows
  * with 16-byte stores: bf16 C in one pass of bf16 rows, fp32 C in passes
- * of PR rows of fp32 (16-byte chunk c of a row at chunk c ^ (row & 15)),
+ * of PR rows of fp32 (16-byte chunks swizzled by row: sidx),
  * or (packed QKV, 256 x 256 tiles) the attention operands of one 64-key
  * block and head per pass. Products with a residual or a window remap
  * stay on k_gemm_nt. SCH interleaves one fragment read between
@@ -637,8 +637,17 @@ k_gemm_nt2(gemm_desc d)
     float *st = (float *)((char *)S + wu * SHARE);
     const int mw = m0 + wm * WM, nw = n0 + wn * WN;
     /* Staged element (row, col) of the wave's pass: 16-byte chunk col / 4
-     * of the 256-byte row at chunk (col / 4) ^ (row & 15). */
-    auto sidx = [](int row, int col) { return row * 64 + ((((col >> 2) ^ (row & 15))) << 2) + (col & 3); };
+     * of the 256-byte row at chunk (col / 4) ^ sw(row), sw(row) = bit 0 of
+     * row, then bits 3..5 of row with bit 2 of row folded into the top:
+     * the accumulator writes (rows r and r + 4 from the two lane halves,
+     * 32 columns each) fill all 64 banks, two rows of 16-byte reads take
+     * complementary chunks, and the V^T column reads (eight rows 8 apart,
+     * eight columns) touch 64 distinct banks. */
+    auto sidx = [](int row, int col) {
+        const int sw = (row & 1) | ((((row >> 3) & 7) ^ (((row >> 2) & 1) << 2)) << 1);
+
+        return row * 64 + (((col >> 2) ^ sw) << 2) + (col & 3);
+    };
     /* The raw accumulators of rows [p0, p0 + PR): alpha, the bias and the
      * activation are applied as the rows are read back (applying them
      * here would let the compiler hoist every product of alpha out of the
@@ -776,8 +785,8 @@ k_gemm_nt2(gemm_desc d)
                 }
                 else {
                     /* V^T: lane l takes channel 8 it + l / 8 and keys 8 (l % 8)
-                     * .. +7, read down the staged column (the row swizzle puts
-                     * eight consecutive rows of a column on distinct banks). */
+                     * .. +7, read down the staged column (rows 8 apart of eight
+                     * columns: distinct banks under sidx's swizzle). */
                     for (int it = 0; it < 8; it++) {
                         const int ch = 8 * it + r8;
                         const float bc = bvt[it];

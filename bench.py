@@ -49,16 +49,16 @@ COND_REGIONS = 150
 
 # HBM bytes per k_attn_bf16 launch (global, 5184 tokens x 16 heads), from
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --kernel-only`
-# (KiB per dispatch), each scaled by what the counter reads for the same
-# run's LayerNorm, whose bytes are known exactly (5184 x 1024 fp32 read with
-# gamma and beta, 20744 KiB, against FETCH_SIZE 10470 KiB; 5184 x 1024 bf16
-# written, 10368 KiB, against WRITE_SIZE 10370 KiB). Above the operands and
-# O (15650 / 20740 KiB on the plain grid), the balanced launch's piece records
-# of cut tiles, stored and read back with agent-scope atomics, add ~8 MB
-# fetched and ~13 MB written. Summary and commands:
-# profiles/attn_bf16_global_5184.md.
-ATTN_FETCH_KIB, ATTN_WRITE_KIB = 20457.0, 35344.0
-FETCH_SCALE, WRITE_SCALE = 20744.0 / 10470.0, 10368.0 / 10370.0
+# (KiB per dispatch, mean of 5), each scaled by what the counter reads for
+# the same run's LayerNorm, whose bytes are known exactly (5184 x 1024 fp32
+# read with gamma and beta, 20744 KiB, against FETCH_SIZE 10470 KiB; 5184 x
+# 1024 bf16 written, 10368 KiB, against WRITE_SIZE 10368 KiB). Above the
+# operands and O (15650 / 20740 KiB on the plain grid), the balanced
+# launch's piece records of cut tiles, stored and read back with
+# agent-scope atomics, add ~11 MB fetched and ~16 MB written. Summary and
+# commands: profiles/attn_bf16_global_5184.md.
+ATTN_FETCH_KIB, ATTN_WRITE_KIB = 21110.0, 36880.0
+FETCH_SCALE, WRITE_SCALE = 20744.0 / 10470.0, 10368.0 / 10368.0
 
 
 def load_hip():

@@ -160,6 +160,82 @@ def timed(be, fn, steps, warmup):
     return ms / steps
 
 
+def bf16_bits(x):
+    """fp32 -> bf16 storage bits, round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u + ((u >> 16) & 1) + 0x7FFF) >> 16).astype(np.uint16)
+
+
+# The trunk's four GEMM shapes at 72 x 72 tokens (sam_encode_trunk):
+# (rows, in, out, activation, residual add, bf16 output).
+TRUNK_GEMMS = {"qkv": (5184, 1024, 3072, 0, 0, False),
+               "proj": (5184, 1024, 1024, 0, 1, False),
+               "fc1": (5184, 1024, 4096, 1, 0, True),
+               "fc2": (5184, 4096, 1024, 0, 1, False)}
+
+
+def trunk_gemms(hip, steps, warmup, rounds=5):
+    """The trunk's GEMMs through linear() (bf16 operands, fp32 accumulate,
+    the trunk's epilogue: bias, GELU on fc1 with a bf16 store, residual
+    add on the projection and fc2) beside the platform's hipBLASLt
+    (torch.nn.functional.linear, bias only, bf16 out) on the same
+    N(0, 1) operands. The engine clock under MFMA load depends on the
+    data, so both legs see the same random values. Median of `rounds`
+    event-timed runs of `steps` launches each."""
+    import torch
+    torch.cuda.init()     # the shared runtime, initialised through torch first
+    be = hip.Backend(precision="bf16")
+    m = hip.Model(be, embed=128, heads=2)
+    g = np.random.default_rng(0)
+    out = {}
+    for name, (M, K, N, act, res, cbf) in TRUNK_GEMMS.items():
+        a16 = bf16_bits(g.standard_normal((M, K), dtype=np.float32))
+        w16 = bf16_bits(g.standard_normal((N, K), dtype=np.float32))
+        bias = g.standard_normal(N, dtype=np.float32)
+        A = be.upload_typed(a16, hip.BF16)
+        W = be.upload_typed(w16, hip.BF16)
+        B = be.upload(bias)
+        c0 = g.standard_normal((M, N), dtype=np.float32)
+        C = be.upload_typed(bf16_bits(c0), hip.BF16) if cbf else be.upload(c0)
+
+        def lib_call():
+            hip.linear(m, M, K, N, A, 0, W, B, C, 0, act, res)
+
+        fl = 2.0 * M * N * K
+        lib_ms = sorted(timed(be, lib_call, steps, warmup)
+                        for _ in range(rounds))[rounds // 2]
+        for d in (A, W, B, C):
+            be.release(d)
+        ta = torch.from_numpy(a16.view(np.int16)).view(torch.bfloat16).cuda()
+        tw = torch.from_numpy(w16.view(np.int16)).view(torch.bfloat16).cuda()
+        tb = torch.from_numpy(bias).cuda().bfloat16()
+
+        def torch_call():
+            torch.nn.functional.linear(ta, tw, tb)
+
+        ts = []
+        for _ in range(rounds):
+            for _ in range(warmup):
+                torch_call()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                torch_call()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) / steps)
+        t_ms = sorted(ts)[rounds // 2]
+        del ta, tw, tb
+        out[name] = {"shape": [M, K, N], "us": round(1e3 * lib_ms, 2),
+                     "TFLOP/s": round(fl / lib_ms / 1e9, 1),
+                     "hipblaslt_us": round(1e3 * t_ms, 2),
+                     "hipblaslt_TFLOP/s": round(fl / t_ms / 1e9, 1)}
+    m.free()
+    be.free()
+    return out
+
+
 def backbone_flops(grid=72, E=1024, mlp=4096, ps=14, depth=32, ws=24,
                    glob_at=(7, 15, 23, 31)):
     """Algorithmic FLOPs of one image through the trunk: patch GEMM, per
@@ -648,6 +724,8 @@ def main():
     ap.add_argument("--region-only", action="store_true",
                     help="only the global block's attention region: LayerNorm, "
                          "packed QKV projection GEMM, attention (profiling)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the trunk's GEMM shapes beside hipBLASLt")
     ap.add_argument("--checkpoint-only", action="store_true",
                     help="only the checkpoint upload timings")
     ap.add_argument("--precision", choices=("bf16", "fp32"),
@@ -660,6 +738,10 @@ def main():
               "with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
+    if args.gemm_only:
+        # torch before the library: the library's libamdhip64.so.7 then
+        # binds to the runtime torch loaded (one HIP runtime per process).
+        import torch  # noqa: F401
     hip = load_hip()
     if args.backbone_only:
         prec = (args.precision,) if args.precision else ("bf16", "fp32")
@@ -670,6 +752,10 @@ def main():
         prec = (args.precision,) if args.precision else ("bf16", "fp32")
         print(json.dumps({"mask_decoder": mask_decoder(
             hip, args.steps, min(args.warmup, 5), prec)}))
+        return
+    if args.gemm_only:
+        print(json.dumps({"trunk_gemms": trunk_gemms(
+            hip, min(args.steps, 20), min(args.warmup, 30))}))
         return
     if args.checkpoint_only:
         prec = (args.precision,) if args.precision else ("bf16", "fp32")

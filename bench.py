@@ -830,9 +830,8 @@ def main():
         mdec["cpu_oracle"] = mdec_cpu
     text = text_attention(hip, sub_steps, sub_warm)
     bb = backbone(hip, 5, 2)
-    # Clock conditioning: the sections above end in profiled passes (a
-    # synchronisation per kernel) and buffer frees, after which the engine
-    # clock has dropped; from there it takes 10-20 ms of sustained work to
+    # Clock conditioning: the sections above end in host work (reading
+    # profiles, freeing buffers), after which the engine clock has dropped; from there it takes 10-20 ms of sustained work to
     # come back (the global kernel runs 122 us after 5 warm-up launches
     # from idle, 110.6 us after 200). The global block's attention region,
     # replayed back to back for ~27 ms, brings it to its loaded state

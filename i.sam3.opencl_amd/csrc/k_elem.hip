@@ -384,24 +384,29 @@ extern "C" int launch_rope_apply(float *qkv, long rows, int E, int hd,
 /* ------------------------------------------------------------ patches */
 
 /* Patch im2col (sam3_kernels.cl:661-672): row t = ty * grid + tx of out
- * holds the 3 x ps x ps patch at (ty, tx), column c * ps^2 + ky * ps + kx;
- * out is float or bf16 (ydt). One thread per output element, consecutive
+ * (rows ldo apart) holds the 3 x ps x ps patch at (ty, tx), column
+ * c * ps^2 + ky * ps + kx, and zeros from column 3 ps^2 to ldo; out is
+ * float or bf16 (ydt). One thread per output element, consecutive
  * threads along a patch row read consecutive image floats. */
 __global__ __launch_bounds__(256) void k_patch_im2col(
     const float *__restrict__ img, void *__restrict__ out, int ydt,
-    long total, int side, int grid, int ps)
+    long total, int side, int grid, int ps, int ldo)
 {
     const long gid = (long)blockIdx.x * 256 + threadIdx.x;
 
     if (gid >= total)
         return;
     const int K = 3 * ps * ps;
-    const long t = gid / K;
-    const int col = (int)(gid % K);
-    const int c = col / (ps * ps), ky = (col % (ps * ps)) / ps, kx = col % ps;
-    const int ty = (int)(t / grid), tx = (int)(t % grid);
-    const float v = img[((long)c * side + ty * ps + ky) * side + tx * ps + kx];
+    const long t = gid / ldo;
+    const int col = (int)(gid % ldo);
+    float v = 0.0f;
 
+    if (col < K) {
+        const int c = col / (ps * ps), ky = (col % (ps * ps)) / ps, kx = col % ps;
+        const int ty = (int)(t / grid), tx = (int)(t % grid);
+
+        v = img[((long)c * side + ty * ps + ky) * side + tx * ps + kx];
+    }
     if (ydt == DT_BF16)
         ((uint16_t *)out)[gid] = f2bf(v);
     else
@@ -409,13 +414,48 @@ __global__ __launch_bounds__(256) void k_patch_im2col(
 }
 
 extern "C" int launch_patch_im2col(const float *img, void *out, int ydt,
-                                   int side, int grid, int ps, void *stream)
+                                   int side, int grid, int ps, int ldo,
+                                   void *stream)
 {
-    const long total = (long)grid * grid * 3 * ps * ps;
+    const long total = (long)grid * grid * ldo;
 
+    if (ldo < 3 * ps * ps)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_patch_im2col, dim3((total + 255) / 256), dim3(256),
                        0, (hipStream_t)stream, img, out, ydt, total, side,
-                       grid, ps);
+                       grid, ps, ldo);
+    return hipGetLastError();
+}
+
+/* rows x K float or bf16 (sdt) -> rows x KP bf16, columns K .. KP - 1
+ * zero: a weight matrix padded to the NT GEMM's 64-wide K steps. */
+__global__ __launch_bounds__(256) void k_pad_rows_bf16(const void *__restrict__ src, int sdt,
+                                                       uint16_t *__restrict__ dst, long total,
+                                                       int K, int KP)
+{
+    const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+
+    if (gid >= total)
+        return;
+    const long r = gid / KP;
+    const int c = (int)(gid % KP);
+    uint16_t v = 0;
+
+    if (c < K)
+        v = sdt == DT_BF16 ? ((const uint16_t *)src)[r * K + c]
+                           : f2bf(((const float *)src)[r * K + c]);
+    dst[gid] = v;
+}
+
+extern "C" int launch_pad_rows_bf16(const void *src, int sdt, void *dst, long rows, int K,
+                                    int KP, void *stream)
+{
+    const long total = rows * KP;
+
+    if (KP < K || total == 0)
+        return total == 0 ? hipSuccess : hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pad_rows_bf16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, src, sdt, (uint16_t *)dst, total, K, KP);
     return hipGetLastError();
 }
 

@@ -95,9 +95,13 @@ int launch_window_unpartition_add(float *X, const float *Wd, int H, int W,
 int launch_add_bcast(float *out, const float *a, const float *b, long n,
                      long bmod, void *stream);
 /* Patch im2col of a 3 x side x side image into grid^2 rows of 3 ps^2
- * float (ydt DT_F32) or bf16 (DT_BF16) columns. */
+ * float (ydt DT_F32) or bf16 (DT_BF16) columns, rows ldo >= 3 ps^2 apart
+ * with the columns past 3 ps^2 zero. */
 int launch_patch_im2col(const float *img, void *out, int ydt, int side,
-                        int grid, int ps, void *stream);
+                        int grid, int ps, int ldo, void *stream);
+/* rows x K float or bf16 (sdt) into rows x KP bf16, columns K.. zero. */
+int launch_pad_rows_bf16(const void *src, int sdt, void *dst, long rows, int K,
+                         int KP, void *stream);
 
 /* Fused attention over nb units of N tokens, head width 64. */
 struct attn_desc {

@@ -1233,15 +1233,41 @@ static void trunk_kernels(struct sam_model *m)
     int i, err;
 
     /* Patch embedding (no bias), tiled position embedding, ln_pre
-     * (sam3_model.c:1119-1130). */
-    hipb_run_begin(b);
-    err = launch_patch_im2col(m->img->ptr, m->mlpbuf->ptr, HIPB_F32,
-                              (int)side, G, ps, b->stream);
-    hipb_run_end(b, err, "patch_im2col", 0.0);
-    if (hipb_failed())
-        return;
-    linear(m, (int)T, K, E, m->mlpbuf, 0, m->pe_w, NULL, m->x, 0, ACT_NONE,
-           0);
+     * (sam3_model.c:1119-1130). With precision=bf16 the patch columns
+     * (K = 588 at patch 14) and the weight rows are padded with zeros to
+     * a multiple of 64 in the bf16 MLP buffer (free until the first
+     * block's projection), so the product takes the NT GEMM's 64-wide K
+     * steps instead of the general kernel; the zero columns add nothing. */
+    if (b->bf16 && K % 64 != 0 && m->mlp > 0 &&
+        (m->pe_w->dtype == HIPB_BF16 || m->pe_w->dtype == HIPB_F32)) {
+        const int KP = (K + 63) / 64 * 64;
+        const size_t need = (size_t)(T + E) * KP, blk = (size_t)T * (m->mlp > E ? m->mlp : E);
+
+        if (!ensure_bf16(b, &m->mlp16, need > blk ? need : blk, "mlp (bf16)"))
+            return;
+        hipb_run_begin(b);
+        err = launch_patch_im2col(m->img->ptr, m->mlp16->ptr, HIPB_BF16, (int)side, G, ps, KP,
+                                  b->stream);
+        hipb_run_end(b, err, "patch_im2col", 0.0);
+        hipb_run_begin(b);
+        err = launch_pad_rows_bf16(m->pe_w->ptr, m->pe_w->dtype,
+                                   (uint16_t *)m->mlp16->ptr + (size_t)T * KP, E, K, KP,
+                                   b->stream);
+        hipb_run_end(b, err, "pad_rows", 0.0);
+        if (hipb_failed())
+            return;
+        gemm(m, (int)T, E, KP, mat(m->mlp16, 0, KP), mat(m->mlp16, T * KP, KP), 1,
+             mat(m->x, 0, E), 1, 1, NULL, NULL, 0, 1.0f, ACT_NONE);
+    }
+    else {
+        hipb_run_begin(b);
+        err = launch_patch_im2col(m->img->ptr, m->mlpbuf->ptr, HIPB_F32, (int)side, G, ps, K,
+                                  b->stream);
+        hipb_run_end(b, err, "patch_im2col", 0.0);
+        if (hipb_failed())
+            return;
+        linear(m, (int)T, K, E, m->mlpbuf, 0, m->pe_w, NULL, m->x, 0, ACT_NONE, 0);
+    }
     add_bcast(m, m->x, m->x, m->pos, T * E, T * E);
     layernorm(m, T, E, m->x, m->x, m->lnpw, m->lnpb, ENC_EPS, ACT_NONE);
     for (i = 0; i < m->depth && !hipb_failed(); i++)

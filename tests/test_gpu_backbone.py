@@ -81,7 +81,7 @@ def test_vit_block_full_size(hip, be, orc, ws):
                   want) <= TOL[be.precision]
 
 
-def trunk(hip, be, orc, grid, ps, E, heads, mlp, windows, seed):
+def trunk(hip, be, orc, grid, ps, E, heads, mlp, windows, seed, pe_f32=False):
     img, pe_w, pos, lnpw, lnpb, blocks = bc.trunk_case(seed, grid, ps, E, mlp,
                                                        windows)
     blks = [upload_block(hip, be, w) for w in blocks]
@@ -90,7 +90,7 @@ def trunk(hip, be, orc, grid, ps, E, heads, mlp, windows, seed):
     rg = orc.rope_table(grid)
     m = hip.Model(be, grid=grid, embed=E, heads=heads, blocks=blks, mlp=mlp)
     m.m.patch = ps
-    m.m.pe_w = be.upload_weight(pe_w)
+    m.m.pe_w = be.upload(pe_w) if pe_f32 else be.upload_weight(pe_w)
     m.m.pos, m.m.lnpw, m.m.lnpb = be.upload(pos), be.upload(lnpw), be.upload(lnpb)
     if rw is not None:
         m.m.rope_win = be.upload(rw)
@@ -110,6 +110,19 @@ def test_encode_trunk_small(hip, be, orc):
     got, want = trunk(hip, be, orc, 8, 4, 128, 2, 256, [4, 0, 4], 90)
     assert report("trunk small %s" % be.precision, got,
                   want) <= TOL[be.precision]
+
+
+def test_trunk_patch_weight_f32(hip, be, orc):
+    """The patch weight left in float32 storage. With precision=bf16 the
+    patch embedding pads the weight rows to whole 64-wide K steps and
+    rounds them to bf16 in the same copy: the same bits as upload_weight's
+    rounding, so the trunk's output equals the bf16-stored weight's run.
+    With fp32 the exact path takes the float weight either way."""
+    got, want = trunk(hip, be, orc, 8, 4, 128, 2, 256, [4, 0, 4], 92, pe_f32=True)
+    assert report("trunk small, fp32 patch weight %s" % be.precision, got,
+                  want) <= TOL[be.precision]
+    ref, _ = trunk(hip, be, orc, 8, 4, 128, 2, 256, [4, 0, 4], 92)
+    assert np.array_equal(got, ref)
 
 
 def test_trunk_prologue_full_size(hip, be, orc):

@@ -1233,7 +1233,9 @@ static void trunk_kernels(struct sam_model *m)
     int i, err;
 
     /* Patch embedding (no bias), tiled position embedding, ln_pre
-     * (sam3_model.c:1119-1130). With precision=bf16 the patch columns
+     * (sam3_model.c:1119-1130); the position embedding (pos: [T][E], the
+     * tokens' layout) is the product's residual operand, added in its
+     * store as add_bcast would add it. With precision=bf16 the patch columns
      * (K = 588 at patch 14) and the weight rows are padded with zeros to
      * a multiple of 64 in the bf16 MLP buffer (free until the first
      * block's projection), so the product takes the NT GEMM's 64-wide K
@@ -1257,7 +1259,7 @@ static void trunk_kernels(struct sam_model *m)
         if (hipb_failed())
             return;
         gemm(m, (int)T, E, KP, mat(m->mlp16, 0, KP), mat(m->mlp16, T * KP, KP), 1,
-             mat(m->x, 0, E), 1, 1, NULL, NULL, 0, 1.0f, ACT_NONE);
+             mat(m->x, 0, E), 1, 1, NULL, m->pos, 0, 1.0f, ACT_NONE);
     }
     else {
         hipb_run_begin(b);
@@ -1266,9 +1268,9 @@ static void trunk_kernels(struct sam_model *m)
         hipb_run_end(b, err, "patch_im2col", 0.0);
         if (hipb_failed())
             return;
-        linear(m, (int)T, K, E, m->mlpbuf, 0, m->pe_w, NULL, m->x, 0, ACT_NONE, 0);
+        gemm(m, (int)T, E, K, mat(m->mlpbuf, 0, K), mat(m->pe_w, 0, K), 1, mat(m->x, 0, E), 1,
+             1, NULL, m->pos, 0, 1.0f, ACT_NONE);
     }
-    add_bcast(m, m->x, m->x, m->pos, T * E, T * E);
     layernorm(m, T, E, m->x, m->x, m->lnpw, m->lnpb, ENC_EPS, ACT_NONE);
     for (i = 0; i < m->depth && !hipb_failed(); i++)
         vit_block(m, &m->blocks[i], 0);

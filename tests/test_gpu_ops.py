@@ -178,6 +178,8 @@ def from_bf16(u):
     (2100, 1000, 2048, 2, False, False),   # 192 x 128 tiles, ragged edges
     (2100, 1000, 2048, 1, False, True),    # the same, bf16 C
     (2100, 1000, 2048, 0, True, True),     # 128 x 64 tiles, bf16 C and residual
+    (5184, 3072, 2048, 0, True, False),    # residual, long K: 256 x 256 tiles of k_gemm_nt
+    (5184, 3072, 2048, 1, True, True),     # the same with GELU and bf16 C
     (3000, 700, 2048, 0, True, False),     # 128 x 64 tiles, residual, ragged
     (2500, 900, 1024, 1, True, False),     # GELU + residual, ragged
     (300, 200, 128, 1, True, False),       # ragged tiles on both sides

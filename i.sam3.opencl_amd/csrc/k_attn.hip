@@ -1648,12 +1648,23 @@ __global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__
     const float *o = part + ((unit * nsplit) * Np + q) * 64 + c4;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll 4
-    for (int sp = grp; sp < nsplit; sp += 4) {
-        const float w_s = __shfl(wt, sp, 64);
-        const f32x4 v = *(const f32x4 *)(o + (long)sp * Np * 64);
+    /* Every lane runs the same trip count, so that each shuffle sees all
+     * 64 lanes active: a shuffle from an inactive lane reads 0, and with
+     * nsplit % 4 != 0 the groups' own loops would end at different
+     * iterations (the last ones reading a weight held by a group that had
+     * left its loop). Splits past nsplit have weight 0 and load nothing. */
+    const int trips = (nsplit + 3) / 4;
 
-        acc += w_s * v;
+#pragma unroll 4
+    for (int it = 0; it < trips; it++) {
+        const int sp = 4 * it + grp;
+        const float w_s = __shfl(wt, sp, 64);
+
+        if (sp < nsplit) {
+            const f32x4 v = *(const f32x4 *)(o + (long)sp * Np * 64);
+
+            acc += w_s * v;
+        }
     }
     for (int e = 0; e < 4; e++) {
         acc[e] += __shfl_xor(acc[e], 16, 64);

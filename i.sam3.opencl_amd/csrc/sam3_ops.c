@@ -698,10 +698,12 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         return;
     }
     {
-        /* The exact kernel's key blocks are 32 keys: split by those (one
-         * 576-token window of 16 heads: 9 splits of 2 blocks, 720
-         * workgroups, against 4 splits of 64-key blocks: 35.5 against 39.5
-         * us with the merge). */
+        /* The exact kernel's key blocks are 32 keys: split by those, at
+         * least three blocks per split (one 576-token window of 16 heads:
+         * 6 splits of 3 blocks, 480 workgroups, 34.5 us with the merge,
+         * against 9 splits of 2 blocks 35.5 us and 4 splits of 64-key
+         * blocks 39.5 us: fewer workgroups pay the Q load and the first
+         * block's copy, and fewer partials go through the merge). */
         int ns = attn_splits(b, N, Nk, nb);
 
         if (ns > 1) {
@@ -709,8 +711,8 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
             const long items = (long)nb * ((N + 127) / 128);
             long n32 = 3L * cus / items;
 
-            if (n32 > (Nk + 31) / 32 / 2)
-                n32 = (Nk + 31) / 32 / 2;
+            if (n32 > (Nk + 31) / 32 / 3)
+                n32 = (Nk + 31) / 32 / 3;
             if (n32 > 64)
                 n32 = 64;
             if (n32 > ns)

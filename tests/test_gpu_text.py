@@ -150,6 +150,21 @@ def test_long_causal_split_keys(hip, be, orc):
     assert report("long causal %s" % be.precision, got, want) <= TOL[be.precision]
 
 
+def test_key_splits_not_a_multiple_of_four(hip, be, orc):
+    """5700 causal tokens, one head of 64: 45 query tiles split the keys 17
+    ways on both paths (causal attention takes the split launch on bf16
+    too). The merge's four lane groups then take 5, 4, 4 and 4 splits; its
+    weights are shuffled between lanes, which must all be active (a lane
+    that had left its loop would hand over 0 and drop a split)."""
+    n, heads, hd = 5700, 1, 64
+    g = np.random.default_rng(37)
+    Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
+               for _ in range(3))
+    got = _run(hip, be, Q, K, V, heads, hd, causal=True)
+    want = orc.attend(Q, K, V, heads, hd, causal=True)
+    assert report("17 key splits causal %s" % be.precision, got, want) <= TOL[be.precision]
+
+
 def test_one_head_many_key_splits(hip, be, orc):
     """2000 tokens, one head of 64: on the bf16 path 16 query tiles leave
     the GPU idle, so the keys split 15 ways and the wave-per-query merge

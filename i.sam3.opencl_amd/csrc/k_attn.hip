@@ -27,6 +27,16 @@
 
 #include <type_traits>
 
+/* XCDs (L2 domains) of an MI355X: workgroup i of a launch runs on XCD
+ * i % NXCD. */
+#define NXCD 8
+
+/* Word 3 of a raw buffer resource (gfx9: 32-bit data format, no
+ * swizzle), and the sc1 cache policy of the buffer loads and stores that
+ * agent-scope atomics also carry (coherent across the XCDs' L2s). */
+#define BUF_RSRC_DW3 0x00020000
+#define CPOL_SC1 16
+
 /* ------------------------------------------------------------ fp32 path */
 
 /* fp32 operands in the reference row layout (Q/K/V/O opnds of
@@ -43,14 +53,21 @@
  * [unit][N][Nk padded to 64] of dy + dx already summed (k_box_bias with
  * scale 1), added to the scaled score as softmax_ext adds it.
  *
- * With nsplit > 1 the workgroup takes key blocks [kb0, kb1) of split sp
- * (blockIdx.x = tile nsplit + sp) and leaves the unnormalised O, its
- * reference point m (in log2 units) and l in `part`, in k_attn_bf16's
- * record layout, for k_attn_merge(_few). A query none of whose keys the
- * split sees (causal) keeps l = 0 and drops out of the merge. */
-template <int HD, bool EXT>
+ * With nsplit > 1 (the SPLIT instance) the workgroup takes key blocks
+ * [kb0, kb1) of split sp, leaves its per-lane state (O, m in log2 units,
+ * l) in its record of `part` (nb, 128-query tiles, nsplit, 4 waves of
+ * 9216 floats), and counts itself in at cnt[unit][tile]; the tile's last split to arrive
+ * merges every split's state in split order (its own from registers, the
+ * bits of its record: the same result whichever split arrives last),
+ * resets the count for the next launch and stores O. A query none of
+ * whose keys a split sees (causal) has l = 0 there and drops out of the
+ * merge. Records and counts are touched only with the sc1 policy of
+ * agent-scope atomics, which reaches the device's coherent memory rather
+ * than one XCD's L2; waiting for the record stores (vmcnt(0)) before the
+ * count orders them. */
+template <int HD, bool EXT, bool SPLIT>
 __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict__ part,
-                                                  int nsplit)
+                                                  unsigned *__restrict__ cnt, int nsplit)
 {
     __shared__ float Kt[2][HD][33]; /* K^T block: [d][key] */
     __shared__ float Vs[2][32][HD + 8]; /* V block:   [key][d] */
@@ -58,16 +75,29 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
     constexpr int LPR = HD / 8;         /* loader threads per key row */
     const int t = threadIdx.x, l = t & 63, w = t >> 6, h = l >> 5,
               l32 = l & 31;
-    const int N = d.N, Nk = d.Nk, Np = (N + 63) / 64 * 64,
-              Npk = (Nk + 63) / 64 * 64;
-    const int tile = blockIdx.x / nsplit, sp = blockIdx.x - tile * nsplit;
-    const long unit = blockIdx.y;
+    const int N = d.N, Nk = d.Nk, Npk = (Nk + 63) / 64 * 64;
+    /* (unit, tile, split) triples in that order, in NXCD contiguous
+     * ranges, one per XCD: the splits of a tile and the tiles of a unit
+     * share one L2 (their Q rows, K and V blocks). */
+    const int ntiles = (N + 127) / 128;
+    const long total = (long)d.nb * ntiles * nsplit, per = (total + NXCD - 1) / NXCD;
+    const long pos = (long)(blockIdx.x % NXCD) * per + blockIdx.x / NXCD;
+
+    if (pos >= total)
+        return;
+    const long item = pos / nsplit, unit = item / ntiles;
+    const int sp = (int)(pos - item * nsplit), tile = (int)(item - unit * ntiles);
     const long b0 = unit / d.nb1, b1 = unit % d.nb1;
     const float *Qb = (const float *)d.Q + d.qoff + b0 * d.sq0 + b1 * d.sq1;
     const float *Kb = (const float *)d.K + d.koff + b0 * d.sk0 + b1 * d.sk1;
     const float *Vb = (const float *)d.V + d.voff + b0 * d.sv0 + b1 * d.sv1;
     const float2 *cs = (const float2 *)d.rope;
     const int qi = tile * 128 + w * 32 + l32;
+    /* A wave whose 32 queries all lie past N (the tail tile's): its
+     * scores are computed and dropped (a branch around the block's
+     * arithmetic would keep the staging stores from overlapping the P V
+     * product), but it leaves no split record. */
+    const bool idle = tile * 128 + __builtin_amdgcn_readfirstlane(w) * 32 >= N;
     const int nblk = (Nk + 31) / 32;
     const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
     /* This lane's row of the bias table, if any (queries past N read the
@@ -147,28 +177,24 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
             }
     };
 
-    fetch(kb0);
-    stage(0);
-    __syncthreads();
-    int lvl = -1;
-
-    for (int kb = kb0; kb < kb1; kb++) {
-        const int buf = (kb - kb0) & 1;
+    /* S^T = K Q^T of the block in buffer buf (unscaled). */
+    auto qk = [&](int buf) {
         f32x16 s;
-        float mx, m_new, mref, corr, rs = 0.0f;
 
-        prio_by_progress(kb - kb0, kb1 - kb0, lvl);
-
-        if (kb + 1 < kb1)
-            fetch(kb + 1);
         for (int r = 0; r < 16; r++)
             s[r] = 0.0f;
 #pragma unroll
         for (int st = 0; st < HH; st++)
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[buf][st + HH * h][l32],
-                                                     qreg[st], s, 0, 0, 0);
-        /* Scale, mask keys past Nk, the causal mask or the bias, online
-         * softmax. Register r holds key kb 32 + 8 (r / 4) + 4 h + r % 4. */
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Kt[buf][st + HH * h][l32], qreg[st], s, 0,
+                                                     0, 0);
+        return s;
+    };
+    /* Scale, mask keys past Nk, the causal mask or the bias, online
+     * softmax of block kb's scores s, then O^T += V^T P^T from buffer buf.
+     * Register r holds key kb 32 + 8 (r / 4) + 4 h + r % 4. */
+    auto soft_pv = [&](f32x16 s, int kb, int buf) {
+        float mx, m_new, mref, corr, rs = 0.0f;
+
         for (int r = 0; r < 16; r++) {
             const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
 
@@ -214,12 +240,27 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
         for (int st = 0; st < 16; st++) {
             const int key = 8 * (st >> 2) + 4 * h + (st & 3);
 
-            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][l32], s[st],
-                                                      o0, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][l32], s[st], o0, 0, 0, 0);
             if (HD == 64)
-                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][32 + l32],
-                                                          s[st], o1, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][key][32 + l32], s[st], o1, 0,
+                                                          0, 0);
         }
+    };
+
+    fetch(kb0);
+    stage(0);
+    __syncthreads();
+    int lvl = -1;
+
+    /* Two buffers: block kb + 1 is fetched while block kb is used and
+     * staged after it. */
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int buf = (kb - kb0) & 1;
+
+        prio_by_progress(kb - kb0, kb1 - kb0, lvl);
+        if (kb + 1 < kb1)
+            fetch(kb + 1);
+        soft_pv(qk(buf), kb, buf);
         if (kb + 1 < kb1)
             stage(buf ^ 1);
         __syncthreads();
@@ -227,33 +268,130 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
     __builtin_amdgcn_s_setprio(0);
 
     l_run += __shfl_xor(l_run, 32, 64);
-    if (qi >= N)
-        return;
-    if (nsplit > 1) {
-        /* Partial record: O rows of 64 floats (HD columns used), then
-         * (m in log2 units, l). */
-        const long pidx = (unit * nsplit + sp) * (long)Np + qi;
-        float *orow = part + pidx * 64;
+    if constexpr (SPLIT) {
+        /* The record of (tile, split, wave): nine 16-byte chunks per lane,
+         * chunk-major (chunk c of lane l at byte 16 (64 c + l)), so that
+         * each chunk of the wave is one coalesced KiB: O^T registers 4 c
+         * .. 4 c + 3 of o0 in chunks 0-3 and of o1 in 4-7 (head width 64),
+         * (m in log2 units, l) in chunk 8. Stored and loaded with the sc1
+         * policy, as agent-scope atomics are. */
+        __shared__ unsigned arrived;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            part + item * nsplit * 9216, (short)0, nsplit * 9216 * 4, BUF_RSRC_DW3);
+        auto off = [&](int s2, int c) { return ((s2 * 4 + w) * 9 + c) * 1024 + 16 * l; };
+        const float mrec = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
+
+        if (!idle) {
+            for (int c = 0; c < 4; c++) {
+                const f32x4 x0 = {o0[4 * c], o0[4 * c + 1], o0[4 * c + 2], o0[4 * c + 3]};
+
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x0), rs,
+                                                       off(sp, c), 0, CPOL_SC1);
+                if (HD == 64) {
+                    const f32x4 x1 = {o1[4 * c], o1[4 * c + 1], o1[4 * c + 2], o1[4 * c + 3]};
+
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x1), rs,
+                                                           off(sp, 4 + c), 0, CPOL_SC1);
+                }
+            }
+            const f32x4 ml = {mrec, l_run, 0.0f, 0.0f};
+
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ml), rs,
+                                                   off(sp, 8), 0, CPOL_SC1);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t == 0)
+            arrived = __hip_atomic_fetch_add(&cnt[item], 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived != (unsigned)(nsplit - 1))
+            return;
+        if (t == 0)
+            __hip_atomic_store(&cnt[item], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (idle)
+            return;
+        /* Splits in order, three at a time, each folded into a running
+         * (M, L, O) like the blocks of the online softmax: M the largest m
+         * so far over splits that saw a key (l > 0), O and L rescaled by
+         * 2^(M_old - M) and the split's o and l added with weight
+         * 2^(m_s - M); a split that saw no key adds nothing. Every split's
+         * state comes back from its record, this one's included (the same
+         * bits whichever split merges). The three splits' loads are all
+         * issued before the first is used: the empty asm statements that
+         * take them also order memory, so no load moves past them. */
+        float M = -INFINITY, L = 0.0f;
+        f32x16 a0, a1;
 
         for (int r = 0; r < 16; r++) {
-            const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
-
-            orow[dd] = o0[r];
-            if (HD == 64)
-                orow[32 + dd] = o1[r];
+            a0[r] = 0.0f;
+            a1[r] = 0.0f;
         }
-        if (h == 0) {
-            float *ml = part + (long)d.nb * nsplit * Np * 64 + pidx * 2;
+        for (int s0 = 0; s0 < nsplit; s0 += 3) {
+            u32x4 ch[3][9];
 
-            ml[0] = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
-            ml[1] = l_run;
+            for (int j = 0; j < 3; j++) {
+                const int s2 = s0 + j < nsplit ? s0 + j : s0;
+
+                for (int c = 0; c < 9; c++)
+                    ch[j][c] = HD == 64 || c < 4 || c == 8
+                                   ? __builtin_amdgcn_raw_buffer_load_b128(rs, off(s2, c), 0,
+                                                                           CPOL_SC1)
+                                   : u32x4{0u, 0u, 0u, 0u};
+            }
+            for (int j = 0; j < 3; j++) {
+                asm volatile("" : "+v"(ch[j][0]), "+v"(ch[j][1]), "+v"(ch[j][2]), "+v"(ch[j][3]),
+                             "+v"(ch[j][4]), "+v"(ch[j][5]), "+v"(ch[j][6]), "+v"(ch[j][7]),
+                             "+v"(ch[j][8])::"memory");
+                const f32x4 ml = __builtin_bit_cast(f32x4, ch[j][8]);
+                const bool take = ml[1] > 0.0f && s0 + j < nsplit;
+                const float Mn = take ? fmaxf(M, ml[0]) : M;
+                const float c = take ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;
+                const float wt = take ? __builtin_amdgcn_exp2f(ml[0] - Mn) : 0.0f;
+
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v0 = __builtin_bit_cast(f32x4, ch[j][q]);
+                    const f32x4 v1 = __builtin_bit_cast(f32x4, ch[j][4 + q]);
+
+                    for (int e = 0; e < 4; e++) {
+                        a0[4 * q + e] = fmaf(v0[e], wt, a0[4 * q + e] * c);
+                        if (HD == 64)
+                            a1[4 * q + e] = fmaf(v1[e], wt, a1[4 * q + e] * c);
+                    }
+                }
+                L = fmaf(ml[1], wt, L * c);
+                M = Mn;
+            }
         }
-        return;
+        o0 = a0;
+        o1 = a1;
+        l_run = L;
     }
+    if (qi >= N)
+        return;
     {
         const float inv = 1.0f / l_run;
         const long orow = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)qi * d.ldo;
 
+        if (d.odt == DT_F32 && ((orow & 3) | ((uintptr_t)d.O & 15)) == 0) {
+            /* Registers 4 g .. 4 g + 3 are columns 8 g + 4 h .. + 3 of the
+             * lane's query row: one 16-byte store each. */
+            float *op = (float *)d.O + orow + 4 * h;
+
+            for (int g = 0; g < 4; g++) {
+                const f32x4 x0 = {o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv,
+                                  o0[4 * g + 3] * inv};
+
+                *(f32x4 *)(op + 8 * g) = x0;
+                if (HD == 64) {
+                    const f32x4 x1 = {o1[4 * g] * inv, o1[4 * g + 1] * inv,
+                                      o1[4 * g + 2] * inv, o1[4 * g + 3] * inv};
+
+                    *(f32x4 *)(op + 32 + 8 * g) = x1;
+                }
+            }
+            return;
+        }
         for (int r = 0; r < 16; r++) {
             const int dd = 8 * (r >> 2) + 4 * h + (r & 3);
 
@@ -519,9 +657,6 @@ struct SoftState {
     f32x16 o0, o1;
     float m, l;
 };
-
-/* XCDs (L2 domains) of an MI355X. */
-#define NXCD 8
 
 /* Asynchronous 16-byte global -> LDS copy (global_load_lds_dwordx4):
  * lane i of the wave writes lds_base + 16 i (lds_base wave-uniform, via
@@ -1752,34 +1887,30 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
     return hipGetLastError();
 }
 
-extern "C" int launch_attn_f32(const attn_desc *d, float *part, int nsplit, void *stream)
+extern "C" int launch_attn_f32(const attn_desc *d, float *part, unsigned *cnt, int nsplit,
+                               void *stream)
 {
-    const int nblk = (d->Nk + 31) / 32, Np = (d->N + 63) / 64 * 64;
-    const long gx = (long)((d->N + 127) / 128) * nsplit;
+    const int nblk = (d->Nk + 31) / 32;
+    const long total = (long)d->nb * ((d->N + 127) / 128) * nsplit;
+    const long grid = (total + NXCD - 1) / NXCD * NXCD;
     const bool ext = d->causal || d->bias;
-    int err;
 
-    if (d->nb > 65535 || gx > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > 64 ||
-        nsplit > nblk || (nsplit > 1 && !part) || (d->hd != 64 && d->hd != 32) ||
+    if (d->N < 1 || d->nb < 1 || grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > 64 ||
+        nsplit > nblk || (nsplit > 1 && (!part || !cnt)) || (d->hd != 64 && d->hd != 32) ||
         (d->hd == 32 && d->rope))
         return hipErrorInvalidConfiguration;
     {
-        auto kern = d->hd == 32 ? (ext ? k_attn_f32<32, true> : k_attn_f32<32, false>)
-                                : (ext ? k_attn_f32<64, true> : k_attn_f32<64, false>);
+        auto kern = nsplit > 1 ? (d->hd == 32 ? (ext ? k_attn_f32<32, true, true>
+                                                     : k_attn_f32<32, false, true>)
+                                              : (ext ? k_attn_f32<64, true, true>
+                                                     : k_attn_f32<64, false, true>))
+                               : (d->hd == 32 ? (ext ? k_attn_f32<32, true, false>
+                                                     : k_attn_f32<32, false, false>)
+                                              : (ext ? k_attn_f32<64, true, false>
+                                                     : k_attn_f32<64, false, false>));
 
-        hipLaunchKernelGGL(kern, dim3((unsigned)gx, d->nb), dim3(256), 0,
-                           (hipStream_t)stream, *d, part, nsplit);
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *d,
+                           part, cnt, nsplit);
     }
-    err = hipGetLastError();
-    if (err != hipSuccess || nsplit == 1)
-        return err;
-    if (nsplit <= 8)
-        hipLaunchKernelGGL(k_attn_merge_few, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
-                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
-                           nsplit, Np);
-    else
-        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 3) / 4)),
-                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
-                           nsplit, Np);
     return hipGetLastError();
 }

@@ -142,9 +142,13 @@ struct attn_desc {
  * queries over Nk keys, head width 64 or 32 (no RoPE), the causal mask or
  * an additive bias table in natural units (d->bias, as launch_box_bias
  * with unit_scale 1 writes it). With 1 < nsplit <= 64 the 32-key blocks
- * are split nsplit ways, `part` (nb nsplit Np 66 floats) holds the
- * partials and the bf16 path's merge kernels combine them into O. */
-int launch_attn_f32(const struct attn_desc *d, float *part, int nsplit, void *stream);
+ * are split nsplit ways in the same launch: `part` (nb, (N + 127) / 128
+ * tiles, nsplit, 4 x 9216 floats) holds each split's records and
+ * `cnt` (nb (N + 127) / 128 counts, zero before the launch and again
+ * after it) counts the splits of each tile in; the last to arrive merges
+ * them in split order. */
+int launch_attn_f32(const struct attn_desc *d, float *part, unsigned *cnt, int nsplit,
+                    void *stream);
 
 /* Packed bf16 staging of the fast path, Np = N rounded up to 64:
  * q16/k16 [nb][Np][64] (RoPE applied, q scaled), vt16 [nb][64][Np],

@@ -526,17 +526,42 @@ static int attn_groups(const struct hipb_backend *b, const struct attn_desc *d, 
     return 0;
 }
 
-/* Partial records for nsplit key splits: nb nsplit Np (64 + 2) floats. */
-static float *attn_part(struct sam_model *m, int N, int nb, int nsplit)
+/* Partial records for nsplit key splits of the bf16 path: nb nsplit Np
+ * (64 + 2) floats; of the exact path (f32 set): nb, 128-query tiles,
+ * nsplit, 4 waves of 9 x 64 x 4 floats. */
+static float *attn_part(struct sam_model *m, int N, int nb, int nsplit, int f32)
 {
-    const size_t np = ((size_t)N + 63) / 64 * 64;
+    const size_t np = ((size_t)N + 63) / 64 * 64, tiles = ((size_t)N + 127) / 128;
+    const size_t count = f32 ? (size_t)nb * tiles * nsplit * 4 * 9 * 64 * 4
+                             : (size_t)nb * nsplit * np * 66;
 
     if (nsplit <= 1)
         return NULL;
-    if (!ensure_typed(m->hip, &m->apart, (size_t)nb * nsplit * np * 66,
-                      HIPB_F32, "attention split partials"))
+    if (!ensure_typed(m->hip, &m->apart, count, HIPB_F32, "attention split partials"))
         return NULL;
     return (float *)m->apart->ptr;
+}
+
+/* Arrival counts, one per (unit, 128-query tile), zero between launches:
+ * zero-filled when (re)allocated, and every launch that counts tiles in
+ * (the balanced bf16 launch, the exact path's key splits) resets each
+ * count it used. */
+static unsigned *attn_cnt(struct sam_model *m, long tiles)
+{
+    struct hipb_backend *b = m->hip;
+    const int fresh = !m->askcnt || hipb_count(m->askcnt) < (size_t)tiles;
+    int err;
+
+    if (!ensure_typed(b, &m->askcnt, (size_t)tiles, HIPB_F32, "attention arrival counts"))
+        return NULL;
+    if (fresh) {
+        hipb_run_begin(b);
+        err = launch_attn_sk_zero((unsigned *)m->askcnt->ptr, tiles, b->stream);
+        hipb_run_end(b, err, "attn_sk_zero", 0.0);
+        if (hipb_failed())
+            return NULL;
+    }
+    return (unsigned *)m->askcnt->ptr;
 }
 
 /* Balanced launch of the bf16 attention (launch_attn_bf16's skG, skdp):
@@ -571,24 +596,11 @@ static int attn_sk(const struct hipb_backend *b, const struct attn_desc *d, int 
 static int attn_skbuf(struct sam_model *m, int G, long tiles, float **rec,
                       unsigned **cnt)
 {
-    struct hipb_backend *b = m->hip;
-    const int fresh = !m->askcnt || hipb_count(m->askcnt) < (size_t)tiles;
-    int err;
-
-    if (!ensure_typed(b, &m->askrec, (size_t)8 * G * ATTN_SK_REC_FLOATS, HIPB_F32,
+    if (!ensure_typed(m->hip, &m->askrec, (size_t)8 * G * ATTN_SK_REC_FLOATS, HIPB_F32,
                       "balanced attention records") ||
-        !ensure_typed(b, &m->askcnt, (size_t)tiles, HIPB_F32,
-                      "balanced attention counters"))
+        !(*cnt = attn_cnt(m, tiles)))
         return 0;
-    if (fresh) {
-        hipb_run_begin(b);
-        err = launch_attn_sk_zero((unsigned *)m->askcnt->ptr, tiles, b->stream);
-        hipb_run_end(b, err, "attn_sk_zero", 0.0);
-        if (hipb_failed())
-            return 0;
-    }
     *rec = (float *)m->askrec->ptr;
-    *cnt = (unsigned *)m->askcnt->ptr;
     return 1;
 }
 
@@ -681,7 +693,7 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
             const int ns = ng ? 1 : attn_splits(b, N, Nk, nb);
             int dp;
             const int G = attn_sk(b, &d, N, Nk, nb, ns, &dp);
-            float *part = attn_part(m, N, nb, ns), *skrec = NULL;
+            float *part = attn_part(m, N, nb, ns, 0), *skrec = NULL;
             unsigned *skcnt = NULL;
 
             if ((ns > 1 && !part) ||
@@ -698,32 +710,36 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         return;
     }
     {
-        /* The exact kernel's key blocks are 32 keys: split by those, at
-         * least three blocks per split (one 576-token window of 16 heads:
-         * 6 splits of 3 blocks, 480 workgroups, 34.5 us with the merge,
-         * against 9 splits of 2 blocks 35.5 us and 4 splits of 64-key
-         * blocks 39.5 us: fewer workgroups pay the Q load and the first
-         * block's copy, and fewer partials go through the merge). */
+        /* The exact kernel's key blocks are 32 keys: split by those into
+         * one round of workgroups, one per CU (at least two splits), at
+         * least three blocks per split. The splits merge inside the
+         * launch. One 576-token window of 16 heads: 3 splits of 6 blocks,
+         * 240 workgroups, 26.4 us; 6 splits of 3 blocks (two workgroups
+         * on most CUs) 27.4 us, 9 splits 33 us: every workgroup pays the
+         * Q load, the first block's copy and its record, and the merge
+         * reads every split's. */
         int ns = attn_splits(b, N, Nk, nb);
 
         if (ns > 1) {
             const int cus = b->cu_count > 0 ? b->cu_count : 256;
             const long items = (long)nb * ((N + 127) / 128);
-            long n32 = 3L * cus / items;
+            long n32 = cus / items;
 
+            if (n32 < 2)
+                n32 = 2;
             if (n32 > (Nk + 31) / 32 / 3)
                 n32 = (Nk + 31) / 32 / 3;
             if (n32 > 64)
                 n32 = 64;
-            if (n32 > ns)
-                ns = (int)n32;
+            ns = n32 > 1 ? (int)n32 : 1;
         }
-        float *part = attn_part(m, N, nb, ns);
+        float *part = attn_part(m, N, nb, ns, 1);
+        unsigned *cnt = ns > 1 ? attn_cnt(m, (long)nb * ((N + 127) / 128)) : NULL;
 
-        if (ns > 1 && !part)
+        if (ns > 1 && (!part || !cnt))
             return;
         hipb_run_begin(b);
-        err = launch_attn_f32(&d, part, ns, b->stream);
+        err = launch_attn_f32(&d, part, cnt, ns, b->stream);
         hipb_run_end(b, err, "attn_f32", 4.0 * N * (double)Nk * hd * nb);
     }
 }
@@ -780,7 +796,7 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     ng = attn_groups(b, &d, N, N, nb);
     ns = ng ? 1 : attn_splits(b, N, N, nb);
     G = attn_sk(b, &d, N, N, nb, ns, &dp);
-    part = attn_part(m, N, nb, ns);
+    part = attn_part(m, N, nb, ns, 0);
     if ((ns > 1 && !part) ||
         (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
         return;

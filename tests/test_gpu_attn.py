@@ -68,6 +68,50 @@ def test_single_window(hip, be, orc):
     be.release(do)
 
 
+def test_split_launch_repeats(hip, be, orc):
+    """Launch-starved shapes merge their key splits inside the one launch
+    (the exact path: the last split of a tile to arrive merges all of them
+    in split order; bf16: key groups inside the workgroup). The same bits
+    on every launch, and each launch leaves its arrival counts at zero for
+    the next one of another tile count: one 576-token window of 16 heads,
+    then 1000 tokens of 2 heads with RoPE, then the window again."""
+    N, H, E = 576, 16, 1024
+    m = hip.Model(be, embed=E, heads=H)
+    qkv = np.random.default_rng(12).standard_normal((N, 3 * E), np.float32)
+    dq = be.upload(qkv)
+    do = be.alloc(N * E * 4)
+
+    def window():
+        hip.attn_fused(m, N, H, H, hip.bmat(dq, 0, 3 * E, 0, 64),
+                       hip.bmat(dq, E, 3 * E, 0, 64),
+                       hip.bmat(dq, 2 * E, 3 * E, 0, 64),
+                       hip.bmat(do, 0, E, 0, 64), None, 1, 0.125)
+        return be.read(do).reshape(N, E)
+
+    first = window()
+    want = _oracle_units(orc, qkv, N, 1, H, E, None)
+    assert report("split window %s" % be.precision, first, want) <= TOL[be.precision]
+
+    N2, H2, E2 = 1000, 2, 128
+    table = orc.rope_table(32)[:N2]
+    qkv2 = np.random.default_rng(13).standard_normal((N2, 3 * E2), np.float32)
+    dq2, dt = be.upload(qkv2), be.upload(table)
+    do2 = be.alloc(N2 * E2 * 4)
+    hip.attn_fused(m, N2, H2, H2, hip.bmat(dq2, 0, 3 * E2, 0, 64),
+                   hip.bmat(dq2, E2, 3 * E2, 0, 64),
+                   hip.bmat(dq2, 2 * E2, 3 * E2, 0, 64),
+                   hip.bmat(do2, 0, E2, 0, 64), dt, N2, 0.125)
+    got2 = be.read(do2).reshape(N2, E2)
+    want2 = _oracle_units(orc, qkv2, N2, 1, H2, E2, table)
+    assert report("split 1000 x 2 %s" % be.precision, got2, want2) <= TOL[be.precision]
+
+    for _ in range(3):
+        assert np.array_equal(window(), first)
+    for x in (dq, do, dq2, dt, do2):
+        be.release(x)
+    m.free()
+
+
 @pytest.mark.parametrize("N,nunits", [(37, 3), (100, 2), (200, 1), (64, 2)])
 def test_rope_and_ragged_lengths(hip, be, orc, N, nunits):
     """Token counts that are not multiples of the 32/64-key blocks or the

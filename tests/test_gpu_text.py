@@ -152,8 +152,9 @@ def test_long_causal_split_keys(hip, be, orc):
 
 def test_key_splits_not_a_multiple_of_four(hip, be, orc):
     """5700 causal tokens, one head of 64: 45 query tiles split the keys 17
-    ways on both paths (causal attention takes the split launch on bf16
-    too). The merge's four lane groups then take 5, 4, 4 and 4 splits; its
+    ways on the bf16 path (causal attention takes the split launch there;
+    the exact path splits them 5 ways and merges inside its launch). The
+    merge kernel's four lane groups then take 5, 4, 4 and 4 splits; its
     weights are shuffled between lanes, which must all be active (a lane
     that had left its loop would hand over 0 and drop a split)."""
     n, heads, hd = 5700, 1, 64
@@ -166,9 +167,11 @@ def test_key_splits_not_a_multiple_of_four(hip, be, orc):
 
 
 def test_one_head_many_key_splits(hip, be, orc):
-    """2000 tokens, one head of 64: on the bf16 path 16 query tiles leave
-    the GPU idle, so the keys split 15 ways and the wave-per-query merge
-    combines them (the bias case above takes 40 splits)."""
+    """2000 tokens, one head of 64: 16 query tiles leave the GPU idle. The
+    exact path splits the keys 16 ways and merges the splits inside its
+    launch; the bf16 path takes the grouped launch (four key groups per
+    workgroup, merged in LDS). The bias case above takes 40 bf16 splits
+    and the wave-per-query merge kernel."""
     n, heads, hd = 2000, 1, 64
     g = np.random.default_rng(36)
     Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)

@@ -719,6 +719,9 @@ def main():
                     help="only the image encoder trunk (profiling)")
     ap.add_argument("--text-only", action="store_true",
                     help="only the text path's attend() shapes (profiling)")
+    ap.add_argument("--one-window-only", action="store_true",
+                    help="only the single 576-token window's attention, bf16 and "
+                         "fp32 (profiling)")
     ap.add_argument("--window-only", action="store_true",
                     help="only the windowed bf16 attention kernel (profiling)")
     ap.add_argument("--region-only", action="store_true",
@@ -783,6 +786,23 @@ def main():
         be.release(src)
         be.release(dst)
 
+    if args.one_window_only:
+        # One 576-token window of 16 heads: the bf16 grouped launch, then
+        # the exact path's launch with its key splits merged inside it.
+        be32 = hip.Backend(precision="fp32")
+        one = Block(hip, be, 24, seed=1, grid=24)
+        one.region()
+        be.finish()
+        one32 = Block(hip, be32, 24, seed=1, grid=24)
+        one32.region()
+        be32.finish()
+        ms = timed(be, one.attn, args.steps, args.warmup)
+        ms32 = timed(be32, one32.attn_f32, args.steps, args.warmup)
+        print(json.dumps({"kernel": "attention, one window 576 x 16 heads",
+                          "bf16_ms": ms, "fp32_ms": ms32,
+                          "bf16_TFLOP/s": one.flops() / ms / 1e9,
+                          "fp32_TFLOP/s": one.flops() / ms32 / 1e9}))
+        return
     if args.window_only:
         win = Block(hip, be, 24, seed=2)
         win.region()

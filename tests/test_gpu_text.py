@@ -180,3 +180,19 @@ def test_one_head_many_key_splits(hip, be, orc):
     rows = np.sort(g.choice(n, 128, replace=False))
     want = orc.attend(Q[rows], K, V, heads, hd)
     assert report("many splits %s" % be.precision, got[rows], want) <= TOL[be.precision]
+
+
+def test_sixty_four_key_splits(hip, be, orc):
+    """256 queries over 8192 keys, one head of 64: two query tiles, so the
+    exact path splits the keys the most it does, 64 ways (four 32-key
+    blocks each), and merges them inside its launch three at a time (the
+    last round one split and two repeats that must add nothing); the bf16
+    path takes the grouped launch. A second launch gives the same bits."""
+    nq, nk, heads, hd = 256, 8192, 1, 64
+    g = np.random.default_rng(38)
+    Q = g.standard_normal((nq, hd)).astype(np.float32)
+    K, V = (g.standard_normal((nk, hd)).astype(np.float32) for _ in range(2))
+    got = _run(hip, be, Q, K, V, heads, hd)
+    want = orc.attend(Q, K, V, heads, hd)
+    assert report("64 key splits %s" % be.precision, got, want) <= TOL[be.precision]
+    assert np.array_equal(_run(hip, be, Q, K, V, heads, hd), got)

@@ -37,6 +37,158 @@
 #define BUF_RSRC_DW3 0x00020000
 #define CPOL_SC1 16
 
+/* Key splits of one (unit, query tile) merged inside their launch, in two
+ * levels: the splits form groups of SPLIT_GROUP (the last group may be
+ * shorter); the last split of a group to arrive folds the group's records
+ * into a group record, and the last group to finish folds the group
+ * records (one group: the group's fold is the result). Every fold takes
+ * its records in order, three at a time, into a running (M, L, O) as the
+ * online softmax folds blocks: M the largest m so far over records that
+ * saw a key (l > 0), O and L rescaled by 2^(M_old - M) and the record's o
+ * and l added with weight 2^(m_r - M); a record that saw no key adds
+ * nothing. Every record comes back from memory, the folding workgroup's
+ * own included, so the bits do not depend on which split or group
+ * arrives last; two levels spread the reading over up to nine
+ * workgroups' CUs instead of one.
+ *
+ * Records: per tile (item) SPLIT_RECS(nsplit) of them at part + item
+ * SPLIT_RECS(nsplit) 9216 floats, the nsplit split records, then the
+ * group records; per record and wave nine 16-byte chunks per lane,
+ * chunk-major (chunk c of lane l at byte 16 (64 c + l), so that each
+ * chunk of a wave is one coalesced KiB): O^T registers 4 c .. 4 c + 3 of
+ * o0 in chunks 0-3 and of o1 in 4-7 (O1), (m in log2 units, l of the whole
+ * query) in chunk 8. Stored and loaded with the sc1 policy of agent-scope
+ * atomics (coherent across the XCDs' L2s); a workgroup counts itself in
+ * (cnt[item SPLIT_CNT + group], then cnt[item SPLIT_CNT + SPLIT_GROUP] for
+ * the groups) once its stores are done (vmcnt(0), then the barrier), and
+ * each last arrival resets the count it read. The loads of three records
+ * are all issued before the first is used: the empty asm statements that
+ * take them also order memory, so no load moves past them (left to itself
+ * the scheduler waited for each load in turn).
+ *
+ * Returns true in the final folding workgroup's waves that store (o0, o1,
+ * m, lq then hold the merged state), false elsewhere. Every wave of the
+ * workgroup calls it; a wave with store false (no query of its own)
+ * meets the barriers but leaves no record and folds nothing. */
+template <bool O1>
+__device__ __forceinline__ bool split_merge(float *__restrict__ part, unsigned *__restrict__ cnt,
+                                            long item, int nsplit, int sp, bool store,
+                                            f32x16 &o0, f32x16 &o1, float &m, float &lq)
+{
+    __shared__ unsigned arrived;
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    const int ngroups = (nsplit + SPLIT_GROUP - 1) / SPLIT_GROUP, nrec = nsplit + ngroups;
+    const int g = sp / SPLIT_GROUP, g0 = g * SPLIT_GROUP;
+    const int gn = nsplit - g0 < SPLIT_GROUP ? nsplit - g0 : SPLIT_GROUP;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        part + item * nrec * 9216, (short)0, nrec * 9216 * 4, BUF_RSRC_DW3);
+    unsigned *const cg = cnt + item * SPLIT_CNT;
+    auto off = [&](int r, int c) { return ((r * 4 + w) * 9 + c) * 1024 + 16 * l; };
+    auto put = [&](int r) {
+        for (int c = 0; c < 4; c++) {
+            const f32x4 x0 = {o0[4 * c], o0[4 * c + 1], o0[4 * c + 2], o0[4 * c + 3]};
+
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x0), rs, off(r, c),
+                                                   0, CPOL_SC1);
+            if (O1) {
+                const f32x4 x1 = {o1[4 * c], o1[4 * c + 1], o1[4 * c + 2], o1[4 * c + 3]};
+
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x1), rs,
+                                                       off(r, 4 + c), 0, CPOL_SC1);
+            }
+        }
+        const f32x4 ml = {m, lq, 0.0f, 0.0f};
+
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ml), rs, off(r, 8), 0,
+                                               CPOL_SC1);
+    };
+    /* Counts the workgroup in at *c after its stores; true in the last of
+     * n arrivals, which resets the count. */
+    auto count_in = [&](unsigned *c, int n) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t == 0)
+            arrived = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrived != (unsigned)(n - 1))
+            return false;
+        if (t == 0)
+            __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    };
+    /* Folds records r0 .. r0 + n - 1 into (o0, o1, m, lq). */
+    auto fold = [&](int r0, int n) {
+        float M = -INFINITY, L = 0.0f;
+        f32x16 a0, a1;
+
+        for (int r = 0; r < 16; r++) {
+            a0[r] = 0.0f;
+            a1[r] = 0.0f;
+        }
+        for (int s0 = 0; s0 < n; s0 += 3) {
+            u32x4 ch[3][9];
+
+            for (int j = 0; j < 3; j++) {
+                const int r = r0 + (s0 + j < n ? s0 + j : s0);
+
+                for (int c = 0; c < 9; c++)
+                    ch[j][c] = O1 || c < 4 || c == 8
+                                   ? __builtin_amdgcn_raw_buffer_load_b128(rs, off(r, c), 0,
+                                                                           CPOL_SC1)
+                                   : u32x4{0u, 0u, 0u, 0u};
+            }
+            for (int j = 0; j < 3; j++) {
+                asm volatile("" : "+v"(ch[j][0]), "+v"(ch[j][1]), "+v"(ch[j][2]),
+                             "+v"(ch[j][3]), "+v"(ch[j][4]), "+v"(ch[j][5]), "+v"(ch[j][6]),
+                             "+v"(ch[j][7]), "+v"(ch[j][8])::"memory");
+                const f32x4 ml = __builtin_bit_cast(f32x4, ch[j][8]);
+                const bool take = ml[1] > 0.0f && s0 + j < n;
+                const float Mn = take ? fmaxf(M, ml[0]) : M;
+                const float c = take ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;
+                const float wt = take ? __builtin_amdgcn_exp2f(ml[0] - Mn) : 0.0f;
+
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 v0 = __builtin_bit_cast(f32x4, ch[j][q]);
+                    const f32x4 v1 = __builtin_bit_cast(f32x4, ch[j][4 + q]);
+
+                    for (int e = 0; e < 4; e++) {
+                        a0[4 * q + e] = fmaf(v0[e], wt, a0[4 * q + e] * c);
+                        if (O1)
+                            a1[4 * q + e] = fmaf(v1[e], wt, a1[4 * q + e] * c);
+                    }
+                }
+                L = fmaf(ml[1], wt, L * c);
+                M = Mn;
+            }
+        }
+        o0 = a0;
+        o1 = a1;
+        m = M;
+        lq = L;
+    };
+
+    /* Level 0: this split's record, its group's count and fold; level 1
+     * (more than one group): the group's record, the groups' count and
+     * fold. One loop, so that the store and the fold are emitted once. */
+    int rec = sp, r0 = g0, n = gn;
+    unsigned *c = cg + g;
+
+    for (int lev = 0;; lev++) {
+        if (store)
+            put(rec);
+        if (!count_in(c, n))
+            return false;
+        if (store)
+            fold(r0, n);
+        if (lev == 1 || ngroups == 1)
+            return store;
+        rec = nsplit + g;
+        r0 = nsplit;
+        n = ngroups;
+        c = cg + SPLIT_GROUP;
+    }
+}
+
 /* ------------------------------------------------------------ fp32 path */
 
 /* fp32 operands in the reference row layout (Q/K/V/O opnds of
@@ -54,17 +206,11 @@
  * scale 1), added to the scaled score as softmax_ext adds it.
  *
  * With nsplit > 1 (the SPLIT instance) the workgroup takes key blocks
- * [kb0, kb1) of split sp, leaves its per-lane state (O, m in log2 units,
- * l) in its record of `part` (nb, 128-query tiles, nsplit, 4 waves of
- * 9216 floats), and counts itself in at cnt[unit][tile]; the tile's last split to arrive
- * merges every split's state in split order (its own from registers, the
- * bits of its record: the same result whichever split arrives last),
- * resets the count for the next launch and stores O. A query none of
- * whose keys a split sees (causal) has l = 0 there and drops out of the
- * merge. Records and counts are touched only with the sc1 policy of
- * agent-scope atomics, which reaches the device's coherent memory rather
- * than one XCD's L2; waiting for the record stores (vmcnt(0)) before the
- * count orders them. */
+ * [kb0, kb1) of split sp and the tile's splits merge inside the launch
+ * (split_merge; `part` holds nb, 128-query tiles, SPLIT_RECS(nsplit)
+ * records of 9216 floats, cnt SPLIT_CNT counts per (unit, tile)): the
+ * final folding workgroup stores O. A query none of whose keys a split
+ * sees (causal) has l = 0 there and drops out of the merge. */
 template <int HD, bool EXT, bool SPLIT>
 __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict__ part,
                                                   unsigned *__restrict__ cnt, int nsplit)
@@ -234,6 +380,11 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
             if (HD == 64)
                 o1[r] *= corr;
         }
+        /* The exponentials issued before the P V MFMAs: left to the
+         * scheduler, which weighs the code after the key loop too, each
+         * MFMA could follow the exponential it reads and wait for it
+         * (3 % on one 576-token window). */
+        __builtin_amdgcn_sched_barrier(0);
         /* O^T += V^T P^T: step st contracts key 8 (st / 4) + 4 h + st % 4,
          * the key of this lane's score register st. */
 #pragma unroll
@@ -269,103 +420,10 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
 
     l_run += __shfl_xor(l_run, 32, 64);
     if constexpr (SPLIT) {
-        /* The record of (tile, split, wave): nine 16-byte chunks per lane,
-         * chunk-major (chunk c of lane l at byte 16 (64 c + l)), so that
-         * each chunk of the wave is one coalesced KiB: O^T registers 4 c
-         * .. 4 c + 3 of o0 in chunks 0-3 and of o1 in 4-7 (head width 64),
-         * (m in log2 units, l) in chunk 8. Stored and loaded with the sc1
-         * policy, as agent-scope atomics are. */
-        __shared__ unsigned arrived;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            part + item * nsplit * 9216, (short)0, nsplit * 9216 * 4, BUF_RSRC_DW3);
-        auto off = [&](int s2, int c) { return ((s2 * 4 + w) * 9 + c) * 1024 + 16 * l; };
-        const float mrec = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
+        float mrec = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
 
-        if (!idle) {
-            for (int c = 0; c < 4; c++) {
-                const f32x4 x0 = {o0[4 * c], o0[4 * c + 1], o0[4 * c + 2], o0[4 * c + 3]};
-
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x0), rs,
-                                                       off(sp, c), 0, CPOL_SC1);
-                if (HD == 64) {
-                    const f32x4 x1 = {o1[4 * c], o1[4 * c + 1], o1[4 * c + 2], o1[4 * c + 3]};
-
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x1), rs,
-                                                           off(sp, 4 + c), 0, CPOL_SC1);
-                }
-            }
-            const f32x4 ml = {mrec, l_run, 0.0f, 0.0f};
-
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ml), rs,
-                                                   off(sp, 8), 0, CPOL_SC1);
-        }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (t == 0)
-            arrived = __hip_atomic_fetch_add(&cnt[item], 1u, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        if (arrived != (unsigned)(nsplit - 1))
+        if (!split_merge<HD == 64>(part, cnt, item, nsplit, sp, !idle, o0, o1, mrec, l_run))
             return;
-        if (t == 0)
-            __hip_atomic_store(&cnt[item], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (idle)
-            return;
-        /* Splits in order, three at a time, each folded into a running
-         * (M, L, O) like the blocks of the online softmax: M the largest m
-         * so far over splits that saw a key (l > 0), O and L rescaled by
-         * 2^(M_old - M) and the split's o and l added with weight
-         * 2^(m_s - M); a split that saw no key adds nothing. Every split's
-         * state comes back from its record, this one's included (the same
-         * bits whichever split merges). The three splits' loads are all
-         * issued before the first is used: the empty asm statements that
-         * take them also order memory, so no load moves past them. */
-        float M = -INFINITY, L = 0.0f;
-        f32x16 a0, a1;
-
-        for (int r = 0; r < 16; r++) {
-            a0[r] = 0.0f;
-            a1[r] = 0.0f;
-        }
-        for (int s0 = 0; s0 < nsplit; s0 += 3) {
-            u32x4 ch[3][9];
-
-            for (int j = 0; j < 3; j++) {
-                const int s2 = s0 + j < nsplit ? s0 + j : s0;
-
-                for (int c = 0; c < 9; c++)
-                    ch[j][c] = HD == 64 || c < 4 || c == 8
-                                   ? __builtin_amdgcn_raw_buffer_load_b128(rs, off(s2, c), 0,
-                                                                           CPOL_SC1)
-                                   : u32x4{0u, 0u, 0u, 0u};
-            }
-            for (int j = 0; j < 3; j++) {
-                asm volatile("" : "+v"(ch[j][0]), "+v"(ch[j][1]), "+v"(ch[j][2]), "+v"(ch[j][3]),
-                             "+v"(ch[j][4]), "+v"(ch[j][5]), "+v"(ch[j][6]), "+v"(ch[j][7]),
-                             "+v"(ch[j][8])::"memory");
-                const f32x4 ml = __builtin_bit_cast(f32x4, ch[j][8]);
-                const bool take = ml[1] > 0.0f && s0 + j < nsplit;
-                const float Mn = take ? fmaxf(M, ml[0]) : M;
-                const float c = take ? __builtin_amdgcn_exp2f(M - Mn) : 1.0f;
-                const float wt = take ? __builtin_amdgcn_exp2f(ml[0] - Mn) : 0.0f;
-
-                for (int q = 0; q < 4; q++) {
-                    const f32x4 v0 = __builtin_bit_cast(f32x4, ch[j][q]);
-                    const f32x4 v1 = __builtin_bit_cast(f32x4, ch[j][4 + q]);
-
-                    for (int e = 0; e < 4; e++) {
-                        a0[4 * q + e] = fmaf(v0[e], wt, a0[4 * q + e] * c);
-                        if (HD == 64)
-                            a1[4 * q + e] = fmaf(v1[e], wt, a1[4 * q + e] * c);
-                    }
-                }
-                L = fmaf(ml[1], wt, L * c);
-                M = Mn;
-            }
-        }
-        o0 = a0;
-        o1 = a1;
-        l_run = L;
     }
     if (qi >= N)
         return;
@@ -737,8 +795,10 @@ struct sk_desc {
 /* Key blocks [kb0, kb1) of query tile `tile` of unit `unit`: the body
  * of k_attn_bf16 (a function rather than a lambda: wrapping it in a
  * lambda costs the bias variant its register budget). `d` is the
- * descriptor or, in stream-K mode, an opaque alias of it. */
-template <bool EXT, bool H32, bool SK, class Desc>
+ * descriptor or, in stream-K mode, an opaque alias of it. With SPL the
+ * key blocks are split sp of nsplit, merged inside the launch
+ * (split_merge, counting on sk.cnt). */
+template <bool EXT, bool H32, bool SK, bool SPL, class Desc>
 __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restrict__ q16,
                                           const uint16_t *__restrict__ k16,
                                           const uint16_t *__restrict__ vt16,
@@ -1154,24 +1214,19 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
         st.m = M;
     }
     st.l += __shfl_xor(st.l, 32, 64);
-    /* Final O / l, or with key splits the unnormalised O of this split
-     * (fp32 rows of 64 at part [unit][split][Np][64]) and its (m, l) pair
-     * (part's tail, [unit][split][Np][2]). */
-    const bool partial = nsplit > 1;
-    const float inv = partial ? 1.0f : 1.0f / st.l;
-    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-    const long pidx = (unit * nsplit + sp) * (long)Np;
-    void *const Obuf = partial ? (void *)part : d.O;
-    const long obase = partial ? pidx * 64 : d.ooff + b0 * d.so0 + b1 * d.so1;
-    const int ldo = partial ? 64 : d.ldo, ocols = partial ? 64 : d.hd;
-    const bool f32out = partial || d.odt == DT_F32;
-
-    if (partial && h == 0 && qi < N) {
-        float *ml = part + (long)d.nb * nsplit * Np * 64 + (pidx + qi) * 2;
-
-        ml[0] = st.m;
-        ml[1] = st.l;
+    if constexpr (SPL) {
+        if (!split_merge<!H32>(part, sk.cnt, unit * ntiles + tile, nsplit, sp, !idle, st.o0,
+                               st.o1, st.m, st.l))
+            return;
     }
+    /* Final O / l. */
+    const float inv = 1.0f / st.l;
+    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
+    void *const Obuf = d.O;
+    const long obase = d.ooff + b0 * d.so0 + b1 * d.so1;
+    const int ldo = d.ldo, ocols = d.hd;
+    const bool f32out = d.odt == DT_F32;
+
     if ((((obase | (long)ldo) & (f32out ? 3 : 7)) | ((uintptr_t)Obuf & 15)) == 0) {
         /* Output rows 16-byte aligned: transpose the wave's O^T through
          * LDS so that 8 lanes write one 128-byte line of one query row.
@@ -1273,7 +1328,7 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
     }
 }
 
-template <bool EXT, bool H32, bool SK>
+template <bool EXT, bool H32, bool SK, bool SPL>
 __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
                                                       const uint16_t *__restrict__ q16,
                                                       const uint16_t *__restrict__ k16,
@@ -1292,10 +1347,9 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
 
     if (!SK) {
         /* One (unit, query tile, key split) item per workgroup: split sp
-         * takes key blocks [sp nblk / nsplit, (sp + 1) nblk / nsplit) and,
-         * with nsplit > 1, leaves partial (O, m, l) records in `part` for
-         * k_attn_merge. 32-bit item arithmetic (the launcher keeps the
-         * grid below 2^31). */
+         * takes key blocks [sp nblk / nsplit, (sp + 1) nblk / nsplit); with
+         * nsplit > 1 (SPL) the splits merge inside the launch. 32-bit item
+         * arithmetic (the launcher keeps the grid below 2^31). */
         const unsigned total = (unsigned)d.nb * ntiles * nsplit, item = rank;
 
         if (item >= total)
@@ -1307,8 +1361,8 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
 
         const int kb0 = (int)((long)sp * nblk / nsplit), kb1 = (int)((long)(sp + 1) * nblk / nsplit);
 
-        attn_tile<EXT, H32, false>(d, q16, k16, vt16, knorm, part, nsplit, sp, sk, rank,
-                                   unit, tile, kb0, kb1, 0, kb1 - kb0, 0, 0);
+        attn_tile<EXT, H32, false, SPL>(d, q16, k16, vt16, knorm, part, nsplit, sp, sk, rank,
+                                        unit, tile, kb0, kb1, 0, kb1 - kb0, 0, 0);
         return;
     }
     /* Balanced launch (sk_desc): XCD x (workgroup g runs on XCD g % NXCD)
@@ -1352,7 +1406,7 @@ __global__ __launch_bounds__(256, 3) void k_attn_bf16(attn_desc d,
         kdesc *dp = (kdesc *)__builtin_amdgcn_kernarg_segment_ptr();
 
         asm volatile("" : "+s"(dp));
-        attn_tile<EXT, H32, true>(*dp, q16, k16, vt16, knorm, part, 1, 0, sk,
+        attn_tile<EXT, H32, true, false>(*dp, q16, k16, vt16, knorm, part, 1, 0, sk,
                                   x * (unsigned)sk.G + (unsigned)sidx, tid / ntiles, tid % ntiles,
                                   k0, k1, a - a0, b - a0, rbase, R);
         a += k1 - k0;
@@ -1701,124 +1755,6 @@ extern "C" int launch_attn_bf16_grp(const attn_desc *d, const void *q16, const v
     return hipGetLastError();
 }
 
-/* Merge of a few key-split partials (nsplit <= 8): 16 threads per
- * (unit, query), four channels each, looping over the splits: M = the
- * largest m_s over splits that saw a key, O = sum w_s o_s / sum w_s l_s
- * with w_s = 2^(m_s - M), stored like the kernel's own epilogue. */
-__global__ __launch_bounds__(256) void k_attn_merge_few(attn_desc d,
-                                                        const float *__restrict__ part,
-                                                        int nsplit, int Np)
-{
-    const long g = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const int c4 = (threadIdx.x & 15) * 4;
-
-    if (g >= (long)d.nb * d.N || c4 >= d.hd)
-        return;
-    const long unit = g / d.N;
-    const int q = (int)(g % d.N);
-    const float *ml = part + (long)d.nb * nsplit * Np * 64;
-    float M = -INFINITY, L = 0.0f;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    for (int sp = 0; sp < nsplit; sp++) {
-        const float *p = ml + ((unit * nsplit + sp) * Np + q) * 2;
-
-        if (p[1] > 0.0f)
-            M = fmaxf(M, p[0]);
-    }
-    for (int sp = 0; sp < nsplit; sp++) {
-        const long r = (unit * nsplit + sp) * Np + q;
-        const float *p = ml + r * 2;
-
-        if (p[1] > 0.0f) {
-            const float wt = __builtin_amdgcn_exp2f(p[0] - M);
-            const f32x4 o = *(const f32x4 *)(part + r * 64 + c4);
-
-            L = fmaf(wt, p[1], L);
-            acc += wt * o;
-        }
-    }
-    const float inv = 1.0f / L;
-    const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-    const long o = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + c4;
-
-    for (int e = 0; e < 4; e++) {
-        if (d.odt == DT_F32)
-            ((float *)d.O)[o + e] = acc[e] * inv;
-        else
-            ((uint16_t *)d.O)[o + e] = f2bf(acc[e] * inv);
-    }
-}
-
-/* Merge of key-split partials (k_attn_bf16 with 8 < nsplit <= 64): a
- * wave per (unit, query). Lane s holds split s's (m, l): M = the largest m
- * over splits that saw a key, weights w_s = 2^(m_s - M), L = sum w_s l_s
- * (wave reductions). The wave then reads four splits at a time: lane
- * group g = l / 16 takes splits g, g + 4, ..., each lane four channels
- * (one coalesced 256-byte row per split and group), and the groups' sums
- * meet by two cross-lane exchanges; O = sum / L is stored like the
- * kernel's own epilogue (hd columns, fp32 or bf16). */
-__global__ __launch_bounds__(256) void k_attn_merge(attn_desc d, const float *__restrict__ part,
-                                                    int nsplit, int Np)
-{
-    const int l = threadIdx.x & 63, grp = l >> 4, c4 = (l & 15) * 4;
-    const long g = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-
-    if (g >= (long)d.nb * d.N)
-        return;
-    const long unit = g / d.N;
-    const int q = (int)(g % d.N);
-    const float *ml = part + (long)d.nb * nsplit * Np * 64;
-    float ms = -INFINITY, ls = 0.0f;
-
-    if (l < nsplit) {
-        const float *p = ml + ((unit * nsplit + l) * Np + q) * 2;
-
-        ms = p[0];
-        ls = p[1];
-    }
-    const float M = wave_max(ls > 0.0f ? ms : -INFINITY);
-    const float wt = ls > 0.0f ? __builtin_amdgcn_exp2f(ms - M) : 0.0f;
-    const float L = wave_sum(wt * ls);
-    const float *o = part + ((unit * nsplit) * Np + q) * 64 + c4;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-
-    /* Every lane runs the same trip count, so that each shuffle sees all
-     * 64 lanes active: a shuffle from an inactive lane reads 0, and with
-     * nsplit % 4 != 0 the groups' own loops would end at different
-     * iterations (the last ones reading a weight held by a group that had
-     * left its loop). Splits past nsplit have weight 0 and load nothing. */
-    const int trips = (nsplit + 3) / 4;
-
-#pragma unroll 4
-    for (int it = 0; it < trips; it++) {
-        const int sp = 4 * it + grp;
-        const float w_s = __shfl(wt, sp, 64);
-
-        if (sp < nsplit) {
-            const f32x4 v = *(const f32x4 *)(o + (long)sp * Np * 64);
-
-            acc += w_s * v;
-        }
-    }
-    for (int e = 0; e < 4; e++) {
-        acc[e] += __shfl_xor(acc[e], 16, 64);
-        acc[e] += __shfl_xor(acc[e], 32, 64);
-    }
-    if (grp == 0 && c4 < d.hd) {
-        const long b0 = unit / d.nb1, b1 = unit % d.nb1;
-        const long oi = d.ooff + b0 * d.so0 + b1 * d.so1 + (long)q * d.ldo + c4;
-        const float inv = 1.0f / L;
-
-        for (int e = 0; e < 4 && c4 + e < d.hd; e++) {
-            if (d.odt == DT_F32)
-                ((float *)d.O)[oi + e] = acc[e] * inv;
-            else
-                ((uint16_t *)d.O)[oi + e] = f2bf(acc[e] * inv);
-        }
-    }
-}
-
 /* Zero fill of the balanced attention's arrival counters (a kernel, not
  * a memset, so that it may sit in a captured graph). */
 __global__ __launch_bounds__(256) void k_attn_sk_zero(unsigned *cnt, long n)
@@ -1844,15 +1780,17 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                                 float *skrec, unsigned *skcnt, int skG, int skdp,
                                 void *stream)
 {
-    const int Np = (d->N + 63) / 64 * 64, nblk = (d->Nk + 63) / 64;
+    const int nblk = (d->Nk + 63) / 64;
     const long tiles = (long)d->nb * ((d->N + 127) / 128);
     const long total = tiles * nsplit, per = (tiles + NXCD - 1) / NXCD;
     const long grid = skG ? (long)NXCD * (skdp + skG) : (total + NXCD - 1) / NXCD * NXCD;
     const sk_desc sk = {skrec, skcnt, skG, skdp};
-    int err;
 
+    /* Key splits merge inside the launch: their records in part (nb,
+     * 128-query tiles, SPLIT_RECS(nsplit) records of 9216 floats) and
+     * SPLIT_CNT arrival counts per tile in skcnt. */
     if (grid > 0x7fffffffL || d->Nk < 1 || nsplit < 1 || nsplit > nblk || nsplit > 64 ||
-        (nsplit > 1 && !part))
+        (nsplit > 1 && (!part || !skcnt)))
         return hipErrorInvalidConfiguration;
     /* Balanced launch: whole-key tiles, head width 64 without bias or
      * causal mask, some tiles left over on an XCD after dp whole ones and
@@ -1863,27 +1801,22 @@ extern "C" int launch_attn_bf16(const attn_desc *d, const void *q16,
                 !skrec || !skcnt || d->bias || d->causal || d->hd != 64))
         return hipErrorInvalidConfiguration;
     {
-        auto kern = skG ? k_attn_bf16<false, false, true>
-                    : d->bias || d->causal ? (d->hd == 32 ? k_attn_bf16<true, true, false>
-                                                          : k_attn_bf16<true, false, false>)
-                                           : (d->hd == 32 ? k_attn_bf16<false, true, false>
-                                                          : k_attn_bf16<false, false, false>);
+        const bool ext = d->bias || d->causal, h32 = d->hd == 32;
+        auto kern = skG ? k_attn_bf16<false, false, true, false>
+                    : nsplit > 1
+                        ? (ext ? (h32 ? k_attn_bf16<true, true, false, true>
+                                      : k_attn_bf16<true, false, false, true>)
+                               : (h32 ? k_attn_bf16<false, true, false, true>
+                                      : k_attn_bf16<false, false, false, true>))
+                        : (ext ? (h32 ? k_attn_bf16<true, true, false, false>
+                                      : k_attn_bf16<true, false, false, false>)
+                               : (h32 ? k_attn_bf16<false, true, false, false>
+                                      : k_attn_bf16<false, false, false, false>));
 
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, *d,
                            (const uint16_t *)q16, (const uint16_t *)k16,
                            (const uint16_t *)vt16, knorm, part, nsplit, sk);
     }
-    err = hipGetLastError();
-    if (err != hipSuccess || nsplit == 1)
-        return err;
-    if (nsplit <= 8)
-        hipLaunchKernelGGL(k_attn_merge_few, dim3((unsigned)(((long)d->nb * d->N + 15) / 16)),
-                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
-                           nsplit, Np);
-    else
-        hipLaunchKernelGGL(k_attn_merge, dim3((unsigned)(((long)d->nb * d->N + 3) / 4)),
-                           dim3(256), 0, (hipStream_t)stream, *d, (const float *)part,
-                           nsplit, Np);
     return hipGetLastError();
 }
 

@@ -142,11 +142,9 @@ struct attn_desc {
  * queries over Nk keys, head width 64 or 32 (no RoPE), the causal mask or
  * an additive bias table in natural units (d->bias, as launch_box_bias
  * with unit_scale 1 writes it). With 1 < nsplit <= 64 the 32-key blocks
- * are split nsplit ways in the same launch: `part` (nb, (N + 127) / 128
- * tiles, nsplit, 4 x 9216 floats) holds each split's records and
- * `cnt` (nb (N + 127) / 128 counts, zero before the launch and again
- * after it) counts the splits of each tile in; the last to arrive merges
- * them in split order. */
+ * are split nsplit ways in the same launch: `part` (nb ceil(N / 128)
+ * SPLIT_RECS(nsplit) 9216 floats) holds the records and `cnt` (nb
+ * ceil(N / 128) SPLIT_CNT counts) the arrival counts. */
 int launch_attn_f32(const struct attn_desc *d, float *part, unsigned *cnt, int nsplit,
                     void *stream);
 
@@ -157,10 +155,19 @@ int launch_attn_f32(const struct attn_desc *d, float *part, unsigned *cnt, int n
 int launch_qkv_pack(const struct attn_desc *d, void *q16, void *k16,
                     void *vt16, float *knorm, void *stream);
 
+/* Key splits merged inside their launch (both attention paths): per
+ * 128-query tile SPLIT_RECS(nsplit) records of 9216 floats (the splits',
+ * then one per group of SPLIT_GROUP splits) and SPLIT_CNT arrival counts,
+ * zero before a launch and left zero by it. */
+#define SPLIT_GROUP 8
+#define SPLIT_CNT (SPLIT_GROUP + 1)
+#define SPLIT_RECS(ns) ((ns) + ((ns) + SPLIT_GROUP - 1) / SPLIT_GROUP)
+
 /* bf16 MFMA attention on the packed operands; O addressed as in d. With
- * 1 < nsplit <= 64 the key blocks are split nsplit ways and `part` (nb nsplit
- * Np 66 floats, Np = N rounded up to 64) holds the partials that a merge
- * kernel combines into O. With skG > 0 (nsplit 1, head width 64 without
+ * 1 < nsplit <= 64 the key blocks are split nsplit ways and merged inside
+ * the launch: `part` (nb ceil(N / 128) SPLIT_RECS(nsplit) 9216 floats)
+ * holds the records and skcnt the counts (nb ceil(N / 128) SPLIT_CNT).
+ * With skG > 0 (nsplit 1, head width 64 without
  * bias or causal mask) the tiles of each XCD's share (the tile list in
  * eight contiguous parts) go to skdp whole-tile workgroups and skG
  * workgroups that share the rest's (tile, key block) pairs evenly:

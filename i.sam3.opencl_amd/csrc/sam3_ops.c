@@ -499,7 +499,7 @@ static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
 
     if (ns > nblk / 2)
         ns = nblk / 2;
-    if (ns > 64) /* the merge takes a split per lane */
+    if (ns > 64) /* the launchers' limit */
         ns = 64;
     return ns > 1 ? (int)ns : 1;
 }
@@ -508,8 +508,8 @@ static int attn_splits(const struct hipb_backend *b, int N, int Nk, int nb)
  * attention that the query tiles alone leave launch-starved (attn_splits
  * would split the keys): 4 groups of 64-query tiles when those tiles fit
  * on the CUs at once with two key blocks per group, else 2 groups of
- * 128-query tiles with two blocks each, else 0 (the split launch and its
- * merge kernel). One 576-token window of 16 heads: 144 workgroups of four
+ * 128-query tiles with two blocks each, else 0 (the split launch, its
+ * splits merged by their last workgroup). One 576-token window of 16 heads: 144 workgroups of four
  * groups of 2-3 key blocks. */
 static int attn_groups(const struct hipb_backend *b, const struct attn_desc *d, int N,
                        int Nk, int nb)
@@ -526,14 +526,12 @@ static int attn_groups(const struct hipb_backend *b, const struct attn_desc *d, 
     return 0;
 }
 
-/* Partial records for nsplit key splits of the bf16 path: nb nsplit Np
- * (64 + 2) floats; of the exact path (f32 set): nb, 128-query tiles,
- * nsplit, 4 waves of 9 x 64 x 4 floats. */
-static float *attn_part(struct sam_model *m, int N, int nb, int nsplit, int f32)
+/* Records of nsplit key splits merged inside their launch (both paths):
+ * nb, 128-query tiles, SPLIT_RECS(nsplit) records of 9216 floats. */
+static float *attn_part(struct sam_model *m, int N, int nb, int nsplit)
 {
-    const size_t np = ((size_t)N + 63) / 64 * 64, tiles = ((size_t)N + 127) / 128;
-    const size_t count = f32 ? (size_t)nb * tiles * nsplit * 4 * 9 * 64 * 4
-                             : (size_t)nb * nsplit * np * 66;
+    const size_t tiles = ((size_t)N + 127) / 128;
+    const size_t count = (size_t)nb * tiles * SPLIT_RECS((size_t)nsplit) * 9216;
 
     if (nsplit <= 1)
         return NULL;
@@ -542,10 +540,10 @@ static float *attn_part(struct sam_model *m, int N, int nb, int nsplit, int f32)
     return (float *)m->apart->ptr;
 }
 
-/* Arrival counts, one per (unit, 128-query tile), zero between launches:
- * zero-filled when (re)allocated, and every launch that counts tiles in
- * (the balanced bf16 launch, the exact path's key splits) resets each
- * count it used. */
+/* n arrival counts (one per 128-query tile for the balanced bf16 launch,
+ * SPLIT_CNT per tile for key splits), zero between launches: zero-filled
+ * when (re)allocated, and every launch that counts in resets each count it
+ * used. */
 static unsigned *attn_cnt(struct sam_model *m, long tiles)
 {
     struct hipb_backend *b = m->hip;
@@ -693,10 +691,11 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
             const int ns = ng ? 1 : attn_splits(b, N, Nk, nb);
             int dp;
             const int G = attn_sk(b, &d, N, Nk, nb, ns, &dp);
-            float *part = attn_part(m, N, nb, ns, 0), *skrec = NULL;
-            unsigned *skcnt = NULL;
+            float *part = attn_part(m, N, nb, ns), *skrec = NULL;
+            unsigned *skcnt =
+                ns > 1 ? attn_cnt(m, (long)nb * ((N + 127) / 128) * SPLIT_CNT) : NULL;
 
-            if ((ns > 1 && !part) ||
+            if ((ns > 1 && (!part || !skcnt)) ||
                 (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
                 return;
             hipb_run_begin(b);
@@ -710,31 +709,35 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
         return;
     }
     {
-        /* The exact kernel's key blocks are 32 keys: split by those into
-         * one round of workgroups, one per CU (at least two splits), at
-         * least three blocks per split. The splits merge inside the
-         * launch. One 576-token window of 16 heads: 3 splits of 6 blocks,
-         * 240 workgroups, 26.4 us; 6 splits of 3 blocks (two workgroups
-         * on most CUs) 27.4 us, 9 splits 33 us: every workgroup pays the
-         * Q load, the first block's copy and its record, and the merge
-         * reads every split's. */
+        /* The exact kernel's key blocks are 32 keys: split by those, at
+         * least three blocks per split, into one full round of three
+         * workgroups per CU when the blocks allow it, else one round of
+         * one per CU (at least two splits); the splits merge inside the
+         * launch. A round that leaves most CUs with two workgroups and
+         * some with one ran slower than either. One 576-token window of
+         * 16 heads (80 tiles, 18 blocks): 3 splits, 240 workgroups, 26.0
+         * us (6 splits 27.4 us, 9 splits 33 us); the decoder's box-biased
+         * cross-attention (16 tiles, 162 blocks): 48 splits, 768
+         * workgroups, 42.1 us (27 splits 44.1 us, 16 splits 50.2 us). */
         int ns = attn_splits(b, N, Nk, nb);
 
         if (ns > 1) {
             const int cus = b->cu_count > 0 ? b->cu_count : 256;
-            const long items = (long)nb * ((N + 127) / 128);
-            long n32 = cus / items;
+            const long items = (long)nb * ((N + 127) / 128), cap = (Nk + 31) / 32 / 3;
+            long n32 = 3L * cus / items;
 
+            if (n32 > cap)
+                n32 = cus / items;
             if (n32 < 2)
                 n32 = 2;
-            if (n32 > (Nk + 31) / 32 / 3)
-                n32 = (Nk + 31) / 32 / 3;
+            if (n32 > cap)
+                n32 = cap;
             if (n32 > 64)
                 n32 = 64;
             ns = n32 > 1 ? (int)n32 : 1;
         }
-        float *part = attn_part(m, N, nb, ns, 1);
-        unsigned *cnt = ns > 1 ? attn_cnt(m, (long)nb * ((N + 127) / 128)) : NULL;
+        float *part = attn_part(m, N, nb, ns);
+        unsigned *cnt = ns > 1 ? attn_cnt(m, (long)nb * ((N + 127) / 128) * SPLIT_CNT) : NULL;
 
         if (ns > 1 && (!part || !cnt))
             return;
@@ -796,7 +799,9 @@ void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
     ng = attn_groups(b, &d, N, N, nb);
     ns = ng ? 1 : attn_splits(b, N, N, nb);
     G = attn_sk(b, &d, N, N, nb, ns, &dp);
-    part = attn_part(m, N, nb, ns, 0);
+    part = attn_part(m, N, nb, ns);
+    if (ns > 1 && !(skcnt = attn_cnt(m, (long)nb * ((N + 127) / 128) * SPLIT_CNT)))
+        return;
     if ((ns > 1 && !part) ||
         (G && !attn_skbuf(m, G, (long)nb * ((N + 127) / 128), &skrec, &skcnt)))
         return;

@@ -70,11 +70,13 @@ def test_single_window(hip, be, orc):
 
 def test_split_launch_repeats(hip, be, orc):
     """Launch-starved shapes merge their key splits inside the one launch
-    (the exact path: the last split of a tile to arrive merges all of them
-    in split order; bf16: key groups inside the workgroup). The same bits
-    on every launch, and each launch leaves its arrival counts at zero for
-    the next one of another tile count: one 576-token window of 16 heads,
-    then 1000 tokens of 2 heads with RoPE, then the window again."""
+    (the exact path: 3 splits of the window's tiles, folded in order by the
+    last to arrive; 10 splits of the 1000-token tiles, in groups of 8 and
+    2 and then across the groups; bf16: key groups inside the workgroup).
+    The same bits on every launch, and each launch leaves its arrival
+    counts at zero for the next one of another tile count: one 576-token
+    window of 16 heads, then 1000 tokens of 2 heads with RoPE, then the
+    window again."""
     N, H, E = 576, 16, 1024
     m = hip.Model(be, embed=E, heads=H)
     qkv = np.random.default_rng(12).standard_normal((N, 3 * E), np.float32)

@@ -152,11 +152,10 @@ def test_long_causal_split_keys(hip, be, orc):
 
 def test_key_splits_not_a_multiple_of_four(hip, be, orc):
     """5700 causal tokens, one head of 64: 45 query tiles split the keys 17
-    ways on the bf16 path (causal attention takes the split launch there;
-    the exact path splits them 5 ways and merges inside its launch). The
-    merge kernel's four lane groups then take 5, 4, 4 and 4 splits; its
-    weights are shuffled between lanes, which must all be active (a lane
-    that had left its loop would hand over 0 and drop a split)."""
+    ways on both paths (causal attention takes the split launch on bf16
+    too), merged inside the launch in groups of 8, 8 and 1 (a short last
+    group), the groups then folded by the last group to finish; splits
+    past a query's position see no key and drop out."""
     n, heads, hd = 5700, 1, 64
     g = np.random.default_rng(37)
     Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
@@ -169,9 +168,9 @@ def test_key_splits_not_a_multiple_of_four(hip, be, orc):
 def test_one_head_many_key_splits(hip, be, orc):
     """2000 tokens, one head of 64: 16 query tiles leave the GPU idle. The
     exact path splits the keys 16 ways and merges the splits inside its
-    launch; the bf16 path takes the grouped launch (four key groups per
-    workgroup, merged in LDS). The bias case above takes 40 bf16 splits
-    and the wave-per-query merge kernel."""
+    launch (two groups of eight); the bf16 path takes the grouped launch
+    (four key groups per workgroup, merged in LDS). The bias case above
+    takes 40 bf16 splits (five groups) and 48 exact ones (six)."""
     n, heads, hd = 2000, 1, 64
     g = np.random.default_rng(36)
     Q, K, V = (g.standard_normal((n, heads * hd)).astype(np.float32)
@@ -185,9 +184,10 @@ def test_one_head_many_key_splits(hip, be, orc):
 def test_sixty_four_key_splits(hip, be, orc):
     """256 queries over 8192 keys, one head of 64: two query tiles, so the
     exact path splits the keys the most it does, 64 ways (four 32-key
-    blocks each), and merges them inside its launch three at a time (the
-    last round one split and two repeats that must add nothing); the bf16
-    path takes the grouped launch. A second launch gives the same bits."""
+    blocks each), merged inside its launch in eight groups of eight, three
+    records at a time (the last round of each group one record and a repeat
+    that must add nothing); the bf16 path takes the grouped launch. A
+    second launch gives the same bits."""
     nq, nk, heads, hd = 256, 8192, 1, 64
     g = np.random.default_rng(38)
     Q = g.standard_normal((nq, hd)).astype(np.float32)

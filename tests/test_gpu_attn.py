@@ -140,13 +140,13 @@ def test_grouped_launch(hip, be, orc, N, nunits, H):
     """Shapes whose query tiles leave the device launch-starved take, on
     the bf16 path, one launch whose workgroups split the key blocks
     between groups of waves and merge them in LDS in group order (no
-    partials, no merge kernel): one 576-token window of 16 heads (four
+    records in memory): one 576-token window of 16 heads (four
     groups of 64-query tiles, every key block resident in LDS), 700 tokens
     (four double-buffered groups; 60 keys in the last block, 60 queries in
     the last tile) and 300 tokens (two groups of 128-query tiles; 44 keys
     in the last block). The exact path splits the 32-key blocks across
-    workgroups and merges the partials. Every row against the oracle, and
-    a relaunch gives the same bits."""
+    workgroups and merges their records inside the launch. Every row
+    against the oracle, and a relaunch gives the same bits."""
     E = 64 * H
     m = hip.Model(be, embed=E, heads=H)
     side = math.isqrt(N)

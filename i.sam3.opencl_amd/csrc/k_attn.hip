@@ -1169,13 +1169,15 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
             return;
         if (t == 0)
             __hip_atomic_store(&sk.cnt[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        /* The merge does not depend on which piece arrived last: every
-         * piece's (O, l) is scaled to the pieces' largest m, M, and the
-         * scaled pieces are summed in piece order r0 .. r1, this piece's
-         * own state (the bits of its record) at its own place. (The
-         * records' m first, then the sums: one more wait on memory than a
-         * merge in arrival order, 1.7 % on the global ViT block; holding
-         * two records at once spills in this instance and costs more.) */
+        /* The merge does not depend on which piece arrived last: the
+         * pieces are folded in piece order r0 .. r1 into a running (M, L,
+         * O), as the online softmax folds blocks (O and L rescaled by
+         * 2^(M_old - M) when M grows, the piece added with weight
+         * 2^(m_r - M)), this piece's own state (the bits of its record) at
+         * its own place. One wait on memory per other piece, its 34 loads
+         * in flight together. (The pieces' largest m read first, then the
+         * sums: one more wait, 1.7 % on the global ViT block; holding two
+         * records at once spills in this instance.) */
         auto rec_of = [&](int r) {
             return sk.rec + ((long)slot_of(r) * 4 + w) * 34 * 64 + l;
         };
@@ -1183,30 +1185,37 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
             return __hip_atomic_load(pr + 64 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         };
         f32x16 a0 = zero16, a1 = zero16;
-        float L = 0.0f, M = st.m;
+        float L = 0.0f, M = -INFINITY;
 
-        for (int r = r0; r <= r1; r++)
-            if (r != me)
-                M = __builtin_fmaxf(M, get(rec_of(r), 32));
         for (int r = r0; r <= r1; r++) {
+            f32x16 p0, p1;
+            float pm, pl;
+
             if (r == me) {
-                const float c = __builtin_amdgcn_exp2f(st.m - M);
+                p0 = st.o0;
+                p1 = st.o1;
+                pm = st.m;
+                pl = st.l;
+            }
+            else {
+                const float *pr = rec_of(r);
 
                 for (int r2 = 0; r2 < 16; r2++) {
-                    a0[r2] = fmaf(st.o0[r2], c, a0[r2]);
-                    a1[r2] = fmaf(st.o1[r2], c, a1[r2]);
+                    p0[r2] = get(pr, r2);
+                    p1[r2] = get(pr, 16 + r2);
                 }
-                L = fmaf(st.l, c, L);
-                continue;
+                pm = get(pr, 32);
+                pl = get(pr, 33);
             }
-            const float *pr = rec_of(r);
-            const float c = __builtin_amdgcn_exp2f(get(pr, 32) - M);
+            const float Mn = __builtin_fmaxf(M, pm);
+            const float ca = __builtin_amdgcn_exp2f(M - Mn), cp = __builtin_amdgcn_exp2f(pm - Mn);
 
             for (int r2 = 0; r2 < 16; r2++) {
-                a0[r2] = fmaf(get(pr, r2), c, a0[r2]);
-                a1[r2] = fmaf(get(pr, 16 + r2), c, a1[r2]);
+                a0[r2] = fmaf(p0[r2], cp, a0[r2] * ca);
+                a1[r2] = fmaf(p1[r2], cp, a1[r2] * ca);
             }
-            L = fmaf(get(pr, 33), c, L);
+            L = fmaf(pl, cp, L * ca);
+            M = Mn;
         }
         st.o0 = a0;
         st.o1 = a1;

@@ -86,11 +86,41 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
 }
 
+/* Sum over a wave64, the same bits in every lane: DPP adds inside each
+ * row of 16 lanes (swap within pairs, then within quads, then the half-row
+ * and row mirrors: every lane of a row ends with the row's sum), then the
+ * four row sums read into scalars and added in a fixed order. Six dependent
+ * VALU steps instead of six LDS-crossbar round trips of the shuffle form. */
+__device__ __forceinline__ float wave_sum_rows(float v)
+{
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                       0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16)),
+                r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+
+    return (r0 + r1) + (r2 + r3);
+}
+
 /* Rows of C = 256 V floats (V <= 16): one wave per output row, four
  * rows per workgroup. Lane l holds floats 4 l + 256 i .. +3 (i < V) in
- * registers from one 16-byte load each; the mean and variance close with
- * wave butterflies (no LDS, no barrier); outputs leave as 16-byte (float)
- * or 8-byte (bf16) stores. Window partition as in k_layernorm. */
+ * registers from one 16-byte load each, its gamma and beta loaded beside
+ * them for C <= 2048 (not after the sums, where they would add an L2 trip
+ * to every wave's path); the mean and variance close with wave_sum_rows
+ * (no LDS, no barrier); outputs leave as 16-byte (float) or 8-byte (bf16)
+ * stores.
+ * Window partition as in k_layernorm, in 32-bit arithmetic (the launcher
+ * keeps the rows below 2^32). At 5184 x 1024 (bf16 out) after a kernel
+ * that wrote X: 7.9 -> 6.6 us against the shuffle sums with late gamma /
+ * beta loads and 64-bit partition divisions. */
 template <typename TY, int V>
 __global__ __launch_bounds__(256) void k_layernorm_w(
     const float *__restrict__ X, TY *__restrict__ Y, const float *__restrict__ g,
@@ -98,50 +128,66 @@ __global__ __launch_bounds__(256) void k_layernorm_w(
     int ws, int nwx)
 {
     constexpr int C = 256 * V;
+    /* Gamma and beta held from the start up to 8 float4 each (96 VGPRs
+     * with the row); wider rows load them at the end. */
+    constexpr bool EARLY = V <= 8;
     const int l = threadIdx.x & 63;
-    const long r = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    long src = r;
-    f32x4 v[V];
+    const unsigned r = blockIdx.x * 4u + (threadIdx.x >> 6);
+    unsigned src = r;
+    f32x4 v[V], gv[V], bv[V];
     float s = 0.0f, mean, var, rs;
 
     if (r >= rows)
         return;
-    TY *yr = Y + r * C + 4 * l;
+    TY *yr = Y + (long)r * C + 4 * l;
     if (ws > 0) {
-        const int w = (int)(r / ((long)ws * ws)), p = (int)(r % ((long)ws * ws));
-        const int y = (w / nwx) * ws + p / ws, x = (w % nwx) * ws + p % ws;
+        const unsigned a = (unsigned)ws * (unsigned)ws, w = r / a, p = r - w * a;
+        const unsigned wy = w / (unsigned)nwx, py = p / (unsigned)ws;
+        const unsigned y = wy * ws + py, x = (w - wy * nwx) * ws + (p - py * ws);
 
-        if (y >= H || x >= H) {
+        if (y >= (unsigned)H || x >= (unsigned)H) {
             for (int i = 0; i < V; i++)
                 for (int e = 0; e < 4; e++)
                     yr[256 * i + e] = (TY)0.0f;
             return;
         }
-        src = (long)y * H + x;
+        src = y * (unsigned)H + x;
     }
-    const float *xr = X + src * C + 4 * l;
-    for (int i = 0; i < V; i++) {
+    const float *xr = X + (long)src * C + 4 * l;
+    for (int i = 0; i < V; i++)
         v[i] = *(const f32x4 *)(xr + 256 * i);
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    if constexpr (EARLY) {
+        for (int i = 0; i < V; i++) {
+            gv[i] = *(const f32x4 *)(g + 4 * l + 256 * i);
+            bv[i] = *(const f32x4 *)(bt + 4 * l + 256 * i);
+        }
+        /* Keeps all loads issued here (the compiler otherwise sinks gamma
+         * and beta below the sums). */
+        for (int i = 0; i < V; i++)
+            asm volatile("" : "+v"(v[i]), "+v"(gv[i]), "+v"(bv[i]));
     }
-    mean = wave_sum(s) / (float)C;
+    for (int i = 0; i < V; i++)
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    mean = wave_sum_rows(s) / (float)C;
     s = 0.0f;
     for (int i = 0; i < V; i++) {
         const f32x4 dv = v[i] - mean;
 
         s = fmaf(dv.x, dv.x, fmaf(dv.y, dv.y, fmaf(dv.z, dv.z, fmaf(dv.w, dv.w, s))));
     }
-    var = wave_sum(s) / (float)C;
+    var = wave_sum_rows(s) / (float)C;
     rs = 1.0f / sqrtf(var + eps);
     for (int i = 0; i < V; i++) {
-        const int c = 4 * l + 256 * i;
-        const f32x4 gv = *(const f32x4 *)(g + c), bv = *(const f32x4 *)(bt + c);
         f32x4 o;
 
-        o.x = act_k(fmaf((v[i].x - mean) * rs, gv.x, bv.x), act);
-        o.y = act_k(fmaf((v[i].y - mean) * rs, gv.y, bv.y), act);
-        o.z = act_k(fmaf((v[i].z - mean) * rs, gv.z, bv.z), act);
-        o.w = act_k(fmaf((v[i].w - mean) * rs, gv.w, bv.w), act);
+        if constexpr (!EARLY) {
+            gv[i] = *(const f32x4 *)(g + 4 * l + 256 * i);
+            bv[i] = *(const f32x4 *)(bt + 4 * l + 256 * i);
+        }
+        o.x = act_k(fmaf((v[i].x - mean) * rs, gv[i].x, bv[i].x), act);
+        o.y = act_k(fmaf((v[i].y - mean) * rs, gv[i].y, bv[i].y), act);
+        o.z = act_k(fmaf((v[i].z - mean) * rs, gv[i].z, bv[i].z), act);
+        o.w = act_k(fmaf((v[i].w - mean) * rs, gv[i].w, bv[i].w), act);
         if constexpr (sizeof(TY) == 4)
             *(f32x4 *)(yr + 256 * i) = o;
         else {
@@ -220,7 +266,8 @@ extern "C" int launch_layernorm(const float *X, void *Y, int ydt,
     }
     /* 16-byte rows of the wave-per-row kernel: C a multiple of 256 up to
      * 4096 (the buffers are hipMalloc'd, so rows start 16-byte aligned). */
-    if (C % 256 == 0 && C <= 4096) {
+    if (C % 256 == 0 && C <= 4096 && out_rows <= 0xffffffffL &&
+        (ws == 0 || (long)H * H <= 0xffffffffL)) {
         const dim3 grid((unsigned)((out_rows + 3) / 4));
 
 #define LNW(V)                                                                \

@@ -189,14 +189,20 @@ __device__ __forceinline__ bool split_merge(float *__restrict__ part, unsigned *
     }
 }
 
+/* Scores may run this far (log2 units) above or below the reference
+ * point m before it must move: exp2 of them stays far inside the float
+ * and bf16 ranges, and the accumulated O and l with it (5184 keys x 2^64
+ * x |v|). */
+#define SAFE_SPAN 64.0f
+
 /* ------------------------------------------------------------ fp32 path */
 
 /* fp32 operands in the reference row layout (Q/K/V/O opnds of
  * sam3_model.c:1004-1011, or the Q, K, V, O rows of the text path's
  * attend, sam3_text.c:305-343), v_mfma_f32_32x32x2_f32, 32-key blocks:
  * the exact path. N queries over Nk keys per unit, head width HD (64, or
- * 32 for the text path's heads). RoPE (HD 64) and the scale are applied
- * on the loads. The contraction index of Q K^T is ordered
+ * 32 for the text path's heads). RoPE (HD 64) is applied on the loads,
+ * the scale to the scores. The contraction index of Q K^T is ordered
  * d = step + (HD / 2) h, so a lane's Q registers are one contiguous half
  * row and RoPE pairs stay in one lane.
  *
@@ -257,7 +263,8 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
     const bool loader = t < 32 * LPR;
     float qreg[HH], kpre[8], vpre[8];
     f32x16 o0, o1;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = 0.0f, l_run = 0.0f;
+    const float sc2 = d.scale * LOG2E_F;
 
     /* Q: lane holds channels HH h .. HH h + HH - 1 of query qi, rotated
      * and scaled. */
@@ -335,17 +342,38 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
                                                      0, 0);
         return s;
     };
-    /* Scale, mask keys past Nk, the causal mask or the bias, online
-     * softmax of block kb's scores s, then O^T += V^T P^T from buffer buf.
-     * Register r holds key kb 32 + 8 (r / 4) + 4 h + r % 4. */
+    /* Scores in log2 units relative to the lane's reference point m
+     * (m_run, log2 units, the same in lanes l and l ^ 32): t = s scale
+     * log2(e) - m as one rounding, keys past Nk (last block), the causal
+     * mask or the bias (added to the scaled score, natural units, as
+     * softmax_ext adds it) applied; then P = exp2(t), O^T += V^T P^T from
+     * buffer buf. Register r holds key kb 32 + 8 (r / 4) + 4 h + r % 4.
+     * m is the first block's max, then moves only when a score leaves
+     * [m - SAFE_SPAN, m + SAFE_SPAN]: up (O and l shrink) when the block
+     * max passes m + SAFE_SPAN, down while the query has no weight yet
+     * and its block max lies below m - SAFE_SPAN. After the first block a
+     * wave takes the exact max (its cross-lane exchange, the rescale of O
+     * and l) only for blocks whose in-lane maxima it cannot clear; O / l
+     * does not depend on m. */
     auto soft_pv = [&](f32x16 s, int kb, int buf) {
-        float mx, m_new, mref, corr, rs = 0.0f;
+        float rs = 0.0f, mx = -INFINITY;
 
-        for (int r = 0; r < 16; r++) {
-            const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (EXT && brow)
+            for (int g = 0; g < 4; g++) {
+                const f32x4 bv = *(const f32x4 *)(brow + kb * 32 + 8 * g + 4 * h);
 
-            s[r] = key < Nk ? s[r] * d.scale : -INFINITY;
-        }
+                for (int e = 0; e < 4; e++)
+                    s[4 * g + e] = fmaf(s[4 * g + e] * d.scale + bv[e], LOG2E_F, -m_run);
+            }
+        else
+            for (int r = 0; r < 16; r++)
+                s[r] = fmaf(s[r], sc2, -m_run);
+        if (kb * 32 + 32 > Nk)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+
+                s[r] = key < Nk ? s[r] : -INFINITY;
+            }
         if (EXT && d.causal)
             for (int r = 0; r < 16; r++) {
                 const int key = kb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -353,33 +381,40 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
                 if (key > qi)
                     s[r] = -INFINITY;
             }
-        else if (EXT && brow)
-            for (int g = 0; g < 4; g++) {
-                const f32x4 bv = *(const f32x4 *)(brow + kb * 32 + 8 * g + 4 * h);
-
-                for (int e = 0; e < 4; e++)
-                    s[4 * g + e] += bv[e];
-            }
-        mx = -INFINITY;
         for (int r = 0; r < 16; r++)
             mx = fmaxf(mx, s[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        m_new = fmaxf(m_run, mx);
-        /* No key seen yet (all masked so far): nothing to rescale, and
-         * every weight of this block is 0. */
-        mref = m_new == -INFINITY ? 0.0f : m_new;
-        corr = m_run == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m_run - mref) * LOG2E_F);
+        if (kb == kb0 || __ballot(mx > SAFE_SPAN || (l_run == 0.0f && mx < -SAFE_SPAN &&
+                                                    mx != -INFINITY)) != 0) {
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const bool empty = l_run + __shfl_xor(l_run, 32, 64) == 0.0f;
+            /* The first block sets m to its max outright, as the reference's
+             * softmax does (that key's weight is then exactly 1: a query
+             * that sees one key gets its value row unchanged). */
+            const float mv = (kb == kb0 || mx > SAFE_SPAN || (empty && mx < -SAFE_SPAN)) &&
+                                     mx != -INFINITY
+                                 ? mx
+                                 : 0.0f;
+
+            if (kb != kb0) {
+                /* Moving down, the query has no weight to rescale. */
+                const float corr = __builtin_amdgcn_exp2f(-fmaxf(mv, 0.0f));
+
+                l_run *= corr;
+                for (int r = 0; r < 16; r++) {
+                    o0[r] *= corr;
+                    if (HD == 64)
+                        o1[r] *= corr;
+                }
+            }
+            for (int r = 0; r < 16; r++)
+                s[r] -= mv;
+            m_run += mv;
+        }
         for (int r = 0; r < 16; r++) {
-            s[r] = __builtin_amdgcn_exp2f((s[r] - mref) * LOG2E_F);
+            s[r] = __builtin_amdgcn_exp2f(s[r]);
             rs += s[r];
         }
-        l_run = l_run * corr + rs;
-        m_run = m_new;
-        for (int r = 0; r < 16; r++) {
-            o0[r] *= corr;
-            if (HD == 64)
-                o1[r] *= corr;
-        }
+        l_run += rs;
         /* The exponentials issued before the P V MFMAs: left to the
          * scheduler, which weighs the code after the key loop too, each
          * MFMA could follow the exponential it reads and wait for it
@@ -419,12 +454,9 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
     __builtin_amdgcn_s_setprio(0);
 
     l_run += __shfl_xor(l_run, 32, 64);
-    if constexpr (SPLIT) {
-        float mrec = m_run == -INFINITY ? 0.0f : m_run * LOG2E_F;
-
-        if (!split_merge<HD == 64>(part, cnt, item, nsplit, sp, !idle, o0, o1, mrec, l_run))
+    if constexpr (SPLIT)
+        if (!split_merge<HD == 64>(part, cnt, item, nsplit, sp, !idle, o0, o1, m_run, l_run))
             return;
-    }
     if (qi >= N)
         return;
     {
@@ -746,12 +778,6 @@ __device__ __forceinline__ void g2lds16_s(const void *base, unsigned voff, unsig
                  : "s"(lds), "v"(voff), "s"(base)
                  : "memory", "m0");
 }
-
-/* Scores may run this far (log2 units) above or below the reference
- * point m before it must move: exp2 of them stays far inside the float
- * and bf16 ranges, and the accumulated O and l with it (5184 keys x 2^64
- * x |v|). */
-#define SAFE_SPAN 64.0f
 
 /* Balanced launch of k_attn_bf16 when the tiles fill between two and
  * three workgroups per CU (the global ViT block: 82 tiles per XCD on 32

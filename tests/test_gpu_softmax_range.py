@@ -4,8 +4,9 @@ The reference's softmax_rows (sam3_kernels.cl:637-656), softmax_ext
 (:885-921) and attn_manykeys merge (:604-633) subtract each row's exact
 maximum, so they are exact whatever the size of the scores. The fused
 kernels here keep a lazy reference point instead: k_attn_bf16 moves it
-only when a score could leave a +-64 (log2 units) span, k_mha_many16 and
-k_t2i_fused when a score passes it by 8. These tests drive scores far past
+only when a score could leave a +-64 (log2 units) span, k_attn_f32 sets
+it to its first key block's maximum and then moves it the same way,
+k_mha_many16 and k_t2i_fused when a score passes it by 8. These tests drive scores far past
 those spans so that every branch of the moves runs:
 
 - rows whose first block already exceeds +64 (move up, nothing to

@@ -129,19 +129,21 @@ struct attn_desc {
     /* Head width: 64, or 32 on the bf16 path (packed with zero channels
      * 32..63, so the 64-wide kernel applies; 32 output columns stored). */
     int hd;
-    /* Keys per unit (N queries, Nk keys; K and V rows count Nk). bf16
-     * path only beyond Nk == N: the additive bias table [unit][N][Nk
-     * padded to 64] in the exp2 domain (-inf in the padding) or NULL, and
-     * the causal mask (key j > query i excluded). */
+    /* Keys per unit (N queries, Nk keys; K and V rows count Nk); beyond
+     * Nk == N: the box bias as rows [unit][N][H + W] of dy then dx values
+     * (launch_box_rows, H = Nk / bW), each key j biased by dy[j / bW] +
+     * dx[j % bW] (the bf16 kernel's rows scaled to its exp2 domain), or
+     * NULL; and the
+     * causal mask (key j > query i excluded). */
     int Nk;
     const float *bias;
+    int bW;
     int causal;
 };
 
-/* fp32 operands, f32 MFMA, RoPE and scale applied on the Q/K loads; N
- * queries over Nk keys, head width 64 or 32 (no RoPE), the causal mask or
- * an additive bias table in natural units (d->bias, as launch_box_bias
- * with unit_scale 1 writes it). With 1 < nsplit <= 64 the 32-key blocks
+/* fp32 operands, f32 MFMA, RoPE applied on the Q/K loads, the scale to
+ * the scores; N queries over Nk keys, head width 64 or 32 (no RoPE), the
+ * causal mask or the box bias (d->bias rows, d->bW) in natural units. With 1 < nsplit <= 64 the 32-key blocks
  * are split nsplit ways in the same launch: `part` (nb ceil(N / 128)
  * SPLIT_RECS(nsplit) 9216 floats) holds the records and `cnt` (nb
  * ceil(N / 128) SPLIT_CNT counts) the arrival counts. */
@@ -188,13 +190,12 @@ int launch_attn_bf16_grp(const struct attn_desc *d, const void *q16, const void 
 /* Zero the n counters of launch_attn_bf16's balanced launch. */
 int launch_attn_sk_zero(unsigned *cnt, long n, void *stream);
 
-/* Additive bias table of the fused attention from the box relative
- * position bias of softmax_ext: out [heads][Nq][Nk padded to 64] =
- * unit_scale (dy[(i H + j / W) nh + h] + dx[(i W + j % W) nh + h]), -inf in
- * the padding (H = Nk / W); unit_scale log2(e) for the bf16 kernel, 1 for
- * the exact path. */
-int launch_box_bias(float *out, const float *dy, const float *dx, int heads,
-                    int Nq, int Nk, int W, int nh, float unit_scale, void *stream);
+/* Bias rows of the fused attention from the box relative position bias
+ * of softmax_ext: out [heads][Nq][H + W] = unit_scale dy[(i H + y) nh + h]
+ * (y < H), then unit_scale dx[(i W + x) nh + h] (x < W), H = Nk / W;
+ * unit_scale 1 for the exact path, log2(e) for the bf16 kernel. */
+int launch_box_rows(float *out, const float *dy, const float *dx, int heads, int Nq,
+                    int Nk, int W, int nh, float unit_scale, void *stream);
 
 /* Decoder attention (8 heads, head width c = dint / 8). */
 int launch_mha_fewkeys(const float *Q, long sq, const float *K, long sk,

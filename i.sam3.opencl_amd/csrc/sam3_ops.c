@@ -607,7 +607,7 @@ static int attn_skbuf(struct sam_model *m, int G, long tiles, float **rec,
 static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
                           int Nk, int nb, int nb1, struct opnd Q, struct opnd K,
                           struct opnd V, struct opnd O, hipb_mem rope,
-                          int npos, float scale, int causal, hipb_mem bias)
+                          int npos, float scale, int causal, hipb_mem bias, int bW)
 {
     struct hipb_backend *b = m->hip;
     struct attn_desc d;
@@ -667,9 +667,14 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
     d.Nk = Nk;
     d.causal = causal != 0;
     d.bias = bias ? (const float *)bias->ptr : NULL;
-    if (bias && !buf_ok(who, "bias table", bias,
-                        (size_t)nb * N * (((size_t)Nk + 63) / 64 * 64), HIPB_F32))
+    d.bW = bias ? bW : 0;
+    if (bias && (bW < 1 || Nk % bW ||
+                 !buf_ok(who, "bias rows", bias, (size_t)nb * N * ((size_t)Nk / bW + bW),
+                         HIPB_F32))) {
+        if (!hipb_failed())
+            hipb_fatal("%s: bias rows need W dividing Nk", who);
         return;
+    }
     if (b->bf16) {
         const size_t np = ((size_t)N + 63) / 64 * 64;
         const size_t npk = ((size_t)Nk + 63) / 64 * 64;
@@ -756,7 +761,7 @@ void attn_fused(struct sam_model *m, int N, int nb, int nb1, struct opnd Q,
         return;
     }
     attn_fused_hd(m, "attn_fused", 64, N, N, nb, nb1, Q, K, V, O, rope, npos,
-                  scale, 0, NULL);
+                  scale, 0, NULL, 0);
 }
 
 void attn_packed(struct sam_model *m, int N, int nb, int nb1, struct opnd O)
@@ -839,30 +844,30 @@ void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
             hipb_fatal("attend: box bias needs dy, dx and W dividing Nk");
         return;
     }
-    /* Fused for head width 64 or 32 with any mask or bias, on both paths
-     * (the bias as a table: in the bf16 kernel's exp2 domain, or as the
-     * sums dy + dx for the exact path). Heads are the units, head h at
-     * column h hd of every operand. */
+    /* Fused for head width 64 or 32 with any mask or bias, on both paths.
+     * The box bias goes to the kernels as rows of each (head, query)'s dy
+     * and dx values, H + W floats, which they add as dy[j / W] + dx[j % W]
+     * per key (on the bf16 path both scaled to its exp2 domain first).
+     * Heads are the units, head h at column h hd of every operand. */
     if (hd == 64 || hd == 32) {
         if (dy) {
-            const size_t npk = ((size_t)Nk + 63) / 64 * 64;
             int err;
 
-            if (!ensure_typed(b, &m->abias, (size_t)heads * Nq * npk, HIPB_F32,
-                              "attention bias table"))
+            if (!ensure_typed(b, &m->abias, (size_t)heads * Nq * ((size_t)Nk / W + W),
+                              HIPB_F32, "attention bias rows"))
                 return;
             hipb_run_begin(b);
-            err = launch_box_bias((float *)m->abias->ptr, (const float *)dy->ptr,
-                                  (const float *)dx->ptr, heads, Nq, Nk, W,
-                                  heads, b->bf16 ? LOG2E_HOST : 1.0f, b->stream);
-            hipb_run_end(b, err, "box_bias", 0.0);
+            err = launch_box_rows((float *)m->abias->ptr, (const float *)dy->ptr,
+                                  (const float *)dx->ptr, heads, Nq, Nk, W, heads,
+                                  b->bf16 ? LOG2E_HOST : 1.0f, b->stream);
+            hipb_run_end(b, err, "box_rows", 0.0);
             if (hipb_failed())
                 return;
         }
         attn_fused_hd(m, "attend", hd, Nq, Nk, heads, heads,
                       bmat(Q, 0, ldq, 0, hd), bmat(K, 0, ldk, 0, hd),
                       bmat(V, 0, ldv, 0, hd), bmat(O, 0, ldo, 0, hd), NULL, 1,
-                      scale, causal, dy ? m->abias : NULL);
+                      scale, causal, dy ? m->abias : NULL, W);
         return;
     }
     /* The reference's sequence (sam3_text.c:305-343): per chunk of heads

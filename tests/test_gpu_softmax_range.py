@@ -26,7 +26,8 @@ every score q . k is an integer and exact in fp32.
 
 Oracles. fp32 path: the oracle (the reference's op sequence, bar 2e-5).
 bf16 path: exact float64 softmax attention of the operands the device
-packed (bf16 Q in log2 units, K, V^T, bias table: read back), bar 1e-2
+packed (bf16 Q in log2 units, K, V^T: read back; the box bias in float32
+as the device forms it), bar 1e-2
 (the kernel rounds the weights P to bf16 for the P V product). Against the
 fp32 oracle the bf16 path has no fixed bar here: a score of 300 log2
 units carries about 1 unit of bf16 input rounding. Each test also checks
@@ -88,16 +89,25 @@ def bf16_to_f64(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def packed_exact(be, m, nb, N, Nk, bias=False, causal=False):
+def box_bias_log2(dy, dx, W):
+    """The box bias [heads, Nq, Nk] the bf16 kernel adds in its exp2
+    domain: dy[j / W] log2(e) + dx[j % W] log2(e), rounded in float32 as
+    the device rounds it."""
+    H = dy.shape[1]
+    j = np.arange(H * W)
+    dyl, dxl = dy * np.float32(LOG2E), dx * np.float32(LOG2E)
+    return (dyl[:, j // W, :] + dxl[:, j % W, :]).transpose(2, 0, 1)
+
+
+def packed_exact(be, m, nb, N, Nk, bias=None, causal=False):
     """Exact attention [nb, N, 64] of the packed bf16 operands left on the
-    device, and the scores' per-row maxima / first-block maxima."""
+    device (plus `bias` [nb, N, Nk], exp2 domain, if given), and the
+    scores' per-row maxima / first-block maxima."""
     Np, Npk = pad64(N), pad64(Nk)
     q = bf16_to_f64(be.read(m.m.q16, nb * Np * 64)).reshape(nb, Np, 64)[:, :N]
     k = bf16_to_f64(be.read(m.m.k16, nb * Npk * 64)).reshape(nb, Npk, 64)[:, :Nk]
     v = bf16_to_f64(be.read(m.m.vt16, nb * Npk * 64)).reshape(nb, 64, Npk)[:, :, :Nk]
-    bt = None
-    if bias:
-        bt = be.read(m.m.abias, nb * N * Npk).reshape(nb, N, Npk)[:, :, :Nk]
+    bt = bias
     out = np.empty((nb, N, 64))
     stats = {"max": [], "first": []}
     for u in range(nb):
@@ -197,8 +207,10 @@ def _attend(hip, be, Q, K, V, heads, hd, causal=False, dy=None, dx=None, W=0):
         got = be.read(do).reshape(Nq, D)
         packed = None
         if be.precision == "bf16":
-            packed = packed_exact(be, m, heads, Nq, Nk, bias=dy is not None,
-                                  causal=causal)
+            packed = packed_exact(
+                be, m, heads, Nq, Nk,
+                bias=box_bias_log2(dy, dx, W) if dy is not None else None,
+                causal=causal)
         return got, packed
     finally:
         for x in (dq, dk, dv, do, ddy, ddx):

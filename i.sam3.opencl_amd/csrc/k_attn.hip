@@ -196,43 +196,39 @@ __device__ __forceinline__ bool split_merge(float *__restrict__ part, unsigned *
 #define SAFE_SPAN 64.0f
 
 /* Box relative position bias of softmax_ext (sam3_kernels.cl:885-921)
- * for keys j0 .. j0 + RUN - 1 of one query, j0 = y W + x (x < W): dy[y']
- * + dx[x'] for each key j = y' W + x' from the query's row of the bias
- * rows (H = Nk / W values of dy, then W of dx: launch_box_rows), 0 past
- * Nk (those keys are masked). A run starting at a multiple of RUN inside
- * one row of a grid whose W is a multiple of RUN and H of 4 reads one dy
- * value and RUN / 4 16-byte runs of dx. The caller finds (y, x) from the
- * block's first key without a division per run (block_yx). */
+ * added to registers r0 .. r0 + RUN - 1 of s, the scores of keys j0 ..
+ * j0 + RUN - 1 of one query, j0 = y W + x (x < W, both multiples of RUN;
+ * W a multiple of RUN, so the run lies in one grid row and is either all
+ * below Nk or all past it, where nothing is added: those keys are
+ * masked): dy[y] + dx[x + e] from the query's row of the bias rows (H =
+ * Nk / W values of dy, then W >= 64 of dx, H a multiple of 4:
+ * launch_box_rows),
+ * one dy value and RUN / 4 16-byte runs of dx. The caller finds (y, x)
+ * from the block's first key without a division per run (block_yx).
+ * Other grids take the bias as a table (launch_box_bias). */
 template <int RUN>
-__device__ __forceinline__ void box_run(const float *__restrict__ row, int H, int W, int Nk,
-                                        int j0, int y, int x, float (&out)[RUN])
+__device__ __forceinline__ void box_add(const float *__restrict__ row, int H, int Nk, int j0,
+                                        int y, int x, f32x16 &s, int r0)
 {
-    if (W % RUN == 0 && H % 4 == 0 && j0 + RUN <= Nk) {
-        const float yv = row[y];
-
-        for (int q = 0; q < RUN / 4; q++) {
-            const f32x4 xv = *(const f32x4 *)(row + H + x + 4 * q);
-
-            for (int e = 0; e < 4; e++)
-                out[4 * q + e] = yv + xv[e];
-        }
+    if (j0 >= Nk)
         return;
-    }
-    for (int e = 0; e < RUN; e++) {
-        out[e] = j0 + e < Nk ? row[y] + row[H + x] : 0.0f;
-        if (++x == W) {
-            x = 0;
-            y++;
-        }
+    const float yv = row[y];
+
+    for (int q = 0; q < RUN / 4; q++) {
+        const f32x4 xv = *(const f32x4 *)(row + H + x + 4 * q);
+
+        for (int e = 0; e < 4; e++)
+            s[r0 + 4 * q + e] += yv + xv[e];
     }
 }
 
-/* (y, x) of key jb + off for a block's first key jb = yb W + xb. */
+/* (y, x) of key jb + off for a block's first key jb = yb W + xb, for
+ * off < 64 <= W (one wrap at most). */
 __device__ __forceinline__ void block_yx(int yb, int xb, int W, int off, int &y, int &x)
 {
     y = yb;
     x = xb + off;
-    while (x >= W) {
+    if (x >= W) {
         x -= W;
         y++;
     }
@@ -251,8 +247,9 @@ __device__ __forceinline__ void block_yx(int yb, int xb, int W, int off, int &y,
  *
  * EXT adds softmax_ext's terms (sam3_kernels.cl:885-921) the way it adds
  * them: the causal mask (key j > query i: -inf), or the box bias dy + dx
- * from the bias rows of launch_box_rows (d.bW = W), added to the scaled
- * score as softmax_ext adds it.
+ * from the bias rows of launch_box_rows (d.bW = W), or from an additive
+ * table [unit][N][Nk padded to 64] of the sums (k_box_bias with scale 1,
+ * d.bW = 0), added to the scaled score as softmax_ext adds it.
  *
  * With nsplit > 1 (the SPLIT instance) the workgroup takes key blocks
  * [kb0, kb1) of split sp and the tile's splits merge inside the launch
@@ -299,7 +296,8 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
      * last row, never stored). */
     const int bH = d.bW > 0 ? Nk / d.bW : 0;
     const float *brow = EXT && d.bias
-                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * (bH + d.bW)
+                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) *
+                                           (d.bW > 0 ? bH + d.bW : (Nk + 63) / 64 * 64)
                             : nullptr;
     /* Loader role: key row kr of a block, 8 channels from dc; with HD 32
      * the upper half of the threads loads nothing. */
@@ -403,17 +401,27 @@ __global__ __launch_bounds__(256) void k_attn_f32(attn_desc d, float *__restrict
         float rs = 0.0f, mx = -INFINITY;
 
         if (EXT && brow) {
-            const int yb = kb * 32 / d.bW, xb = kb * 32 - yb * d.bW;
+            for (int r = 0; r < 16; r++)
+                s[r] *= d.scale;
+            if (d.bW > 0) {
+                const int yb = kb * 32 / d.bW, xb = kb * 32 - yb * d.bW;
 
-            for (int g = 0; g < 4; g++) {
-                float bv[4];
-                int y, x;
+                for (int g = 0; g < 4; g++) {
+                    int y, x;
 
-                block_yx(yb, xb, d.bW, 8 * g + 4 * h, y, x);
-                box_run<4>(brow, bH, d.bW, Nk, kb * 32 + 8 * g + 4 * h, y, x, bv);
-                for (int e = 0; e < 4; e++)
-                    s[4 * g + e] = fmaf(s[4 * g + e] * d.scale + bv[e], LOG2E_F, -m_run);
+                    block_yx(yb, xb, d.bW, 8 * g + 4 * h, y, x);
+                    box_add<4>(brow, bH, Nk, kb * 32 + 8 * g + 4 * h, y, x, s, 4 * g);
+                }
             }
+            else
+                for (int g = 0; g < 4; g++) {
+                    const f32x4 bv = *(const f32x4 *)(brow + kb * 32 + 8 * g + 4 * h);
+
+                    for (int e = 0; e < 4; e++)
+                        s[4 * g + e] += bv[e];
+                }
+            for (int r = 0; r < 16; r++)
+                s[r] = fmaf(s[r], LOG2E_F, -m_run);
         }
         else
             for (int r = 0; r < 16; r++)
@@ -693,7 +701,7 @@ extern "C" int launch_qkv_pack(const attn_desc *d, void *q16, void *k16,
  * bias of softmax_ext (sam3_kernels.cl:904-906): out[h][i] = unit_scale
  * dy[(i H + y) nh + h] for y < H, then unit_scale dx[(i W + x) nh + h] for
  * x < W (H = Nk / W), one row of H + W floats per (head, query); the
- * kernels add dy[j / W] + dx[j % W] to the score of key j (box_run)
+ * kernels add dy[j / W] + dx[j % W] to the score of key j (box_add)
  * instead of reading an [Nq][Nk] table per head. unit_scale 1 for the
  * exact path (the sum dy + dx softmax_ext makes), log2(e) for the bf16
  * kernel's exp2 domain. One thread per element. */
@@ -728,6 +736,61 @@ extern "C" int launch_box_rows(float *out, const float *dy, const float *dx, int
         return hipErrorInvalidConfiguration;
     hipLaunchKernelGGL(k_box_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, out, dy, dx, Nq, Nk / W, W, nh, n, unit_scale);
+    return hipGetLastError();
+}
+
+/* Additive bias table of the fused attention kernels,
+ * out[unit][i][j] = unit_scale (dy[(i H + j / W) nh + h] + dx[(i W + j % W)
+ * nh + h]) for keys j < Nk and -inf for the padding up to Npk (unit = head
+ * h, H = Nk / W): the box relative position bias of softmax_ext
+ * (sam3_kernels.cl:904-906) for every (head, query, key), with unit_scale
+ * log2(e) for the bf16 kernel's exp2 domain and 1 for the exact path (the
+ * sum dy + dx then has softmax_ext's own rounding). */
+__global__ __launch_bounds__(256) void k_box_bias(float *__restrict__ out,
+                                                  const float *__restrict__ dy,
+                                                  const float *__restrict__ dx,
+                                                  int heads, int Nq, int Nk, int Npk,
+                                                  int W, int nh, float unit_scale)
+{
+    /* Workgroup: one (head, query) row; its H dy and W dx values go to
+     * LDS once, then the row is written as 16-byte runs of four keys. */
+    extern __shared__ float sxy[];
+    const int r = blockIdx.x, h = r / Nq, i = r - h * Nq, H = Nk / W;
+    float *sy = sxy, *sx = sxy + H;
+    float *orow = out + (long)r * Npk;
+
+    for (int t = threadIdx.x; t < H; t += 256)
+        sy[t] = dy[((long)i * H + t) * nh + h];
+    for (int t = threadIdx.x; t < W; t += 256)
+        sx[t] = dx[((long)i * W + t) * nh + h];
+    __syncthreads();
+    for (int j0 = 4 * threadIdx.x; j0 < Npk; j0 += 1024) {
+        f32x4 v;
+
+        for (int k = 0; k < 4; k++) {
+            const unsigned j = j0 + k, y = j / (unsigned)W;
+
+            v[k] = j < (unsigned)Nk ? (sy[y] + sx[j - y * W]) * unit_scale : -INFINITY;
+        }
+        *(f32x4 *)(orow + j0) = v;
+    }
+}
+
+extern "C" int launch_box_bias(float *out, const float *dy, const float *dx,
+                               int heads, int Nq, int Nk, int W, int nh,
+                               float unit_scale, void *stream)
+{
+    const int Npk = (Nk + 63) / 64 * 64;
+    const long rows = (long)heads * Nq;
+    const size_t lds = ((size_t)Nk / W + W) * sizeof(float);
+
+    if (rows == 0)
+        return hipSuccess;
+    if (rows > 0x7fffffffL || W < 1 || lds > 65536)
+        return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(k_box_bias, dim3((unsigned)rows), dim3(256), lds,
+                       (hipStream_t)stream, out, dy, dx, heads, Nq, Nk, Npk, W, nh,
+                       unit_scale);
     return hipGetLastError();
 }
 
@@ -918,7 +981,8 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
      * Nk), if any; queries past N read the last row (never stored). */
     const int bH = d.bW > 0 ? Nk / d.bW : 0;
     const float *brow = EXT && d.bias
-                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) * (bH + d.bW)
+                            ? d.bias + ((long)unit * N + (qi < N ? qi : N - 1)) *
+                                           (d.bW > 0 ? bH + d.bW : Npk)
                             : nullptr;
     bf16x8 qb[4];
     SoftState st;
@@ -1089,19 +1153,35 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
              * such block takes the exact max below). Registers 8a .. 8a + 7
              * of s0 are keys 16 a + 8 h .. +7 of the block, s1's 32
              * further. */
-            const int yb = kb * 64 / d.bW, xb = kb * 64 - yb * d.bW;
+            /* Rows at head width 32 only: at 64 the instance has no
+             * registers to spare for them (they spilled 20 VGPRs). */
+            if (H32 && d.bW > 0) {
+                const int yb = kb * 64 / d.bW, xb = kb * 64 - yb * d.bW;
 
-            for (int a = 0; a < 2; a++) {
-                float b0[8], b1[8];
-                int y, x;
+                for (int a = 0; a < 2; a++) {
+                    int y, x;
 
-                block_yx(yb, xb, d.bW, 16 * a + 8 * h, y, x);
-                box_run<8>(brow, bH, d.bW, Nk, kb * 64 + 16 * a + 8 * h, y, x, b0);
-                block_yx(yb, xb, d.bW, 32 + 16 * a + 8 * h, y, x);
-                box_run<8>(brow, bH, d.bW, Nk, kb * 64 + 32 + 16 * a + 8 * h, y, x, b1);
-                for (int e = 0; e < 8; e++) {
-                    s0[8 * a + e] += b0[e];
-                    s1[8 * a + e] += b1[e];
+                    block_yx(yb, xb, d.bW, 16 * a + 8 * h, y, x);
+                    box_add<8>(brow, bH, Nk, kb * 64 + 16 * a + 8 * h, y, x, s0, 8 * a);
+                    block_yx(yb, xb, d.bW, 32 + 16 * a + 8 * h, y, x);
+                    box_add<8>(brow, bH, Nk, kb * 64 + 32 + 16 * a + 8 * h, y, x, s1, 8 * a);
+                }
+            }
+            else {
+                const float *bk = brow + kb * 64 + 8 * h;
+
+                for (int a = 0; a < 2; a++) {
+                    const f32x4 b0 = *(const f32x4 *)(bk + 16 * a);
+                    const f32x4 b1 = *(const f32x4 *)(bk + 16 * a + 4);
+                    const f32x4 b2 = *(const f32x4 *)(bk + 32 + 16 * a);
+                    const f32x4 b3 = *(const f32x4 *)(bk + 32 + 16 * a + 4);
+
+                    for (int e = 0; e < 4; e++) {
+                        s0[8 * a + e] += b0[e];
+                        s0[8 * a + 4 + e] += b1[e];
+                        s1[8 * a + e] += b2[e];
+                        s1[8 * a + 4 + e] += b3[e];
+                    }
                 }
             }
         }

@@ -131,9 +131,11 @@ struct attn_desc {
     int hd;
     /* Keys per unit (N queries, Nk keys; K and V rows count Nk); beyond
      * Nk == N: the box bias as rows [unit][N][H + W] of dy then dx values
-     * (launch_box_rows, H = Nk / bW), each key j biased by dy[j / bW] +
-     * dx[j % bW] (the bf16 kernel's rows scaled to its exp2 domain), or
-     * NULL; and the
+     * (launch_box_rows, H = Nk / bW; bW >= 64 a multiple of 8, H of 4;
+     * on the bf16 path at head width 32 only), each key
+     * j biased by dy[j / bW] + dx[j % bW], or with bW = 0 as a table
+     * [unit][N][Nk padded to 64] (launch_box_bias), on the bf16 path
+     * scaled to its exp2 domain; or NULL; and the
      * causal mask (key j > query i excluded). */
     int Nk;
     const float *bias;
@@ -189,6 +191,14 @@ int launch_attn_bf16_grp(const struct attn_desc *d, const void *q16, const void 
                          const void *vt16, const float *knorm, int ng, void *stream);
 /* Zero the n counters of launch_attn_bf16's balanced launch. */
 int launch_attn_sk_zero(unsigned *cnt, long n, void *stream);
+
+/* Additive bias table of the fused attention from the box relative
+ * position bias of softmax_ext, for grids the bias rows do not take:
+ * out [heads][Nq][Nk padded to 64] = unit_scale (dy[(i H + j / W) nh + h]
+ * + dx[(i W + j % W) nh + h]), -inf in the padding (H = Nk / W);
+ * unit_scale log2(e) for the bf16 kernel, 1 for the exact path. */
+int launch_box_bias(float *out, const float *dy, const float *dx, int heads,
+                    int Nq, int Nk, int W, int nh, float unit_scale, void *stream);
 
 /* Bias rows of the fused attention from the box relative position bias
  * of softmax_ext: out [heads][Nq][H + W] = unit_scale dy[(i H + y) nh + h]

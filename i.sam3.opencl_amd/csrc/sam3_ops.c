@@ -668,13 +668,19 @@ static void attn_fused_hd(struct sam_model *m, const char *who, int hd, int N,
     d.causal = causal != 0;
     d.bias = bias ? (const float *)bias->ptr : NULL;
     d.bW = bias ? bW : 0;
-    if (bias && (bW < 1 || Nk % bW ||
-                 !buf_ok(who, "bias rows", bias, (size_t)nb * N * ((size_t)Nk / bW + bW),
-                         HIPB_F32))) {
+    if (bias && bW > 0 &&
+        (bW < 64 || bW % 8 || Nk % bW || (Nk / bW) % 4 || (b->bf16 && hd != 32) ||
+         !buf_ok(who, "bias rows", bias, (size_t)nb * N * ((size_t)Nk / bW + bW),
+                 HIPB_F32))) {
         if (!hipb_failed())
-            hipb_fatal("%s: bias rows need W dividing Nk", who);
+            hipb_fatal("%s: bias rows need W >= 64, a multiple of 8 dividing Nk "
+                       "into a multiple of 4 rows (bf16: head width 32)", who);
         return;
     }
+    if (bias && bW == 0 &&
+        !buf_ok(who, "bias table", bias,
+                (size_t)nb * N * (((size_t)Nk + 63) / 64 * 64), HIPB_F32))
+        return;
     if (b->bf16) {
         const size_t np = ((size_t)N + 63) / 64 * 64;
         const size_t npk = ((size_t)Nk + 63) / 64 * 64;
@@ -847,27 +853,38 @@ void attend(struct sam_model *m, int Nq, int Nk, int heads, int hd, hipb_mem Q,
     /* Fused for head width 64 or 32 with any mask or bias, on both paths.
      * The box bias goes to the kernels as rows of each (head, query)'s dy
      * and dx values, H + W floats, which they add as dy[j / W] + dx[j % W]
-     * per key (on the bf16 path both scaled to its exp2 domain first).
-     * Heads are the units, head h at column h hd of every operand. */
+     * per key, when W >= 64 is a multiple of 8 and H of 4 (the decoder's
+     * 72 x 72 grid) on the exact path or at head width 32 on bf16; else as
+     * a table [head][Nq][Nk padded to 64] of the sums. On the bf16 path
+     * both are scaled to its exp2 domain. Heads are the units, head h at
+     * column h hd of every operand. */
     if (hd == 64 || hd == 32) {
+        const int rows = dy && W >= 64 && W % 8 == 0 && (Nk / W) % 4 == 0 &&
+                         (!b->bf16 || hd == 32);
+
         if (dy) {
+            const float us = b->bf16 ? LOG2E_HOST : 1.0f;
+            const size_t n = rows ? (size_t)heads * Nq * ((size_t)Nk / W + W)
+                                  : (size_t)heads * Nq * (((size_t)Nk + 63) / 64 * 64);
             int err;
 
-            if (!ensure_typed(b, &m->abias, (size_t)heads * Nq * ((size_t)Nk / W + W),
-                              HIPB_F32, "attention bias rows"))
+            if (!ensure_typed(b, &m->abias, n, HIPB_F32, "attention bias"))
                 return;
             hipb_run_begin(b);
-            err = launch_box_rows((float *)m->abias->ptr, (const float *)dy->ptr,
-                                  (const float *)dx->ptr, heads, Nq, Nk, W, heads,
-                                  b->bf16 ? LOG2E_HOST : 1.0f, b->stream);
-            hipb_run_end(b, err, "box_rows", 0.0);
+            err = rows ? launch_box_rows((float *)m->abias->ptr, (const float *)dy->ptr,
+                                         (const float *)dx->ptr, heads, Nq, Nk, W, heads, us,
+                                         b->stream)
+                       : launch_box_bias((float *)m->abias->ptr, (const float *)dy->ptr,
+                                         (const float *)dx->ptr, heads, Nq, Nk, W, heads, us,
+                                         b->stream);
+            hipb_run_end(b, err, rows ? "box_rows" : "box_bias", 0.0);
             if (hipb_failed())
                 return;
         }
         attn_fused_hd(m, "attend", hd, Nq, Nk, heads, heads,
                       bmat(Q, 0, ldq, 0, hd), bmat(K, 0, ldk, 0, hd),
                       bmat(V, 0, ldv, 0, hd), bmat(O, 0, ldo, 0, hd), NULL, 1,
-                      scale, causal, dy ? m->abias : NULL, W);
+                      scale, causal, dy ? m->abias : NULL, rows ? W : 0);
         return;
     }
     /* The reference's sequence (sam3_text.c:305-343): per chunk of heads

@@ -89,14 +89,19 @@ def bf16_to_f64(u16):
     return (u16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def box_bias_log2(dy, dx, W):
+def box_bias_log2(dy, dx, W, rows):
     """The box bias [heads, Nq, Nk] the bf16 kernel adds in its exp2
-    domain: dy[j / W] log2(e) + dx[j % W] log2(e), rounded in float32 as
-    the device rounds it."""
+    domain, rounded in float32 as the device rounds it: from bias rows
+    (head width 32, W >= 64 a multiple of 8) dy[j / W] log2(e) +
+    dx[j % W] log2(e), from a table (dy[j / W] + dx[j % W]) log2(e)."""
     H = dy.shape[1]
     j = np.arange(H * W)
-    dyl, dxl = dy * np.float32(LOG2E), dx * np.float32(LOG2E)
-    return (dyl[:, j // W, :] + dxl[:, j % W, :]).transpose(2, 0, 1)
+    L = np.float32(LOG2E)
+    if rows:
+        b = (dy * L)[:, j // W, :] + (dx * L)[:, j % W, :]
+    else:
+        b = (dy[:, j // W, :] + dx[:, j % W, :]) * L
+    return b.transpose(2, 0, 1)
 
 
 def packed_exact(be, m, nb, N, Nk, bias=None, causal=False):
@@ -209,7 +214,7 @@ def _attend(hip, be, Q, K, V, heads, hd, causal=False, dy=None, dx=None, W=0):
         if be.precision == "bf16":
             packed = packed_exact(
                 be, m, heads, Nq, Nk,
-                bias=box_bias_log2(dy, dx, W) if dy is not None else None,
+                bias=box_bias_log2(dy, dx, W, hd == 32) if dy is not None else None,
                 causal=causal)
         return got, packed
     finally:

@@ -218,8 +218,9 @@ struct sam_model {
      * hipGraphExec_t, and the work-buffer generation it was captured at. */
     void *trunk_graph, *trunk_exec;
     unsigned long trunk_gen;
-    /* attend(): the box bias as the bf16 kernel's additive table
-     * [heads][Nq][Nk padded to 64] (exp2 domain). */
+    /* attend(): the box bias of the fused kernels, as rows [heads][Nq][H
+     * + W] of dy then dx values or as an additive table [heads][Nq][Nk
+     * padded to 64] (exp2 domain on the bf16 path). */
     hipb_mem abias;
     /* Key-split partial records of the bf16 attention ([unit][split][Np]
      * rows of 64 O values, then their (m, l) pairs). */

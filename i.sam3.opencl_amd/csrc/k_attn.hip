@@ -1391,6 +1391,13 @@ __device__ __forceinline__ void attn_tile(const Desc &d, const uint16_t *__restr
          * and the reads (one row, 8 chunks) free of bank conflicts. */
         const int fs = (kb1 - kb0) & 1;
         char *stg = w < 2 ? (char *)&Ks[fs][32 * w][0] : (char *)&Vt[fs][32 * (w - 2)][0];
+        /* The lane index again, opaque to the compiler: the staging
+         * offsets below are then formed here rather than kept from the
+         * prologue across the key loop (which spilled them). */
+        int l = threadIdx.x & 63;
+
+        asm volatile("" : "+v"(l));
+        const int l32 = l & 31, h = l >> 5;
         const int q0 = qi - l32, c = l & 7;
         /* All 32 rows of the wave inside N (every wave but those of a
          * ragged tail tile): the stores need no per-row test. */

@@ -78,12 +78,13 @@ __global__ __launch_bounds__(256) void k_layernorm(
     }
     var = block_sum256(s, red) / (float)C;
     rs = 1.0f / sqrtf(var + eps);
-    for (c = t; c < C; c += 256) {
-        const float xv = c < 2048 ? v[c >> 8] : xr[c];
-        const float y = fmaf((xv - mean) * rs, g[c], bt[c]);
-
-        Y[r * C + c] = (TY)act_k(y, act);
+    for (i = 0; i < 8; i++) {
+        c = t + 256 * i;
+        if (c < C)
+            Y[r * C + c] = (TY)act_k(fmaf((v[i] - mean) * rs, g[c], bt[c]), act);
     }
+    for (c = t + 2048; c < C; c += 256)
+        Y[r * C + c] = (TY)act_k(fmaf((xr[c] - mean) * rs, g[c], bt[c]), act);
 }
 
 /* Sum over a wave64, the same bits in every lane: DPP adds inside each
@@ -116,11 +117,11 @@ __device__ __forceinline__ float wave_sum_rows(float v)
  * them for C <= 2048 (not after the sums, where they would add an L2 trip
  * to every wave's path); the mean and variance close with wave_sum_rows
  * (no LDS, no barrier); outputs leave as 16-byte (float) or 8-byte (bf16)
- * stores.
- * Window partition as in k_layernorm, in 32-bit arithmetic (the launcher
- * keeps the rows below 2^32). At 5184 x 1024 (bf16 out) after a kernel
- * that wrote X: 7.9 -> 6.6 us against the shuffle sums with late gamma /
- * beta loads and 64-bit partition divisions. */
+ * stores. Window partition as in k_layernorm, in 32-bit arithmetic (the
+ * launcher keeps the rows below 2^32). At 5184 x 1024 (bf16 out) after a
+ * kernel that wrote X: 7.9 -> 6.6 us against the shuffle sums with late
+ * gamma / beta loads and 64-bit partition divisions. Every loop over the
+ * row is unrolled (left rolled at C >= 3072, the row went to scratch). */
 template <typename TY, int V>
 __global__ __launch_bounds__(256) void k_layernorm_w(
     const float *__restrict__ X, TY *__restrict__ Y, const float *__restrict__ g,
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(256) void k_layernorm_w(
         const unsigned y = wy * ws + py, x = (w - wy * nwx) * ws + (p - py * ws);
 
         if (y >= (unsigned)H || x >= (unsigned)H) {
+#pragma unroll
             for (int i = 0; i < V; i++)
                 for (int e = 0; e < 4; e++)
                     yr[256 * i + e] = (TY)0.0f;
@@ -154,22 +156,27 @@ __global__ __launch_bounds__(256) void k_layernorm_w(
         src = y * (unsigned)H + x;
     }
     const float *xr = X + (long)src * C + 4 * l;
+#pragma unroll
     for (int i = 0; i < V; i++)
         v[i] = *(const f32x4 *)(xr + 256 * i);
     if constexpr (EARLY) {
+#pragma unroll
         for (int i = 0; i < V; i++) {
             gv[i] = *(const f32x4 *)(g + 4 * l + 256 * i);
             bv[i] = *(const f32x4 *)(bt + 4 * l + 256 * i);
         }
         /* Keeps all loads issued here (the compiler otherwise sinks gamma
          * and beta below the sums). */
+#pragma unroll
         for (int i = 0; i < V; i++)
             asm volatile("" : "+v"(v[i]), "+v"(gv[i]), "+v"(bv[i]));
     }
+#pragma unroll
     for (int i = 0; i < V; i++)
         s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     mean = wave_sum_rows(s) / (float)C;
     s = 0.0f;
+#pragma unroll
     for (int i = 0; i < V; i++) {
         const f32x4 dv = v[i] - mean;
 
@@ -177,6 +184,7 @@ __global__ __launch_bounds__(256) void k_layernorm_w(
     }
     var = wave_sum_rows(s) / (float)C;
     rs = 1.0f / sqrtf(var + eps);
+#pragma unroll
     for (int i = 0; i < V; i++) {
         f32x4 o;
 

@@ -41,7 +41,7 @@ def rng(seed):
     return np.random.default_rng(seed)
 
 
-@pytest.mark.parametrize("C", [1024, 256, 100, 3000, 64, 32, 128])
+@pytest.mark.parametrize("C", [1024, 256, 100, 3000, 3072, 4096, 4608, 64, 32, 128])
 def test_layernorm(hip, be, orc, C):
     m = model(hip, be)
     g = rng(C)

@@ -196,3 +196,29 @@ def test_sixty_four_key_splits(hip, be, orc):
     want = orc.attend(Q, K, V, heads, hd)
     assert report("64 key splits %s" % be.precision, got, want) <= TOL[be.precision]
     assert np.array_equal(_run(hip, be, Q, K, V, heads, hd), got)
+
+
+@pytest.mark.parametrize("Nq,H,W,hd", [
+    (37, 8, 64, 32),    # bias rows (W >= 64 a multiple of 8, H a multiple of 4)
+    (37, 8, 64, 64),    # rows on the exact path, the table on bf16 (head width 64)
+    (37, 6, 64, 32),    # H not a multiple of 4: the table
+    (130, 4, 72, 32),   # rows, two query tiles, a ragged last key block
+    (21, 5, 80, 32),    # H = 5: the table
+])
+def test_box_bias_grids(hip, be, orc, Nq, H, W, hd):
+    """The box bias of softmax_ext (sam3_kernels.cl:904-906) on grids that
+    take the per-query dy / dx rows or the bias table, against the
+    oracle's reference sequence."""
+    heads = 4
+    Nk = H * W
+    g = np.random.default_rng(Nq * H + W + hd)
+    Q = g.standard_normal((Nq, heads * hd)).astype(np.float32)
+    K, V = (g.standard_normal((Nk, heads * hd)).astype(np.float32) for _ in range(2))
+    dy = (2 * g.standard_normal((Nq, H, heads))).astype(np.float32)
+    dx = (2 * g.standard_normal((Nq, W, heads))).astype(np.float32)
+    print("attend box grid Nq=%d H=%d W=%d hd=%d %s" % (Nq, H, W, hd, be.precision),
+          flush=True)
+    got = _run(hip, be, Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    want = orc.attend(Q, K, V, heads, hd, dy=dy, dx=dx, W=W)
+    assert report("box grid H=%d W=%d hd=%d %s" % (H, W, hd, be.precision), got,
+                  want) <= TOL[be.precision]

@@ -202,10 +202,9 @@ __device__ __forceinline__ bool split_merge(float *__restrict__ part, unsigned *
  * below Nk or all past it, where nothing is added: those keys are
  * masked): dy[y] + dx[x + e] from the query's row of the bias rows (H =
  * Nk / W values of dy, then W >= 64 of dx, H a multiple of 4:
- * launch_box_rows),
- * one dy value and RUN / 4 16-byte runs of dx. The caller finds (y, x)
- * from the block's first key without a division per run (block_yx).
- * Other grids take the bias as a table (launch_box_bias). */
+ * launch_box_rows), one dy value and RUN / 4 16-byte runs of dx. The
+ * caller finds (y, x) from the block's first key without a division per
+ * run (block_yx). Other grids take the bias as a table (launch_box_bias). */
 template <int RUN>
 __device__ __forceinline__ void box_add(const float *__restrict__ row, int H, int Nk, int j0,
                                         int y, int x, f32x16 &s, int r0)

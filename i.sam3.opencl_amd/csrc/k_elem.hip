@@ -468,6 +468,52 @@ __global__ __launch_bounds__(256) void k_patch_im2col(
         ((float *)out)[gid] = v;
 }
 
+/* The same columns as bf16 for an even patch side, one workgroup per
+ * (row of patches ty, channel c): the patch row's ps image rows of the
+ * channel go to LDS with 16-byte loads (whole rows, coalesced), then
+ * each token's ps * ps columns of that channel leave as a contiguous run
+ * of bf16 pairs; the channel-2 workgroup also writes the tokens' zero
+ * columns K .. ldo - 1. 1024 threads. The launcher checks the shapes
+ * (side a multiple of 4, ps * side floats within 64 KiB of LDS, 32-bit
+ * indices). */
+__global__ __launch_bounds__(1024) void k_patch_im2col_bf16(const float *__restrict__ img,
+                                                            uint32_t *__restrict__ out,
+                                                            int side, int grid, int ps, int ldo)
+{
+    extern __shared__ __attribute__((aligned(16))) float rows[];
+    const int ty = blockIdx.x, c = blockIdx.y, K = 3 * ps * ps, pp = ps * ps;
+    const f32x4 *src = (const f32x4 *)(img + ((size_t)c * side + (size_t)ty * ps) * side);
+    const int n4 = ps * side / 4;
+    f32x4 v[4];
+
+    /* At most four 16-byte loads per thread (64 KiB), all issued before
+     * the first is stored: one trip to memory instead of one per load. */
+    for (int k = 0; k < 4; k++)
+        if (threadIdx.x + 1024 * k < n4)
+            v[k] = src[threadIdx.x + 1024 * k];
+    for (int k = 0; k < 4; k++)
+        if (threadIdx.x + 1024 * k < n4)
+            ((f32x4 *)rows)[threadIdx.x + 1024 * k] = v[k];
+    __syncthreads();
+    const int half = pp / 2, work = grid * half;
+
+    for (int i = threadIdx.x; i < work; i += 1024) {
+        const int tx = i / half, j = 2 * (i - tx * half), ky = j / ps, kx = j - ky * ps;
+        const float *r = rows + ky * side + tx * ps + kx;
+
+        out[((size_t)(ty * grid + tx) * ldo + c * pp + j) / 2] = pack_bf16x2(r[0], r[1]);
+    }
+    if (c == 2) {
+        const int zh = (ldo - K) / 2;
+
+        for (int i = threadIdx.x; i < grid * zh; i += 1024) {
+            const int tx = i / zh, j = i - tx * zh;
+
+            out[((size_t)(ty * grid + tx) * ldo + K) / 2 + j] = 0u;
+        }
+    }
+}
+
 extern "C" int launch_patch_im2col(const float *img, void *out, int ydt,
                                    int side, int grid, int ps, int ldo,
                                    void *stream)
@@ -476,6 +522,14 @@ extern "C" int launch_patch_im2col(const float *img, void *out, int ydt,
 
     if (ldo < 3 * ps * ps)
         return hipErrorInvalidValue;
+    if (ydt == DT_BF16 && ps % 2 == 0 && ldo % 2 == 0 && side % 4 == 0 &&
+        grid * ps <= side && (size_t)ps * side * sizeof(float) <= 65536 &&
+        total < 0x7fffffffL) {
+        hipLaunchKernelGGL(k_patch_im2col_bf16, dim3((unsigned)grid, 3), dim3(1024),
+                           (size_t)ps * side * sizeof(float), (hipStream_t)stream, img,
+                           (uint32_t *)out, side, grid, ps, ldo);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(k_patch_im2col, dim3((total + 255) / 256), dim3(256),
                        0, (hipStream_t)stream, img, out, ydt, total, side,
                        grid, ps, ldo);
